@@ -1,0 +1,184 @@
+/*
+ * smallinf_hip.h -- C ABI of the MI355X (gfx950) paged-attention decode path.
+ *
+ * One shared library, libsmallinf_hip.so, built with hipcc for gfx950. Every pointer argument is a device
+ * pointer owned by the caller; the library allocates nothing on the device, keeps no pointer after a call
+ * returns and launches asynchronously on the caller's stream (a hipStream_t passed as void*, NULL for the
+ * default stream). No call synchronizes the host.
+ *
+ * Return codes: SIPA_OK (0) or a negative SIPA_E* code; sipa_last_error() then holds a message for the calling
+ * thread. Shape, stride and dtype checks happen on the host before any launch, so a failed call launched nothing.
+ *
+ * Element strides are in elements of the tensor they describe, not bytes. Layouts follow the reference:
+ *   KV pool, one layer: [H_kv, N, B, D] (head, block, offset in block, channel), each block row contiguous.
+ *   A token's slot is block_table[p / B] * B + p % B; it addresses [:, block, offset] of every layer.
+ */
+#ifndef SMALLINF_HIP_H
+#define SMALLINF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIPA_ABI_VERSION 1
+
+/* element types */
+enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
+
+/* return codes */
+enum {
+  SIPA_OK = 0,
+  SIPA_EINVAL = -1,       /* bad shape, stride, pointer or argument combination */
+  SIPA_EUNSUPPORTED = -2, /* valid request outside the built support matrix */
+  SIPA_EHIP = -3,         /* a HIP runtime call failed (launch, device query) */
+  SIPA_EWORKSPACE = -4    /* workspace missing or smaller than sipa_decode_workspace_bytes() */
+};
+
+/* kv_mode of sipa_decode_params */
+enum {
+  SIPA_KV_PLAIN = 0,      /* K/V pools in q_dtype */
+  SIPA_KV_INT8_TOKEN = 1, /* int8 K and V, one scale per (head, block, offset) each */
+  SIPA_KV_INT8_KCHAN = 2  /* int8 K with one scale per (head, block, channel) and each sequence's partial last
+                             block of K in a bf16 staging slot; int8 V with one scale per token */
+};
+
+/* impl of sipa_decode_params */
+enum { SIPA_IMPL_AUTO = 0, SIPA_IMPL_VALU = 1, SIPA_IMPL_MFMA = 2 };
+
+/* combine of sipa_decode_params */
+enum { SIPA_COMBINE_FUSED = 0, SIPA_COMBINE_KERNEL = 1 };
+
+/*
+ * Paged decode attention: one query token per sequence over its paged context.
+ *   out[s, h*G + g, :] = sum_{t < ctx[s]} softmax_t(scale * q[s, h*G+g, :] . k_t) v_t,   G = Hq / Hkv,
+ *   k_t, v_t = pool[h, block_tables[s, t / B], t % B, :].
+ * Replaces paged_decode_attention / _decode_kernel / _combine_kernel (reference engine/triton_decode.py:51-161,
+ * 188-238).
+ */
+typedef struct sipa_decode_params {
+  int32_t struct_size;   /* sizeof(sipa_decode_params): guards against a stale binding */
+  int32_t num_seqs;      /* S */
+  int32_t num_q_heads;   /* Hq */
+  int32_t num_kv_heads;  /* Hkv; Hq % Hkv == 0 */
+  int32_t head_dim;      /* D */
+  int32_t block_size;    /* B; 64 % B == 0 (reference engine/triton_decode.py:211) */
+  int32_t num_blocks;    /* N, blocks in the pool */
+  int32_t max_context;   /* max(context_lens), known on the host; sizes the split grid */
+  int32_t num_splits;    /* <= 0: choose from the device's CU count (sipa_choose_splits) */
+  int32_t q_dtype;       /* SIPA_F32 or SIPA_BF16: q, out, and the pool when kv_mode == SIPA_KV_PLAIN */
+  int32_t kv_mode;       /* SIPA_KV_* */
+  int32_t impl;          /* SIPA_IMPL_* */
+  int32_t combine;       /* SIPA_COMBINE_* */
+  float scale;           /* softmax scale, head_dim^-0.5 in the model */
+  const void* q;         /* [S, Hq, D]; last dim contiguous */
+  int64_t q_stride_s, q_stride_h;
+  const void* k_cache;   /* [Hkv, N, B, D] */
+  const void* v_cache;   /* [Hkv, N, B, D] */
+  int64_t kv_stride_h, kv_stride_n; /* block rows are contiguous: offset stride D, channel stride 1 */
+  const int32_t* block_tables; /* [S, >= ceil(max_context / B)], padding never read */
+  int64_t bt_stride_s;
+  const int32_t* context_lens; /* [S], each >= 1, the new token included */
+  void* out;             /* [S, Hq, D] in q_dtype */
+  int64_t out_stride_s, out_stride_h;
+  /* SIPA_KV_INT8_TOKEN: k_scale, v_scale [Hkv, N, B].  SIPA_KV_INT8_KCHAN: k_scale [Hkv, N, D] (a zero block
+     stride gives one scale per (head, channel) for the whole pool), v_scale [Hkv, N, B]. SIPA_F16 or SIPA_F32. */
+  const void* k_scale;
+  int32_t k_scale_dtype;
+  int64_t ks_stride_h, ks_stride_n;
+  const void* v_scale;
+  int32_t v_scale_dtype;
+  int64_t vs_stride_h, vs_stride_n;
+  /* SIPA_KV_INT8_KCHAN only: bf16 staging [Hkv, n_stage, B, D] and the staging slot of each sequence's partial
+     last block (-1 when ctx % B == 0). */
+  const void* stage;
+  int64_t st_stride_h, st_stride_n, st_stride_b;
+  const int32_t* tail_slots;
+  /* Split partials and merge counters; at least sipa_decode_workspace_bytes() bytes, 256-byte aligned. The
+     counter words must be zero before the first call that uses the buffer; every completed call leaves them
+     zero again. Calls that share one workspace must be ordered (one stream). May be NULL when 1 split runs. */
+  void* workspace;
+  int64_t workspace_bytes;
+} sipa_decode_params;
+
+int32_t sipa_abi_version(void);
+const char* sipa_last_error(void);
+
+/* Compute units of a device (256 on MI355X); < 0 on error. */
+int32_t sipa_device_cu_count(int32_t device);
+
+/*
+ * Splits per sequence for a call. Replaces the reference's 20-SM policy choose_splits (reference
+ * engine/triton_decode.py:164-172) with one sized from the CU count: enough (sequence, KV head, split)
+ * workgroups to fill every CU several times, each split at most SIPA_MAX_CHUNK tokens so that a long
+ * sequence in a ragged batch is spread over many CUs.
+ */
+int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count);
+
+/* Tokens per split for a call with num_splits splits (a multiple of the 32-token tile). */
+int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits);
+
+/* Workspace bytes sipa_decode needs for these sizes (0 when num_splits resolves to 1). */
+int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t num_splits);
+
+int32_t sipa_decode(const sipa_decode_params* p, void* stream);
+
+/*
+ * Per-token INT8 quantize-and-store (reference engine/triton_quant.py:24-39,61-71 and the quantizer
+ * engine/quant.py:22-31): for every (t, h),
+ *   s = fp16(max_d |x[t,h,d]| / 127);  q[d] = s > 0 ? clamp(rint(x[t,h,d] / float(s)), -127, 127) : 0
+ * with IEEE fp32 division and round-half-even, stored to q_pool[h, blocks[t], offsets[t], :] (int8) and
+ * s_pool[h, blocks[t], offsets[t]] (fp16).
+ *   x [T, H, D] in x_dtype (SIPA_F32 / SIPA_BF16 / SIPA_F16), last dim contiguous;
+ *   blocks, offsets [T] int64; q_pool [H, N, B, D] int8 (offset stride D); s_pool [H, N, B] fp16.
+ */
+int32_t sipa_quantize_store_tokens(const void* x, int32_t x_dtype, int64_t x_stride_t, int64_t x_stride_h,
+                                   int32_t T, int32_t H, int32_t D, const int64_t* blocks,
+                                   const int64_t* offsets, int8_t* q_pool, int64_t q_stride_h,
+                                   int64_t q_stride_n, int32_t B, void* s_pool, int64_t s_stride_h,
+                                   int64_t s_stride_n, void* stream);
+
+/*
+ * Per-channel INT8 quantize-and-store of whole blocks (reference engine/triton_quant.py:42-58,74-84): for every
+ * (i, h) the [B, D] tile src_pool[h, src[i]] gets one scale per channel over its B tokens,
+ *   s[d] = fp16(max_b |x[b,d]| / 127), codes as above, stored to q_pool[h, dst[i]] and s_pool[h, dst[i], :].
+ *   src_pool [H, n_src, B, D] in src_dtype (bf16 staging in the cache); src, dst [n] int64;
+ *   q_pool [H, N, B, D] int8; s_pool [H, N, D] fp16.
+ */
+int32_t sipa_quantize_store_blocks(const void* src_pool, int32_t src_dtype, int64_t src_stride_h,
+                                   int64_t src_stride_n, int64_t src_stride_b, const int64_t* src,
+                                   const int64_t* dst, int32_t n, int32_t H, int32_t B, int32_t D,
+                                   int8_t* q_pool, int64_t q_stride_h, int64_t q_stride_n, void* s_pool,
+                                   int64_t s_stride_h, int64_t s_stride_n, void* stream);
+
+/*
+ * The same per-channel block quantization with the block's B tokens taken from rows of x [T, H, D]:
+ * block i holds rows[i*B + b], b < B. Each value is rounded to bf16 first, as the reference's cache does for
+ * blocks one forward writes whole (reference engine/quant_cache.py:147-153,171-177).
+ */
+int32_t sipa_quantize_store_block_rows(const void* x, int32_t x_dtype, int64_t x_stride_t, int64_t x_stride_h,
+                                       const int64_t* rows, const int64_t* dst, int32_t n, int32_t H,
+                                       int32_t B, int32_t D, int8_t* q_pool, int64_t q_stride_h,
+                                       int64_t q_stride_n, void* s_pool, int64_t s_stride_h,
+                                       int64_t s_stride_n, void* stream);
+
+/*
+ * Scatter-store of token vectors into a pool (reference engine/paged_cache.py:135-139 for the K/V pool and
+ * engine/quant_cache.py:139-141,165-167 for the bf16 staging slots):
+ *   pool[h, blocks[i], offsets[i], :] = convert(x[rows ? rows[i] : i, h, :])   for i < n, h < H.
+ * x in x_dtype, pool in pool_dtype (SIPA_F32 / SIPA_BF16 / SIPA_F16; conversion rounds to nearest even).
+ * A second tensor pair (x2, pool2) with the same shapes is stored in the same launch when x2 != NULL.
+ */
+int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dtype, int64_t x_stride_t,
+                          int64_t x_stride_h, const int64_t* rows, int32_t n, int32_t H, int32_t D,
+                          const int64_t* blocks, const int64_t* offsets, void* pool, void* pool2,
+                          int32_t pool_dtype, int64_t p_stride_h, int64_t p_stride_n, int64_t p_stride_b,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMALLINF_HIP_H */

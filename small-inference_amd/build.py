@@ -1,0 +1,54 @@
+"""Build recipe of libsmallinf_hip.so: hipcc for gfx950, in-tree, no torch extension machinery.
+
+    python small-inference_amd/build.py        # or __graft_entry__.build()
+
+The library is written next to the Python package (small-inference_amd/build/libsmallinf_hip.so) so that it
+travels with the source tree to the GPU machine; engine/_hip.py loads it from there.
+"""
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OUT_DIR = PKG / "build"
+LIB = OUT_DIR / "libsmallinf_hip.so"
+SOURCES = ["capi.hip", "decode.hip", "quant_store.hip"]
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_fma_f32 and kin); the kernels are written
+# with scalar fp32 arithmetic only.
+# Code object v5: loadable by torch's bundled HIP runtime (ROCm 7.0), which is the one in the process, since
+# torch's libamdhip64 is loaded first and shares the SONAME libamdhip64.so.7 with ROCm's.
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}", "-mcode-object-version=5",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas"]
+
+
+def hipcc() -> str:
+    """Path of hipcc (ROCm's, if not on PATH)."""
+    return shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into one shared library; returns its path. Always recompiles."""
+    OUT_DIR.mkdir(exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, "-I", str(ROOT / "include"), *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    if verbose and proc.stderr.strip():
+        print(proc.stderr, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

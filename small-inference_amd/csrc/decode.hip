@@ -1,0 +1,724 @@
+// Paged-attention decode for gfx950: one query token per sequence, K/V read in place from the block pool.
+//
+// Reference: engine/triton_decode.py:51-161 (_decode_kernel, _combine_kernel) and :188-238 (the wrapper).
+//
+// Work decomposition. A workgroup (4 waves) owns one (sequence s, KV head h, split sp): tokens
+// [sp*chunk, min((sp+1)*chunk, ctx[s])). Splits past a sequence's end exit at once, so one grid
+// (splits, Hkv, S) serves ragged batches: a long sequence spreads over many CUs, a short one uses one
+// workgroup. Every query head of the GQA group is computed from the same K/V loads, so each KV head's cache
+// is read from HBM once per call. The four waves of a workgroup take 32- (MFMA) or 64-token (VALU) tiles
+// round-robin and merge their online-softmax states through LDS at the end. A workgroup that holds a whole
+// sequence writes the output; otherwise it writes an unnormalised partial (acc, m, l) and either the last
+// workgroup of the (s, h) to finish merges all partials (an atomic counter per (s, h)), or a separate combine
+// kernel does.
+//
+// Online softmax per query head (reference engine/triton_decode.py:118-131), with scores kept in the exp2
+// domain (x * scale * log2 e):  m' = max(m, max_t s_t);  a = 2^(m - m');  l = l a + sum_t 2^(s_t - m');
+// acc = acc a + sum_t 2^(s_t - m') v_t;  out = acc / l.  Combine (reference :144-161):
+// M = max_j m_j;  out = sum_j 2^(m_j - M) acc_j / sum_j 2^(m_j - M) l_j.
+//
+// MFMA kernel (bf16 q and pool, 16-token blocks, head_dim 64 or 128, group <= 16). Per 32-token tile (two
+// blocks) and wave:
+//   S^T[16 tok x 16 g] = K[16 tok x 32 d] . Q^T[32 d x 16 g]   v_mfma_f32_16x16x32_bf16, D/32 steps per block
+//     A = K straight from HBM: lane (r, q4) = (lane % 16, lane / 16) loads 16 B of token r at channel
+//     32 j + 8 q4, so the 16 lanes of a quarter-wave read 16 rows x 16 B and each load instruction covers one
+//     contiguous 64-B half of every 128-B row of the block.
+//     B = the group's query rows (zero rows pad G to 16), loaded once per wave.
+//   Lane (r, q4) then holds head g = r for tokens 4 q4 .. 4 q4 + 3 of each block: the softmax state of head g
+//   lives in the 4 lanes r, r+16, r+32, r+48 (two xor-shuffles give the tile max).
+//   O^T[16 d x 16 g] += V^T[16 d x 32 tok] . P^T[32 tok x 16 g]    D/16 MFMAs per tile
+//     B = P^T comes from the S^T registers without any shuffle (token slot i of lane q4 is token
+//     16 (i / 4) + 4 q4 + i % 4); A = V^T needs 8 tokens of one channel per lane, so each wave stages its V
+//     tile in LDS (coalesced 2 KiB block loads, row-major with padding) and reads it back transposed.
+//   P is rounded to bf16 for the MFMA; the softmax itself and all accumulation stay fp32.
+//
+// VALU kernel (any supported shape, fp32 or bf16, all KV modes): lane = token for q.k (q of the group in
+// LDS as fp32, fp32 FMAs), lane = channel for p.v (p of the tile in LDS). IEEE fp32 arithmetic throughout,
+// as the reference uses for fp32 caches (engine/triton_decode.py:208-210).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "sipa_common.h"
+
+namespace sipa {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <bool OUT_F32>
+__device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, int d, float v) {
+  const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d;
+  if (OUT_F32)
+    ((float*)a.out)[i] = v;
+  else
+    ((uint16_t*)a.out)[i] = f32_to_bf16_bits(v);
+}
+
+// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G).
+template <int D, bool OUT_F32>
+__device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
+  const int G = a.G;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
+    float M = kNegInf;
+    for (int j = 0; j < nvalid; ++j) M = fmaxf(M, a.pm[row0 + j]);
+    float num = 0.f, den = 0.f;
+    for (int j = 0; j < nvalid; ++j) {
+      const float w = fast_exp2(a.pm[row0 + j] - M);
+      num += w * a.part[(row0 + j) * D + d];
+      den += w * a.pl[row0 + j];
+    }
+    store_out<OUT_F32>(a, s, h * G + g, d, num / den);
+  }
+}
+
+// Merge the four waves' states (ms, ls [4][16], accs [4][16][D] in LDS, after a barrier) and write the output
+// (whole sequence in this workgroup) or the split partial; with fused merging, the last split workgroup of
+// (s, h) to arrive then combines all partials.
+template <int D, bool OUT_F32>
+__device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nvalid, const float* ms,
+                             const float* ls, const float* accs, int* last_flag) {
+  const int G = a.G;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ms[w * kMaxGroup + g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = ms[w * kMaxGroup + g];
+      const float e = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);  // a wave with no tokens drops out
+      L += e * ls[w * kMaxGroup + g];
+      O += e * accs[(w * kMaxGroup + g) * D + d];
+    }
+    if (nvalid == 1) {
+      store_out<OUT_F32>(a, s, h * G + g, d, O / L);
+    } else {
+      const int64_t row = ((int64_t)s * a.Hq + h * G + g) * a.splits + sp;
+      a.part[row * D + d] = O;
+      if (d == 0) {
+        a.pm[row] = M;
+        a.pl[row] = L;
+      }
+    }
+  }
+  if (nvalid == 1 || !a.fused) return;
+  // Release this split's partial, count it, and let the last arriving split merge (acquire the others').
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(a.counters + (int64_t)s * a.Hkv + h, 1);
+    *last_flag = (prev == nvalid - 1);
+  }
+  __syncthreads();
+  if (!*last_flag) return;
+  __threadfence();
+  combine_group<D, OUT_F32>(a, s, h, nvalid);
+  if (threadIdx.x == 0) a.counters[(int64_t)s * a.Hkv + h] = 0;  // ready for the next call
+}
+
+// ---- MFMA kernel: bf16, B = 16 ---------------------------------------------------------------------------------
+
+template <int D>
+struct MfmaSmem {
+  static constexpr int kVPitch = D + 8;                                // bf16 elements per LDS row of V
+  static constexpr int kVBytes = kWaves * 32 * kVPitch * 2;            // per-wave [32 tok][D] V tiles
+  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * D) * 4;
+  static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
+};
+
+template <int D>
+__global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a) {
+  constexpr int KS = D / 32;  // QK k-steps per block
+  constexpr int DT = D / 16;  // PV d-tiles
+  constexpr int VC = D / 32;  // 16-byte V chunks per lane per block
+  constexpr int VP = MfmaSmem<D>::kVPitch;
+  constexpr int CPR = D / 8;  // 16-byte chunks per token row
+  __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
+  __shared__ int last_flag;
+
+  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int ctx = a.ctx[s];
+  const int start = sp * a.chunk;
+  if (start >= ctx) return;
+  const int end = min(start + a.chunk, ctx);
+  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  const int G = a.G;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+
+  bf16x8 qop[KS];
+  {
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      uint4 u = *(const uint4*)(qrow + 32 * j + 8 * q4);
+      if (r >= G) u = make_uint4(0, 0, 0, 0);
+      qop[j] = __builtin_bit_cast(bf16x8, u);
+    }
+  }
+
+  const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
+  const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
+  uint16_t* vw = (uint16_t*)smem + wave * 32 * VP;
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint4 kc[2][KS], vc[2][VC], kn[2][KS], vn[2][VC];
+
+  auto load_tile = [&](int t0, uint4(&kr)[2][KS], uint4(&vr)[2][VC]) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int tb = t0 + 16 * mt;
+      if (tb < end) {
+        const int blk = btr[tb >> 4];
+        const uint16_t* kb = kh + (int64_t)blk * a.kv_sn;
+        const uint4* vb = (const uint4*)(vh + (int64_t)blk * a.kv_sn);
+#pragma unroll
+        for (int j = 0; j < KS; ++j) kr[mt][j] = *(const uint4*)(kb + r * D + 32 * j + 8 * q4);
+#pragma unroll
+        for (int i = 0; i < VC; ++i) vr[mt][i] = vb[lane + 64 * i];
+      } else {
+#pragma unroll
+        for (int j = 0; j < KS; ++j) kr[mt][j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < VC; ++i) vr[mt][i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  int t0 = start + 32 * wave;
+  if (t0 < end) load_tile(t0, kc, vc);
+  for (; t0 < end; t0 += 32 * kWaves) {
+    const int tn = t0 + 32 * kWaves;
+    if (tn < end) load_tile(tn, kn, vn);
+
+    // V rows at or past the end of this split are masked (zero) so that 0-weight garbage cannot give NaN.
+    if (t0 + 32 > end) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < VC; ++i)
+          if (t0 + 16 * mt + (lane + 64 * i) / CPR >= end) vc[mt][i] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < VC; ++i) {
+        const int c = lane + 64 * i;
+        *(uint4*)(vw + (16 * mt + c / CPR) * VP + (c % CPR) * 8) = vc[mt][i];
+      }
+
+    f32x4 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kc[mt][j]), qop[j], sc[mt], 0,
+                                                         0, 0);
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 16 * mt + 4 * q4 + i;
+        sc[mt][i] = (t < end) ? sc[mt][i] * a.scale_log2 : kNegInf;
+        mx = fmaxf(mx, sc[mt][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    bf16x8 pop;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p = fast_exp2(sc[i >> 2][i & 3] - m_new);
+      psum += p;
+      pop[i] = (__bf16)p;
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+
+    wave_sync();  // the wave's V tile is in LDS
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x8 vop;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        vop[i] = __builtin_bit_cast(__bf16, vw[(16 * (i >> 2) + 4 * q4 + (i & 3)) * VP + 16 * dt + r]);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[dt], 0, 0, 0);
+    }
+    wave_sync();  // reads done before the next tile overwrites the LDS tile
+
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) kc[mt][j] = kn[mt][j];
+#pragma unroll
+      for (int i = 0; i < VC; ++i) vc[mt][i] = vn[mt][i];
+    }
+  }
+
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  __syncthreads();  // every wave is done with its V tile: the LDS becomes the merge buffer
+  float* ms = (float*)smem;
+  float* ls = ms + kWaves * kMaxGroup;
+  float* accs = ls + kWaves * kMaxGroup;
+  if (q4 == 0) {
+    ms[wave * kMaxGroup + r] = m_run;
+    ls[wave * kMaxGroup + r] = l_run;
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) *(f32x4*)(accs + (wave * kMaxGroup + r) * D + 16 * dt + 4 * q4) = acc[dt];
+  __syncthreads();
+  finish_split<D, false>(a, s, h, sp, nvalid, ms, ls, accs, &last_flag);
+}
+
+// ---- VALU kernel: any supported shape, fp32 / bf16, KV modes 0 / 1 / 2 -----------------------------------------
+
+template <int TQ>
+__device__ __forceinline__ void load8_f32(const void* base, int64_t i, float (&f)[8]) {
+  if (TQ == SIPA_F32) {
+    const float4* p = (const float4*)((const float*)base + i);
+    const float4 a = p[0], b = p[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 u = *(const uint4*)((const uint16_t*)base + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[2 * k] = __uint_as_float(w[k] << 16);
+      f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+}
+
+__device__ __forceinline__ void load8_i8(const int8_t* p, float (&f)[8]) {
+  const uint2 u = *(const uint2*)p;
+  const uint32_t w[2] = {u.x, u.y};
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) f[4 * k + b] = (float)(int8_t)(w[k] >> (8 * b));
+}
+
+__device__ __forceinline__ float load_scale(const void* p, int64_t i, int is_f32) {
+  return is_f32 ? ((const float*)p)[i] : f16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+template <int D>
+struct ValuSmem {
+  static constexpr int kPBytes = kWaves * 64 * kMaxGroup * 4;  // per-wave p tiles [64 tok][16 g]
+  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * D) * 4;
+  static constexpr int kBytes = kPBytes > kMergeBytes ? kPBytes : kMergeBytes;
+};
+
+template <int TQ, int MODE, int D>
+__global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
+  constexpr int DPL = (D + 63) / 64;  // channels per lane in p.v
+  __shared__ __align__(16) float qs[kMaxGroup * D];
+  __shared__ __align__(16) char smem[ValuSmem<D>::kBytes];
+  __shared__ int last_flag;
+
+  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int ctx = a.ctx[s];
+  const int start = sp * a.chunk;
+  if (start >= ctx) return;
+  const int end = min(start + a.chunk, ctx);
+  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  const int G = a.G, B = a.B;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads)
+    qs[idx] = load_as_f32(a.q, (int64_t)s * a.q_ss + (int64_t)(h * G + idx / D) * a.q_sh + idx % D, TQ);
+  __syncthreads();
+
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
+  const int n_quant = (ctx / B) * B;  // MODE 2: tokens in full (quantized) blocks; the rest are staged
+  const int tail = (MODE == 2) ? a.tail[s] : 0;
+  float* pw = (float*)smem + wave * 64 * kMaxGroup;
+
+  float m_run[kMaxGroup], l_run[kMaxGroup], acc[kMaxGroup][DPL];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) {
+    m_run[g] = kNegInf;
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int u = 0; u < DPL; ++u) acc[g][u] = 0.f;
+  }
+
+  for (int t0 = start + 64 * wave; t0 < end; t0 += 64 * kWaves) {
+    const int t = t0 + lane;
+    const bool valid = t < end;
+    int blk = 0, off = 0;
+    float sc[kMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) sc[g] = 0.f;
+    float vscale = 1.f;
+    if (valid) {
+      blk = btr[t / B];
+      off = t % B;
+      const int64_t row = (int64_t)h * a.kv_sh + (int64_t)blk * a.kv_sn + (int64_t)off * D;
+      const bool staged = (MODE == 2) && (t >= n_quant) && (tail >= 0);  // -1: no staging slot to read
+      for (int d0 = 0; d0 < D; d0 += 8) {
+        float kf[8];
+        if (MODE == 0) {
+          load8_f32<TQ>(a.k, row + d0, kf);
+        } else if (staged) {
+          load8_f32<SIPA_BF16>(a.stage, (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn + (int64_t)off * a.st_sb + d0,
+                               kf);
+        } else {
+          load8_i8((const int8_t*)a.k + row + d0, kf);
+          if (MODE == 2) {
+            const int64_t si = (int64_t)h * a.ks_sh + (int64_t)blk * a.ks_sn + d0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] *= load_scale(a.ks, si + i, a.ks_f32);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+          if (g < G) {
+            const float4 qa = *(const float4*)(qs + g * D + d0);
+            const float4 qb = *(const float4*)(qs + g * D + d0 + 4);
+            float x = sc[g];
+            x = fmaf(qa.x, kf[0], x); x = fmaf(qa.y, kf[1], x); x = fmaf(qa.z, kf[2], x); x = fmaf(qa.w, kf[3], x);
+            x = fmaf(qb.x, kf[4], x); x = fmaf(qb.y, kf[5], x); x = fmaf(qb.z, kf[6], x); x = fmaf(qb.w, kf[7], x);
+            sc[g] = x;
+          }
+        }
+      }
+      if (MODE == 1) {
+        const float ks = load_scale(a.ks, (int64_t)h * a.ks_sh + (int64_t)blk * a.ks_sn + off, a.ks_f32);
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) sc[g] *= ks;
+      }
+      if (MODE != 0) vscale = load_scale(a.vs, (int64_t)h * a.vs_sh + (int64_t)blk * a.vs_sn + off, a.vs_f32);
+    }
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+      if (g < G) {
+        const float x = valid ? sc[g] * a.scale_log2 : kNegInf;
+        const float m_new = fmaxf(m_run[g], wave_max(x));
+        const float alpha = fast_exp2(m_run[g] - m_new);
+        const float p = fast_exp2(x - m_new);
+        l_run[g] = l_run[g] * alpha + p;
+        m_run[g] = m_new;
+#pragma unroll
+        for (int u = 0; u < DPL; ++u) acc[g][u] *= alpha;
+        pw[lane * kMaxGroup + g] = p * vscale;  // V's per-token scale folds into p; l keeps the unscaled p
+      }
+    }
+    wave_sync();
+    const int ntok = min(64, end - t0);
+    for (int j = 0; j < ntok; ++j) {
+      const int bj = __builtin_amdgcn_readlane(blk, j);
+      const int oj = __builtin_amdgcn_readlane(off, j);
+      const int64_t row = (int64_t)h * a.kv_sh + (int64_t)bj * a.kv_sn + (int64_t)oj * D;
+      float vf[DPL];
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) {
+        const int d = lane + 64 * u;
+        if (d < D)
+          vf[u] = (MODE == 0) ? load_as_f32(a.v, row + d, TQ) : (float)((const int8_t*)a.v)[row + d];
+        else
+          vf[u] = 0.f;
+      }
+      const float4* prow = (const float4*)(pw + j * kMaxGroup);
+#pragma unroll
+      for (int g4 = 0; g4 < kMaxGroup / 4; ++g4) {
+        if (4 * g4 < G) {
+          const float4 p4 = prow[g4];
+          const float pg[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int u = 0; u < DPL; ++u) acc[4 * g4 + e][u] = fmaf(pg[e], vf[u], acc[4 * g4 + e][u]);
+        }
+      }
+    }
+    wave_sync();
+  }
+
+  float lw[kMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) lw[g] = (g < G) ? wave_sum(l_run[g]) : 0.f;
+  __syncthreads();  // p tiles are dead: the LDS becomes the merge buffer
+  float* ms = (float*)smem;
+  float* ls = ms + kWaves * kMaxGroup;
+  float* accs = ls + kWaves * kMaxGroup;
+  if (lane < kMaxGroup) {
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+      if (g == lane) {
+        ms[wave * kMaxGroup + g] = m_run[g];
+        ls[wave * kMaxGroup + g] = lw[g];
+      }
+  }
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g)
+    if (g < G)
+#pragma unroll
+      for (int u = 0; u < DPL; ++u) {
+        const int d = lane + 64 * u;
+        if (d < D) accs[(wave * kMaxGroup + g) * D + d] = acc[g][u];
+      }
+  __syncthreads();
+  finish_split<D, TQ == SIPA_F32>(a, s, h, sp, nvalid, ms, ls, accs, &last_flag);
+}
+
+// ---- separate combine kernel ------------------------------------------------------------------------------------
+
+template <int D, bool OUT_F32>
+__global__ void __launch_bounds__(kThreads) combine_splits(const DecodeArgs a) {
+  const int h = blockIdx.x, s = blockIdx.y;
+  const int nvalid = (a.ctx[s] + a.chunk - 1) / a.chunk;
+  if (nvalid <= 1) return;  // the single split wrote the output itself
+  combine_group<D, OUT_F32>(a, s, h, nvalid);
+}
+
+// ---- host side --------------------------------------------------------------------------------------------------
+
+static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+struct WorkspaceLayout {
+  int64_t counters, pm, pl, part, total;
+};
+
+static WorkspaceLayout workspace_layout(int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t splits) {
+  WorkspaceLayout w;
+  w.counters = 0;
+  w.pm = align256(S * Hkv * 4);
+  w.pl = w.pm + align256(S * Hq * splits * 4);
+  w.part = w.pl + align256(S * Hq * splits * 4);
+  w.total = w.part + align256(S * Hq * splits * D * 4);
+  return w;
+}
+
+static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count) {
+  if (S <= 0 || Hkv <= 0 || max_ctx <= 0) return 1;
+  if (cu_count <= 0) cu_count = 256;
+  const int64_t programs = (int64_t)S * Hkv;
+  const int64_t want = 4 * (int64_t)cu_count;  // workgroups: about four per CU
+  int64_t splits = (want + programs - 1) / programs;
+  splits = std::min<int64_t>(splits, ceil_div(max_ctx, kMinChunk));
+  splits = std::max<int64_t>(splits, ceil_div(max_ctx, kMaxChunk));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(splits, 1 << 20));
+}
+
+int split_chunk_host(int max_ctx, int splits) {
+  splits = std::max(1, splits);
+  const int per = ceil_div(std::max(1, max_ctx), splits);
+  return ceil_div(per, kChunkAlign) * kChunkAlign;
+}
+
+template <typename Kernel>
+static int launch(Kernel k, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k, grid, dim3(kThreads), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIPA_EHIP, "decode launch failed: %s", hipGetErrorString(e));
+  return SIPA_OK;
+}
+
+template <int TQ, int D>
+static int launch_valu(int mode, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  switch (mode) {
+    case 0: return launch(decode_valu<TQ, 0, D>, grid, a, st);
+    case 1: return launch(decode_valu<TQ, 1, D>, grid, a, st);
+    default: return launch(decode_valu<TQ, 2, D>, grid, a, st);
+  }
+}
+
+template <int TQ>
+static int dispatch_valu(int D, int mode, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  switch (D) {
+    case 16: return launch_valu<TQ, 16>(mode, grid, a, st);
+    case 32: return launch_valu<TQ, 32>(mode, grid, a, st);
+    case 64: return launch_valu<TQ, 64>(mode, grid, a, st);
+    default: return launch_valu<TQ, 128>(mode, grid, a, st);
+  }
+}
+
+template <bool F32>
+static int dispatch_combine(int D, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  switch (D) {
+    case 16: return launch(combine_splits<16, F32>, grid, a, st);
+    case 32: return launch(combine_splits<32, F32>, grid, a, st);
+    case 64: return launch(combine_splits<64, F32>, grid, a, st);
+    default: return launch(combine_splits<128, F32>, grid, a, st);
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace sipa
+
+using namespace sipa;
+
+extern "C" int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context,
+                                      int32_t cu_count) {
+  return choose_splits_host(num_seqs, num_kv_heads, max_context, cu_count);
+}
+
+extern "C" int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits) {
+  return split_chunk_host(max_context, num_splits);
+}
+
+static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int* chunk) {
+  int splits = requested;
+  if (splits <= 0) splits = choose_splits_host(S, Hkv, max_ctx, sipa_device_cu_count(-1));
+  *chunk = split_chunk_host(max_ctx, splits);
+  return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
+}
+
+extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                               int32_t head_dim, int32_t num_splits) {
+  if (num_splits <= 1) return 0;
+  return workspace_layout(num_seqs, num_q_heads, num_kv_heads, head_dim, num_splits).total;
+}
+
+extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
+  SIPA_CHECK(p != nullptr, SIPA_EINVAL, "params is NULL");
+  SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params), SIPA_EINVAL,
+             "struct_size %d does not match this library's sipa_decode_params (%d bytes)", p->struct_size,
+             (int)sizeof(sipa_decode_params));
+  const int S = p->num_seqs, Hq = p->num_q_heads, Hkv = p->num_kv_heads, D = p->head_dim, B = p->block_size;
+  if (S == 0) return SIPA_OK;
+  SIPA_CHECK(S > 0 && S <= 65535, SIPA_EINVAL, "num_seqs %d outside [0, 65535]", S);
+  SIPA_CHECK(Hkv > 0 && Hkv <= 65535 && Hq > 0 && Hq % Hkv == 0, SIPA_EINVAL,
+             "num_q_heads %d must be a positive multiple of num_kv_heads %d", Hq, Hkv);
+  const int G = Hq / Hkv;
+  SIPA_CHECK(G <= kMaxGroup, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kMaxGroup);
+  SIPA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {16,32,64,128}", D);
+  SIPA_CHECK(B > 0 && 64 % B == 0, SIPA_EINVAL, "block_size %d must divide 64 (block-aligned 64-token tiles)", B);
+  SIPA_CHECK(p->max_context > 0, SIPA_EINVAL, "max_context %d must be >= 1", p->max_context);
+  SIPA_CHECK(p->q_dtype == SIPA_F32 || p->q_dtype == SIPA_BF16, SIPA_EUNSUPPORTED, "q_dtype %d not f32/bf16",
+             p->q_dtype);
+  SIPA_CHECK(p->kv_mode >= 0 && p->kv_mode <= 2, SIPA_EINVAL, "kv_mode %d", p->kv_mode);
+  SIPA_CHECK(p->q && p->k_cache && p->v_cache && p->block_tables && p->context_lens && p->out, SIPA_EINVAL,
+             "NULL tensor pointer");
+  SIPA_CHECK(aligned16(p->k_cache) && aligned16(p->v_cache), SIPA_EINVAL, "K/V pools must be 16-byte aligned");
+  SIPA_CHECK(p->kv_stride_h % 16 == 0 && p->kv_stride_n % 16 == 0, SIPA_EINVAL,
+             "pool head/block strides must be multiples of 16 elements");
+  const int mode = p->kv_mode;
+  if (mode != SIPA_KV_PLAIN) {
+    SIPA_CHECK(p->k_scale && p->v_scale, SIPA_EINVAL, "INT8 modes need k_scale and v_scale");
+    SIPA_CHECK((p->k_scale_dtype == SIPA_F16 || p->k_scale_dtype == SIPA_F32) &&
+                   (p->v_scale_dtype == SIPA_F16 || p->v_scale_dtype == SIPA_F32),
+               SIPA_EUNSUPPORTED, "scales must be f16 or f32");
+  }
+  if (mode == SIPA_KV_INT8_KCHAN) {
+    SIPA_CHECK(p->stage && p->tail_slots, SIPA_EINVAL, "int8 per-channel K needs stage and tail_slots");
+    SIPA_CHECK(aligned16(p->stage) && p->st_stride_h % 8 == 0 && p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
+               SIPA_EINVAL, "staging must be 16-byte aligned with strides multiple of 8");
+  }
+
+  int chunk = 0;
+  const int splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, &chunk);
+
+  DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = p->q;
+  a.q_ss = p->q_stride_s;
+  a.q_sh = p->q_stride_h;
+  a.k = p->k_cache;
+  a.v = p->v_cache;
+  a.kv_sh = p->kv_stride_h;
+  a.kv_sn = p->kv_stride_n;
+  a.bt = p->block_tables;
+  a.bt_ss = p->bt_stride_s;
+  a.ctx = p->context_lens;
+  a.out = p->out;
+  a.o_ss = p->out_stride_s;
+  a.o_sh = p->out_stride_h;
+  a.ks = p->k_scale;
+  a.ks_sh = p->ks_stride_h;
+  a.ks_sn = p->ks_stride_n;
+  a.vs = p->v_scale;
+  a.vs_sh = p->vs_stride_h;
+  a.vs_sn = p->vs_stride_n;
+  a.stage = p->stage;
+  a.st_sh = p->st_stride_h;
+  a.st_sn = p->st_stride_n;
+  a.st_sb = p->st_stride_b;
+  a.tail = p->tail_slots;
+  a.ks_f32 = p->k_scale_dtype == SIPA_F32;
+  a.vs_f32 = p->v_scale_dtype == SIPA_F32;
+  a.S = S;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = G;
+  a.B = B;
+  a.splits = splits;
+  a.chunk = chunk;
+  a.fused = p->combine == SIPA_COMBINE_FUSED;
+  a.scale_log2 = p->scale * 1.4426950408889634f;
+
+  if (splits > 1) {
+    const WorkspaceLayout w = workspace_layout(S, Hq, Hkv, D, splits);
+    SIPA_CHECK(p->workspace != nullptr && p->workspace_bytes >= w.total, SIPA_EWORKSPACE,
+               "workspace of %lld bytes needed for %d splits (got %lld)", (long long)w.total, splits,
+               (long long)p->workspace_bytes);
+    SIPA_CHECK(((uintptr_t)p->workspace & 255) == 0, SIPA_EWORKSPACE, "workspace must be 256-byte aligned");
+    char* base = (char*)p->workspace;
+    a.counters = (int32_t*)(base + w.counters);
+    a.pm = (float*)(base + w.pm);
+    a.pl = (float*)(base + w.pl);
+    a.part = (float*)(base + w.part);
+  }
+
+  const bool q_aligned = aligned16(p->q) && p->q_stride_s % 8 == 0 && p->q_stride_h % 8 == 0;
+  const bool mfma_ok = p->q_dtype == SIPA_BF16 && mode == SIPA_KV_PLAIN && B == 16 && (D == 64 || D == 128) &&
+                       q_aligned;
+  SIPA_CHECK(p->impl != SIPA_IMPL_MFMA || mfma_ok, SIPA_EUNSUPPORTED,
+             "the MFMA kernel needs bf16, kv_mode 0, block 16, head_dim 64/128 and 16-byte aligned q rows");
+  const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
+
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(splits, Hkv, S);
+  int rc;
+  if (use_mfma)
+    rc = (D == 64) ? launch(decode_mfma_bf16<64>, grid, a, st) : launch(decode_mfma_bf16<128>, grid, a, st);
+  else if (p->q_dtype == SIPA_F32)
+    rc = dispatch_valu<SIPA_F32>(D, mode, grid, a, st);
+  else
+    rc = dispatch_valu<SIPA_BF16>(D, mode, grid, a, st);
+  if (rc != SIPA_OK || splits == 1 || a.fused) return rc;
+  return p->q_dtype == SIPA_F32 ? dispatch_combine<true>(D, dim3(Hkv, S), a, st)
+                                : dispatch_combine<false>(D, dim3(Hkv, S), a, st);
+}

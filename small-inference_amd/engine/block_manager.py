@@ -1,0 +1,150 @@
+"""Which fixed-size blocks of the KV pool each sequence owns (CPU bookkeeping).
+
+Same contract as the reference's BlockManager (engine/block_manager.py:19-137), because block-table indexing
+must be bit-exact with it:
+  - a token's slot is table[p // B] * B + p % B;
+  - free blocks form a LIFO stack that initially hands out block 0, then 1, ...; a freed sequence's blocks go
+    back in reverse table order, so the next allocation receives them in their old table order, and long-lived
+    pools end up with scattered, non-monotonic tables;
+  - per-block reference counts (0 or 1 without sharing), free listeners, OutOfBlocks leaves state unchanged.
+"""
+
+from __future__ import annotations
+
+from typing import Callable
+
+
+class OutOfBlocks(RuntimeError):
+    """Not enough free blocks for the request; nothing was changed."""
+
+
+class BlockManager:
+    def __init__(self, num_blocks: int, block_size: int = 16):
+        """A pool of num_blocks blocks of block_size tokens, all free."""
+        if num_blocks < 1 or block_size < 1:
+            raise ValueError("need at least one block of at least one token")
+        self.num_blocks, self.block_size = num_blocks, block_size
+        # The top of the stack is the end of the list: block 0 is handed out first.
+        self._free: list[int] = list(reversed(range(num_blocks)))
+        self._ref = [0] * num_blocks
+        self._tables: dict[int, list[int]] = {}
+        self._lengths: dict[int, int] = {}
+        self._free_listeners: list[Callable[[list[int]], None]] = []
+
+    # ---- queries -------------------------------------------------------------------------------------------------
+
+    def blocks_for(self, n_tokens: int) -> int:
+        """ceil(n_tokens / block_size)."""
+        return (n_tokens + self.block_size - 1) // self.block_size
+
+    def num_free_blocks(self) -> int:
+        """Blocks owned by no sequence."""
+        return len(self._free)
+
+    def can_allocate(self, n_tokens: int, watermark_blocks: int = 0) -> bool:
+        """Whether a new sequence of n_tokens fits while keeping watermark_blocks free."""
+        return self.blocks_for(n_tokens) + watermark_blocks <= len(self._free)
+
+    def new_blocks_needed(self, seq_id: int, n: int = 1) -> int:
+        """Blocks that appending n tokens to seq_id takes from the free stack."""
+        return self.blocks_for(self._lengths[seq_id] + n) - len(self._tables[seq_id])
+
+    def can_append(self, seq_id: int, n: int = 1) -> bool:
+        """Whether n more tokens fit for seq_id."""
+        return self.new_blocks_needed(seq_id, n) <= len(self._free)
+
+    def ref_count(self, block: int) -> int:
+        """Sequences holding `block`."""
+        return self._ref[block]
+
+    def block_table(self, seq_id: int) -> list[int]:
+        """The sequence's blocks in token order (a copy)."""
+        return self._tables[seq_id][:]
+
+    def seq_len(self, seq_id: int) -> int:
+        """Tokens the sequence holds."""
+        return self._lengths[seq_id]
+
+    def seq_ids(self) -> list[int]:
+        """Live sequences."""
+        return list(self._tables)
+
+    def slots(self, seq_id: int, start: int, end: int) -> list[int]:
+        """Slots of positions [start, end) of the sequence."""
+        n = self._lengths[seq_id]
+        if not (0 <= start <= end <= n):
+            raise ValueError(f"positions [{start}, {end}) outside sequence {seq_id} of length {n}")
+        table, B = self._tables[seq_id], self.block_size
+        return [table[p // B] * B + p % B for p in range(start, end)]
+
+    # ---- mutations -----------------------------------------------------------------------------------------------
+
+    def add_free_listener(self, fn: Callable[[list[int]], None]) -> None:
+        """Call fn(blocks) with the blocks each free() returns to the stack."""
+        self._free_listeners.append(fn)
+
+    def _pop_blocks(self, count: int) -> list[int]:
+        taken = []
+        for _ in range(count):
+            b = self._free.pop()
+            assert self._ref[b] == 0, f"block {b} on the free list with ref count {self._ref[b]}"
+            self._ref[b] = 1
+            taken.append(b)
+        return taken
+
+    def allocate(self, seq_id: int, n_tokens: int) -> list[int]:
+        """Create seq_id holding n_tokens (>= 0) and return their slots."""
+        if seq_id in self._tables:
+            raise ValueError(f"sequence {seq_id} already allocated")
+        if n_tokens < 0:
+            raise ValueError("n_tokens must be >= 0")
+        need = self.blocks_for(n_tokens)
+        if need > len(self._free):
+            raise OutOfBlocks(f"{need} blocks needed, {len(self._free)} free")
+        self._tables[seq_id] = self._pop_blocks(need)
+        self._lengths[seq_id] = n_tokens
+        return self.slots(seq_id, 0, n_tokens)
+
+    def append_slots(self, seq_id: int, n: int = 1) -> list[int]:
+        """Extend seq_id by n tokens and return their slots."""
+        need = self.new_blocks_needed(seq_id, n)
+        if need > len(self._free):
+            raise OutOfBlocks(f"sequence {seq_id}: {need} blocks needed, {len(self._free)} free")
+        self._tables[seq_id].extend(self._pop_blocks(need))
+        start = self._lengths[seq_id]
+        self._lengths[seq_id] = start + n
+        return self.slots(seq_id, start, start + n)
+
+    def append_slot(self, seq_id: int) -> int:
+        """Extend seq_id by one token and return its slot."""
+        return self.append_slots(seq_id, 1)[0]
+
+    def free(self, seq_id: int) -> None:
+        """Release seq_id; a block returns to the stack when its reference count reaches 0."""
+        table = self._tables.pop(seq_id)
+        del self._lengths[seq_id]
+        released = []
+        for b in table[::-1]:  # last block first, so the stack hands the blocks out again in table order
+            self._ref[b] -= 1
+            assert self._ref[b] >= 0, f"block {b} freed twice"
+            if self._ref[b] == 0:
+                self._free.append(b)
+                released.append(b)
+        for fn in self._free_listeners:
+            fn(released)
+
+    # ---- checking ------------------------------------------------------------------------------------------------
+
+    def check_invariants(self) -> None:
+        """Assert consistency: every block free xor owned, reference counts equal owners, table sizes match
+        lengths. Raises AssertionError otherwise."""
+        free = set(self._free)
+        assert len(free) == len(self._free), "duplicate block on the free list"
+        owners = [0] * self.num_blocks
+        for seq_id, table in self._tables.items():
+            assert len(table) == self.blocks_for(self._lengths[seq_id]), f"sequence {seq_id}: table size wrong"
+            for b in table:
+                owners[b] += 1
+        for b, n in enumerate(owners):
+            assert n == self._ref[b], f"block {b}: ref {self._ref[b]} but {n} owners"
+            assert (b in free) == (n == 0), f"block {b}: free={b in free} with {n} owners"

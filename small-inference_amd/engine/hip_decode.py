@@ -1,0 +1,170 @@
+"""Paged decode attention on MI355X through libsmallinf_hip.so: the drop-in for the reference's
+engine/triton_decode.py (paged_decode_attention, choose_splits, QuantKV; reference :164-238).
+
+One query token per sequence, K/V read in place from the [Hkv, N, B, D] pool of one layer through the block
+tables. The split count comes from the GPU's CU count instead of the reference's 20-SM constants: enough
+(sequence, KV head, split) workgroups to fill the 256 CUs several times over, splits of at most 512 tokens so that
+ragged batches balance. A split past a sequence's end does no work; the last split workgroup of a (sequence, KV
+head) to finish merges the partials (combine="fused"), or a second kernel does (combine="kernel").
+
+Kernels: bf16 pools with 16-token blocks and head_dim 64/128 run the MFMA kernel; everything else (fp32 models,
+other block sizes or head dims, and both INT8 modes) runs the VALU kernel. impl="valu" / "mfma" forces one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _hip
+
+TILE = 64  # split chunks are multiples of 64 tokens; the block size must divide it (as in the reference)
+DEFAULT_CU_COUNT = 256  # MI355X; used when no GPU is visible (host-side planning only)
+
+
+@dataclass
+class QuantKV:
+    """INT8 side inputs of one layer. mode 1: k_scale, v_scale [Hkv, N, B] (per token). mode 2: k_scale
+    [Hkv, N, D] (per block and channel; a zero block stride gives per-(head, channel) scales), v_scale [Hkv, N, B],
+    stage [Hkv, n_stage, B, D] bf16 holding each sequence's partial last block of K, tail_slots [S] int32 (the
+    sequence's staging slot, -1 if its last block is full). Scales are fp16 (the caches') or fp32."""
+    mode: int
+    k_scale: torch.Tensor
+    v_scale: torch.Tensor
+    stage: torch.Tensor | None = None
+    tail_slots: torch.Tensor | None = None
+
+
+_cu_counts: dict[int, int] = {}
+
+
+def device_cu_count(device: torch.device | int | None = None) -> int:
+    """CU count of a GPU (cached); DEFAULT_CU_COUNT when no GPU is visible."""
+    if not torch.cuda.is_available():
+        return DEFAULT_CU_COUNT
+    if device is None:
+        idx = torch.cuda.current_device()
+    else:
+        d = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        idx = d.index if d.index is not None else torch.cuda.current_device()
+    if idx not in _cu_counts:
+        n = _hip.lib().sipa_device_cu_count(idx)
+        if n <= 0:
+            _hip.check(n, "sipa_device_cu_count")
+        _cu_counts[idx] = n
+    return _cu_counts[idx]
+
+
+def choose_splits(num_seqs: int, num_kv_heads: int, max_context: int, cu_count: int | None = None) -> int:
+    """Splits per sequence for a call: about four workgroups per CU, splits of 256 to 512 tokens."""
+    cu = device_cu_count() if cu_count is None else cu_count
+    return int(_hip.lib().sipa_choose_splits(num_seqs, num_kv_heads, max_context, cu))
+
+
+def split_plan(max_context: int, num_splits: int) -> tuple[int, int]:
+    """(splits actually launched, tokens per split) for a requested split count: chunks are rounded up to a
+    multiple of 64 tokens and splits that would be empty for every sequence are dropped."""
+    chunk = int(_hip.lib().sipa_split_chunk(max_context, num_splits))
+    return math.ceil(max_context / chunk), chunk
+
+
+# Workspace (split partials + merge counters) per (device, stream): zero-filled once, the kernels leave the
+# counters zero again, so later calls on the same stream reuse it without a memset.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                           context_lens: torch.Tensor, scale: float, max_context: int,
+                           num_splits: int | None = None, quant: QuantKV | None = None, *, impl: str = "auto",
+                           combine: str = "fused", out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention of one query token per sequence over its paged context.
+
+    q [S, Hq, D] (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, B, D], one layer of the
+    pool, contiguous (int8 when `quant` is given); block_tables [S, max_blocks] int32; context_lens [S] int32 (each
+    >= 1, the new token included); max_context = max(context_lens), known on the host. num_splits None picks from
+    the CU count. Returns [S, Hq, D] in q's dtype (written into `out` if given).
+    """
+    S, Hq, D = q.shape
+    Hkv, N, B, _ = k_cache.shape
+    assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and block_tables.stride(-1) == 1
+    assert TILE % B == 0, "tiles must be block-aligned"
+    _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens)
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise ValueError("block_tables and context_lens must be int32")
+    if not context_lens.is_contiguous():
+        context_lens = context_lens.contiguous()
+    if out is None:
+        out = torch.empty(S, Hq, D, device=q.device, dtype=q.dtype)
+    elif out.shape != (S, Hq, D) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must be [S, Hq, D] in q's dtype with a contiguous last dim")
+    if S == 0:
+        return out
+
+    requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
+    splits, _ = split_plan(max_context, requested)
+    lib = _hip.lib()
+    stream = _hip.stream_of(q)
+
+    p = _hip.DecodeParams()
+    p.struct_size = ctypes.sizeof(_hip.DecodeParams)
+    p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = S, Hq, Hkv, D, B
+    p.num_blocks, p.max_context, p.num_splits = N, max_context, requested
+    p.q_dtype = _hip.dtype_code(q.dtype)
+    p.impl = _hip.IMPL[impl]
+    p.combine = _hip.COMBINE[combine]
+    p.scale = float(scale)
+    p.q, p.q_stride_s, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
+    p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
+    p.context_lens = context_lens.data_ptr()
+    p.out, p.out_stride_s, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    keep = []  # tensors that must outlive the call
+    if quant is None:
+        if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+            raise ValueError("without `quant` the pool must be in q's dtype")
+        p.kv_mode = _hip.KV_PLAIN
+    else:
+        if k_cache.dtype != torch.int8 or v_cache.dtype != torch.int8:
+            raise ValueError("INT8 modes need int8 pools")
+        if quant.mode not in (1, 2):
+            raise ValueError(f"QuantKV.mode must be 1 or 2, got {quant.mode}")
+        ks, vs = quant.k_scale, quant.v_scale
+        if ks.stride(-1) != 1 or vs.stride(-1) != 1:
+            raise ValueError("scales need a contiguous last dim")
+        p.kv_mode = quant.mode
+        p.k_scale, p.k_scale_dtype, p.ks_stride_h, p.ks_stride_n = \
+            ks.data_ptr(), _hip.dtype_code(ks.dtype), ks.stride(0), ks.stride(1)
+        p.v_scale, p.v_scale_dtype, p.vs_stride_h, p.vs_stride_n = \
+            vs.data_ptr(), _hip.dtype_code(vs.dtype), vs.stride(0), vs.stride(1)
+        if quant.mode == 2:
+            st, tails = quant.stage, quant.tail_slots
+            if st is None or tails is None:
+                raise ValueError("mode 2 needs stage and tail_slots")
+            if st.dtype != torch.bfloat16 or st.stride(-1) != 1:
+                raise ValueError("stage must be bf16 with a contiguous last dim")
+            if tails.dtype != torch.int32:
+                raise ValueError("tail_slots must be int32")
+            tails = tails.contiguous()
+            keep.append(tails)
+            p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = st.data_ptr(), st.stride(0), st.stride(1), \
+                st.stride(2)
+            p.tail_slots = tails.data_ptr()
+    if splits > 1:
+        nbytes = int(lib.sipa_decode_workspace_bytes(S, Hq, Hkv, D, requested))
+        ws = _workspace(q.device, stream, nbytes)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    _hip.check(lib.sipa_decode(ctypes.byref(p), stream), "paged_decode_attention")
+    return out

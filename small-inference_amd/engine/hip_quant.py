@@ -1,0 +1,100 @@
+"""Fused INT8 quantize-and-store and plain scatter-store on MI355X through libsmallinf_hip.so: the drop-in for the
+reference's engine/triton_quant.py (quantize_store_tokens, quantize_store_blocks; reference :61-84), plus the two
+stores the reference leaves to torch ops (the pool scatter of engine/paged_cache.py:135-139 and format B's
+staging and whole-block writes, engine/quant_cache.py:165-177).
+
+The quantizer is bit-exact with engine/quant.py: scale = fp16(absmax / 127), code = clamp(rint(x / scale),
+-127, 127) with IEEE fp32 division and round-half-even; a zero scale gives zero codes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+
+
+def _i64(t: torch.Tensor) -> torch.Tensor:
+    """Index vectors go to the kernels as contiguous int64."""
+    return t if (t.dtype == torch.int64 and t.is_contiguous()) else t.to(torch.int64).contiguous()
+
+
+def quantize_store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, q_pool: torch.Tensor,
+                          s_pool: torch.Tensor) -> None:
+    """x [T, H, D] (rows may be strided; last dim contiguous) -> q_pool [H, N, B, D] int8 and s_pool [H, N, B]
+    fp16 at (blocks[t], offsets[t]). One launch."""
+    T, H, D = x.shape
+    if T == 0:
+        return
+    assert x.stride(-1) == 1 and q_pool.is_contiguous() and s_pool.is_contiguous()
+    if q_pool.dtype != torch.int8 or s_pool.dtype != torch.float16:
+        raise ValueError("q_pool must be int8 and s_pool fp16")
+    _hip.require_gpu(x, blocks, offsets, q_pool, s_pool)
+    blocks, offsets = _i64(blocks), _i64(offsets)
+    rc = _hip.lib().sipa_quantize_store_tokens(
+        x.data_ptr(), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), T, H, D, blocks.data_ptr(),
+        offsets.data_ptr(), q_pool.data_ptr(), q_pool.stride(0), q_pool.stride(1), q_pool.shape[2],
+        s_pool.data_ptr(), s_pool.stride(0), s_pool.stride(1), _hip.stream_of(x))
+    _hip.check(rc, "quantize_store_tokens")
+
+
+def quantize_store_blocks(src_pool: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, q_pool: torch.Tensor,
+                          s_pool: torch.Tensor) -> None:
+    """Blocks src_pool[:, src[i]] ([H, n_src, B, D], e.g. bf16 staging) -> q_pool[:, dst[i]] int8 with per-channel
+    scales s_pool[:, dst[i]] ([H, N, D] fp16). One launch."""
+    if src.numel() == 0:
+        return
+    H, _, B, D = src_pool.shape
+    assert src_pool.is_contiguous() and q_pool.is_contiguous() and s_pool.is_contiguous()
+    if q_pool.dtype != torch.int8 or s_pool.dtype != torch.float16:
+        raise ValueError("q_pool must be int8 and s_pool fp16")
+    _hip.require_gpu(src_pool, src, dst, q_pool, s_pool)
+    src, dst = _i64(src), _i64(dst)
+    rc = _hip.lib().sipa_quantize_store_blocks(
+        src_pool.data_ptr(), _hip.dtype_code(src_pool.dtype), src_pool.stride(0), src_pool.stride(1),
+        src_pool.stride(2), src.data_ptr(), dst.data_ptr(), src.numel(), H, B, D, q_pool.data_ptr(),
+        q_pool.stride(0), q_pool.stride(1), s_pool.data_ptr(), s_pool.stride(0), s_pool.stride(1),
+        _hip.stream_of(src_pool))
+    _hip.check(rc, "quantize_store_blocks")
+
+
+def quantize_store_block_rows(x: torch.Tensor, rows: torch.Tensor, dst: torch.Tensor, q_pool: torch.Tensor,
+                              s_pool: torch.Tensor) -> None:
+    """Whole blocks taken from rows of x [T, H, D]: block i is rows[i*B : (i+1)*B] (B = q_pool's block size),
+    rounded to bf16, then quantized per channel into q_pool[:, dst[i]], s_pool[:, dst[i]]. One launch."""
+    if dst.numel() == 0:
+        return
+    H, _, B, D = q_pool.shape
+    assert x.stride(-1) == 1 and q_pool.is_contiguous() and s_pool.is_contiguous()
+    if rows.numel() != dst.numel() * B:
+        raise ValueError(f"{rows.numel()} rows for {dst.numel()} blocks of {B}")
+    _hip.require_gpu(x, rows, dst, q_pool, s_pool)
+    rows, dst = _i64(rows), _i64(dst)
+    rc = _hip.lib().sipa_quantize_store_block_rows(
+        x.data_ptr(), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), rows.data_ptr(), dst.data_ptr(),
+        dst.numel(), H, B, D, q_pool.data_ptr(), q_pool.stride(0), q_pool.stride(1), s_pool.data_ptr(),
+        s_pool.stride(0), s_pool.stride(1), _hip.stream_of(x))
+    _hip.check(rc, "quantize_store_block_rows")
+
+
+def store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, pool: torch.Tensor,
+                 rows: torch.Tensor | None = None, x2: torch.Tensor | None = None,
+                 pool2: torch.Tensor | None = None) -> None:
+    """pool[:, blocks[i], offsets[i]] = x[rows[i] if rows is not None else i] (x [T, H, D], pool [H, N, B, D]),
+    converted to the pool's dtype with round-to-nearest-even; (x2, pool2) in the same launch. One launch."""
+    n = blocks.numel()
+    if n == 0:
+        return
+    _, H, D = x.shape
+    assert x.stride(-1) == 1 and pool.stride(-1) == 1
+    if x2 is not None:
+        assert x2.shape == x.shape and x2.stride() == x.stride() and x2.dtype == x.dtype
+        assert pool2 is not None and pool2.stride() == pool.stride() and pool2.dtype == pool.dtype
+    _hip.require_gpu(x, blocks, offsets, pool)
+    blocks, offsets = _i64(blocks), _i64(offsets)
+    rows = None if rows is None else _i64(rows)
+    rc = _hip.lib().sipa_store_tokens(
+        x.data_ptr(), _hip.ptr(x2), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), _hip.ptr(rows), n, H, D,
+        blocks.data_ptr(), offsets.data_ptr(), pool.data_ptr(), _hip.ptr(pool2), _hip.dtype_code(pool.dtype),
+        pool.stride(0), pool.stride(1), pool.stride(2), _hip.stream_of(x))
+    _hip.check(rc, "store_tokens")

@@ -1,0 +1,203 @@
+"""Paged KV cache: the block pool, per-forward packed metadata, and the begin / write / attend interface the
+model calls (drop-in for the reference's engine/paged_cache.py:28-180).
+
+Pool layout per layer: K and V as [H_kv, num_blocks, block_size, d] ([2, N, 16, 64] for Qwen2.5-0.5B); one
+(head, block) is 16 x 64 x 2 B = 2 KiB contiguous in HBM, the unit the decode kernel streams. A token's slot
+(block * B + offset) addresses [:, block, offset] in every layer.
+
+Backends (attn_backend, mutable after construction):
+  "hip"    decode rows (one new token per sequence) go through the HIP paged-decode kernel in one launch per
+           layer, reading blocks in place; rows with several new tokens (prefill chunks) use the gather path.
+  "triton" the reference's name for the same in-place decode backend: selects the HIP kernel, so callers that
+           pass it (the reference's ContinuousEngine defaults to it) run unchanged.
+  "gather" every sequence gathers its blocks and runs attention() (the reference's default).
+On a GPU pool, write() scatters K and V with one HIP store launch; a CPU pool uses torch indexing.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .attention import attention
+from .block_manager import BlockManager
+from .config import ModelConfig
+
+BACKENDS = ("gather", "hip", "triton")
+KERNEL_BACKENDS = ("hip", "triton")
+
+
+@dataclass
+class PagedMetadata:
+    """What a forward needs to read and write the paged cache: CPU lists for host-side loops, device tensors for
+    the kernels. Built once per forward, shared by every layer."""
+    num_tokens: int
+    query_starts: list[int]  # [num_seqs + 1]: sequence i's new tokens are rows query_starts[i]:query_starts[i+1]
+    context_lens: list[int]  # [num_seqs]: tokens in the cache after this forward's writes
+    positions: torch.Tensor  # [T] absolute position of each new token
+    slots_cpu: list[int]  # [T] the same slots on the CPU
+    slot_mapping: torch.Tensor  # [T] int64 slot of each new token
+    slot_blocks: torch.Tensor  # [T] slot // block_size
+    slot_offsets: torch.Tensor  # [T] slot % block_size
+    block_ids: list[torch.Tensor]  # per sequence: its first ceil(context_len / B) blocks, int64 on the device
+    block_ids_cpu: list[list[int]]  # the same on the CPU
+    block_tables: torch.Tensor  # [num_seqs, max_blocks] int32, padded with -1 (the kernel-facing form)
+    context_lens_t: torch.Tensor  # [num_seqs] int32 on the device
+    last_token_indices: torch.Tensor  # [num_seqs] row of each sequence's last new token
+
+    @property
+    def num_seqs(self) -> int:
+        """Sequences in this forward."""
+        return len(self.context_lens)
+
+
+def build_metadata(manager: BlockManager, batch: list[tuple[int, int, int]],
+                   device: str | torch.device) -> PagedMetadata:
+    """Metadata for a forward over batch = [(seq_id, start, n), ...]: n new tokens per sequence at positions
+    start .. start + n - 1, whose slots the manager already holds. Afterwards each context is start + n tokens."""
+    B = manager.block_size
+    positions: list[int] = []
+    slot_list: list[int] = []
+    starts, lens, tables = [0], [], []
+    for seq_id, start, n in batch:
+        if n < 1:
+            raise ValueError(f"sequence {seq_id}: a forward needs at least one new token")
+        ctx = start + n
+        held = manager.seq_len(seq_id)
+        if held < ctx:
+            raise ValueError(f"sequence {seq_id} holds {held} tokens, forward needs {ctx}")
+        positions.extend(range(start, ctx))
+        slot_list.extend(manager.slots(seq_id, start, ctx))
+        starts.append(starts[-1] + n)
+        lens.append(ctx)
+        tables.append(manager.block_table(seq_id)[:manager.blocks_for(ctx)])
+    width = max(len(t) for t in tables)
+
+    def dev64(xs):
+        return torch.tensor(xs, dtype=torch.int64, device=device)
+
+    return PagedMetadata(
+        num_tokens=len(positions),
+        query_starts=starts,
+        context_lens=lens,
+        positions=dev64(positions),
+        slots_cpu=slot_list,
+        slot_mapping=dev64(slot_list),
+        slot_blocks=dev64([s // B for s in slot_list]),
+        slot_offsets=dev64([s % B for s in slot_list]),
+        block_ids=[dev64(t) for t in tables],
+        block_ids_cpu=tables,
+        block_tables=torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32, device=device),
+        context_lens_t=torch.tensor(lens, dtype=torch.int32, device=device),
+        last_token_indices=dev64([e - 1 for e in starts[1:]]),
+    )
+
+
+class PagedKVCache:
+    def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int, device: str | torch.device,
+                 dtype: torch.dtype, attn_backend: str = "gather"):
+        """K and V pools of [layers, H_kv, num_blocks, block_size, d]; contents are garbage until written."""
+        if attn_backend not in BACKENDS:
+            raise ValueError(f"attn_backend must be one of {BACKENDS}")
+        self.attn_backend = attn_backend
+        self.cfg, self.num_blocks, self.block_size, self.dtype = cfg, num_blocks, block_size, dtype
+        self.device = torch.device(device)
+        self._allocate((cfg.num_layers, cfg.num_kv_heads, num_blocks, block_size, cfg.head_dim), device, dtype)
+        self.meta: PagedMetadata | None = None
+        self._decode = None
+        self._arange = torch.empty(0, dtype=torch.int64, device=device)
+
+    def _allocate(self, shape: tuple, device: str | torch.device, dtype: torch.dtype) -> None:
+        """K and V pools in the model dtype (the INT8 cache overrides this)."""
+        self.k = torch.empty(shape, device=device, dtype=dtype)
+        self.v = torch.empty(shape, device=device, dtype=dtype)
+
+    @staticmethod
+    def blocks_for_budget(cfg: ModelConfig, budget_bytes: int, block_size: int, bytes_per_elem: int = 2) -> int:
+        """Blocks that fit in budget_bytes (2 GiB -> 10,922 blocks of 16 tokens for 0.5B in bf16)."""
+        return budget_bytes // (block_size * cfg.kv_bytes_per_token(bytes_per_elem))
+
+    @property
+    def on_gpu(self) -> bool:
+        return self.device.type == "cuda"
+
+    def begin(self, n_tokens: int, meta: PagedMetadata | None) -> None:
+        """Start a forward over n_tokens new tokens described by meta."""
+        if meta is None or meta.num_tokens != n_tokens:
+            raise ValueError("a paged forward needs metadata for exactly its tokens")
+        self.meta = meta
+        self._decode = None
+        if self.attn_backend not in KERNEL_BACKENDS:
+            return
+        if not self.on_gpu:
+            raise ValueError(f"attn_backend {self.attn_backend!r} runs the HIP kernel and needs a GPU pool")
+        per_seq = [meta.query_starts[i + 1] - meta.query_starts[i] for i in range(meta.num_seqs)]
+        dec = [i for i, n in enumerate(per_seq) if n == 1]
+        self._prefill = [i for i, n in enumerate(per_seq) if n > 1]
+        if dec:
+            # Once per forward, shared by every layer: the decode rows and their slice of the metadata.
+            if len(dec) == meta.num_seqs:
+                rows, bt, ctx = None, meta.block_tables, meta.context_lens_t
+            else:
+                idx = torch.tensor(dec, device=meta.positions.device)
+                rows, bt, ctx = meta.last_token_indices[idx], meta.block_tables[idx], meta.context_lens_t[idx]
+            self._decode = (rows, bt, ctx, max(meta.context_lens[i] for i in dec))
+            self._decode_seqs = dec
+
+    def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Scatter this forward's k, v [T, H_kv, d] into their slots."""
+        m = self.meta
+        if self.on_gpu:
+            from .hip_quant import store_tokens
+
+            store_tokens(k, m.slot_blocks, m.slot_offsets, self.k[layer], x2=v, pool2=self.v[layer])
+            return
+        self.k[layer][:, m.slot_blocks, m.slot_offsets] = k.transpose(0, 1)
+        self.v[layer][:, m.slot_blocks, m.slot_offsets] = v.transpose(0, 1)
+
+    def gather(self, layer: int, seq: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Sequence seq's K, V as [H_kv, context_len, d] copies."""
+        m, (Hkv, d) = self.meta, (self.cfg.num_kv_heads, self.cfg.head_dim)
+        ctx, blocks = m.context_lens[seq], m.block_ids[seq]
+        k = self.k[layer][:, blocks].view(Hkv, -1, d)[:, :ctx]
+        v = self.v[layer][:, blocks].view(Hkv, -1, d)[:, :ctx]
+        return k, v
+
+    def _key_positions(self, n: int) -> torch.Tensor:
+        if self._arange.numel() < n:
+            self._arange = torch.arange(max(n, 2 * self._arange.numel()), device=self.device)
+        return self._arange[:n]
+
+    def _attend_gather(self, layer: int, i: int, q: torch.Tensor, positions: torch.Tensor,
+                       scale: float) -> torch.Tensor:
+        """Reference attention for sequence i's rows of q over its gathered context."""
+        m = self.meta
+        a, b = m.query_starts[i], m.query_starts[i + 1]
+        k, v = self.gather(layer, i)
+        return attention(q[a:b], k, v, positions[a:b], self._key_positions(m.context_lens[i]), scale)
+
+    def attend(self, layer: int, q: torch.Tensor, positions: torch.Tensor, scale: float) -> torch.Tensor:
+        """Attention of every sequence in the forward over its own context. Returns [T, Hq * d]."""
+        m = self.meta
+        if self._decode is None:
+            outs = [self._attend_gather(layer, i, q, positions, scale) for i in range(m.num_seqs)]
+            return outs[0] if len(outs) == 1 else torch.cat(outs)
+        from .hip_decode import paged_decode_attention
+
+        rows, bt, ctx, max_ctx = self._decode
+        T, Hq, d = q.shape
+        q_dec = q if rows is None else q[rows]
+        dec = paged_decode_attention(q_dec, self.k[layer], self.v[layer], bt, ctx, scale, max_ctx,
+                                     quant=self._kernel_quant(layer))
+        if rows is None:
+            return dec.view(T, Hq * d)
+        out = torch.empty(T, Hq * d, device=q.device, dtype=q.dtype)
+        out[rows] = dec.view(-1, Hq * d)
+        for i in self._prefill:
+            out[m.query_starts[i]:m.query_starts[i + 1]] = self._attend_gather(layer, i, q, positions, scale)
+        return out
+
+    def _kernel_quant(self, layer: int):
+        """Extra kernel inputs of INT8 caches; None for the model-dtype pool."""
+        return None

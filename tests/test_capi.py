@@ -1,0 +1,95 @@
+"""The C-ABI library loads, exports every entry point include/smallinf_hip.h declares, and rejects bad arguments
+on the host before launching anything (no GPU needed)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from engine import _hip
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "smallinf_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(sipa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    names = declared_functions()
+    assert len(names) >= 10, names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert set(names) == set(_hip.SIGNATURES), "the ctypes binding and the header disagree"
+
+
+def test_abi_and_struct_layout():
+    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION
+    # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives.
+    assert ctypes.sizeof(_hip.DecodeParams) == _hip.DecodeParams.workspace_bytes.offset + 8
+
+
+def bad_params(**over):
+    p = _hip.DecodeParams()
+    p.struct_size = ctypes.sizeof(_hip.DecodeParams)
+    p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = 1, 14, 2, 64, 16
+    p.max_context, p.q_dtype, p.scale = 16, _hip.BF16, 0.125
+    for ptr in ("q", "k_cache", "v_cache", "block_tables", "context_lens", "out"):
+        setattr(p, ptr, 4096)
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"struct_size": 8}, _hip.EINVAL),
+    ({"num_q_heads": 13}, _hip.EINVAL),
+    ({"num_q_heads": 34}, _hip.EUNSUPPORTED),          # group 17 > 16
+    ({"head_dim": 96}, _hip.EUNSUPPORTED),
+    ({"block_size": 12}, _hip.EINVAL),                  # must divide 64
+    ({"max_context": 0}, _hip.EINVAL),
+    ({"q_dtype": _hip.F16}, _hip.EUNSUPPORTED),
+    ({"kv_mode": 1}, _hip.EINVAL),                      # INT8 without scales
+    ({"k_cache": 4100}, _hip.EINVAL),                   # unaligned pool
+    ({"out": None}, _hip.EINVAL),
+    ({"max_context": 8192, "num_splits": 16}, _hip.EWORKSPACE),
+])
+def test_decode_rejects_bad_arguments_before_launch(over, code):
+    lib = _hip.lib()
+    rc = lib.sipa_decode(ctypes.byref(bad_params(**over)), None)
+    assert rc == code, lib.sipa_last_error()
+    assert lib.sipa_last_error()
+
+
+def test_zero_sequences_is_a_no_op():
+    assert _hip.lib().sipa_decode(ctypes.byref(bad_params(num_seqs=0)), None) == _hip.OK
+
+
+def test_store_entry_points_reject_bad_arguments():
+    lib = _hip.lib()
+    assert lib.sipa_quantize_store_tokens(4096, _hip.BF16, 128, 64, 4, 2, 48, 4096, 4096, 4096, 1, 1, 16, 4096,
+                                          1, 1, None) == _hip.EUNSUPPORTED
+    assert lib.sipa_quantize_store_tokens(None, _hip.BF16, 128, 64, 0, 2, 64, None, None, None, 1, 1, 16, None, 1,
+                                          1, None) == _hip.OK  # T = 0
+    assert lib.sipa_quantize_store_blocks(4096, _hip.I8, 1, 1, 1, 4096, 4096, 1, 2, 16, 64, 4096, 1, 1, 4096, 1, 1,
+                                          None) == _hip.EUNSUPPORTED
+    assert lib.sipa_store_tokens(4096, 4096, _hip.BF16, 1, 1, None, 3, 2, 64, 4096, 4096, 4096, None, _hip.BF16, 1,
+                                 1, 1, None) == _hip.EINVAL  # x2 without pool2
+
+
+def test_split_policy_host_side():
+    """CU-count split policy: a full grid needs no split; small grids split up to >= 4 workgroups per CU with
+    splits of 256..512 tokens; long contexts are always cut to <= 512-token splits."""
+    lib = _hip.lib()
+    for S, Hkv, ctx in [(1, 2, 8192), (32, 2, 8192), (256, 2, 8192), (64, 2, 4096), (1, 2, 1024), (512, 2, 300)]:
+        req = lib.sipa_choose_splits(S, Hkv, ctx, 256)
+        chunk = lib.sipa_split_chunk(ctx, req)
+        launched = -(-ctx // chunk)
+        assert chunk % 64 == 0 and chunk <= max(512, 64)
+        assert S * Hkv * launched >= min(1024, S * Hkv * -(-ctx // 256)), (S, Hkv, ctx, req, chunk)
+    assert lib.sipa_choose_splits(32, 2, 8192, 256) == 16
+    assert lib.sipa_split_chunk(8192, 16) == 512
+    assert lib.sipa_decode_workspace_bytes(32, 14, 2, 64, 1) == 0

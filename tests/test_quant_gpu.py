@@ -1,0 +1,227 @@
+"""INT8 on the GPU: fused quantize-and-store is bit-exact with the C oracle, and the INT8 decode modes match the
+oracle's dequantize-then-attend.
+
+Mirrors the reference's tests/test_quant_cache.py:221-259 (kernel vs fp64 attention over the cache's own
+dequantized K/V: lengths [1, 15, 16, 17, 33, 100, 700], outlier channels 1 + 5 * (c % 13 == 0), chunked writes
+[37, n - 37], both formats, B 8 / 16 / 32, fp32 / bf16, single / auto splits; tolerances 1e-4 fp32 and 2e-2
+bf16 as there, plus the north-star 8e-3 max-abs for bf16 against the fp32 oracle) and :351-410 (fused writes
+bit-exact, from a strided view with a zero vector, blocks, whole chunked fills).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import HEADS, as_np32
+from engine.block_manager import BlockManager
+from engine.config import ModelConfig
+from engine.hip_decode import paged_decode_attention
+from engine.hip_quant import quantize_store_block_rows, quantize_store_blocks, quantize_store_tokens, store_tokens
+from engine.paged_cache import build_metadata
+from engine.quant_cache import QuantPagedKVCache
+from oracle import paged_ref
+
+pytestmark = pytest.mark.gpu
+FMTS = ["int8", "int8-kchannel"]
+
+
+def bits16(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+# ---- quantize-and-store, bit-exact ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16], ids=["bf16", "fp32", "fp16"])
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_token_quantization_is_exact(dtype, D):
+    """Per-token codes and fp16 scales equal the oracle's, from a strided view, including a zero vector."""
+    g = torch.Generator().manual_seed(0)
+    big = (torch.randn(37, 16, D, generator=g) * 3).to("cuda", dtype)
+    x = big[:, 14:]  # [37, 2, D], row stride 16 * D
+    x[5, 1] = 0
+    N, B = 20, 16
+    blocks = torch.randperm(N, generator=g)[:3].repeat_interleave(B)[:37].cuda()
+    offsets = (torch.arange(37) % B).cuda()
+    qp = torch.zeros(2, N, B, D, dtype=torch.int8, device="cuda")
+    sp = torch.zeros(2, N, B, dtype=torch.float16, device="cuda")
+    print(f"case tokens {dtype} D={D}", flush=True)
+    quantize_store_tokens(x, blocks, offsets, qp, sp)
+    q_ref, s_ref = paged_ref.quantize_per_token(as_np32(x))
+    assert np.array_equal(qp[:, blocks, offsets].transpose(0, 1).cpu().numpy(), q_ref)
+    assert np.array_equal(bits16(sp[:, blocks, offsets].t().cpu().numpy()), bits16(s_ref))
+
+
+def test_token_quantization_edge_values():
+    """Scales that round to zero or to fp16 subnormals, exact .5 ties of x / s, values at the +-127 edge, and
+    absmax near fp16 rounding ties: codes and scales still equal the oracle's."""
+    rows = []
+    rows.append(np.zeros(64, np.float32))                                   # scale 0
+    rows.append(np.full(64, 1e-9, np.float32))                              # absmax/127 underflows fp16
+    rows.append(np.linspace(-7e-4, 7e-4, 64).astype(np.float32))            # subnormal fp16 scale
+    s = np.float32(np.float16(3.0 / 127))                                   # a representable scale
+    ties = (np.arange(64, dtype=np.float32) - 32.0 + 0.5) * s              # x / s lands on .5
+    ties[0] = 127 * s
+    rows.append(ties.astype(np.float32))
+    for k in range(4, 16):                                                  # absmax / 127 near fp16 ties
+        base = np.float32(np.float16(2.0 ** -k)) * 127
+        r = np.random.default_rng(k).standard_normal(64).astype(np.float32) * base / 4
+        r[3] = np.nextafter(base, np.float32(0)) if k % 2 else np.nextafter(base, np.float32(1))
+        rows.append(r)
+    rows.append(np.array([127.0, -127.0, 63.5, -63.5] * 16, np.float32))
+    x_np = np.stack(rows)[:, None, :]  # [T, 1, 64]
+    T = x_np.shape[0]
+    x = torch.from_numpy(x_np).cuda()
+    blocks = torch.arange(T, device="cuda") // 16
+    offsets = torch.arange(T, device="cuda") % 16
+    nb = -(-T // 16)
+    qp = torch.zeros(1, nb, 16, 64, dtype=torch.int8, device="cuda")
+    sp = torch.zeros(1, nb, 16, dtype=torch.float16, device="cuda")
+    quantize_store_tokens(x, blocks, offsets, qp, sp)
+    q_ref, s_ref = paged_ref.quantize_per_token(x_np)
+    assert np.array_equal(qp[:, blocks, offsets].transpose(0, 1).cpu().numpy(), q_ref)
+    assert np.array_equal(bits16(sp[:, blocks, offsets].t().cpu().numpy()), bits16(s_ref))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_block_quantization_is_exact(D):
+    """Per-channel blocks from bf16 staging equal the oracle's codes and channel scales."""
+    g = torch.Generator().manual_seed(1)
+    stage = (torch.randn(2, 8, 16, D, generator=g) * torch.rand(1, 1, 1, D, generator=g) * 4).bfloat16().cuda()
+    src = torch.tensor([3, 0, 6], device="cuda")
+    dst = torch.tensor([11, 2, 7], device="cuda")
+    qp = torch.zeros(2, 12, 16, D, dtype=torch.int8, device="cuda")
+    sp = torch.zeros(2, 12, D, dtype=torch.float16, device="cuda")
+    quantize_store_blocks(stage, src, dst, qp, sp)
+    q_ref, s_ref = paged_ref.quantize_per_channel(as_np32(stage[:, src]), axis=2)
+    assert np.array_equal(qp[:, dst].cpu().numpy(), q_ref)
+    assert np.array_equal(bits16(sp[:, dst].cpu().numpy()), bits16(s_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_block_rows_quantization_is_exact(dtype):
+    """Whole blocks from rows of a forward's K are rounded to bf16, then quantized per channel."""
+    g = torch.Generator().manual_seed(2)
+    B, D = 16, 64
+    x = (torch.randn(48, 2, D, generator=g) * 2).to("cuda", dtype)
+    rows = torch.tensor(list(range(16, 48)), device="cuda")
+    dst = torch.tensor([5, 1], device="cuda")
+    qp = torch.zeros(2, 8, B, D, dtype=torch.int8, device="cuda")
+    sp = torch.zeros(2, 8, D, dtype=torch.float16, device="cuda")
+    quantize_store_block_rows(x, rows, dst, qp, sp)
+    tiles = paged_ref.bf16_round(as_np32(x[16:48])).reshape(2, B, 2, D).transpose(2, 0, 1, 3)  # [H, n, B, D]
+    q_ref, s_ref = paged_ref.quantize_per_channel(tiles, axis=2)
+    assert np.array_equal(qp[:, dst].cpu().numpy(), q_ref)
+    assert np.array_equal(bits16(sp[:, dst].cpu().numpy()), bits16(s_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_store_tokens_is_exact(dtype):
+    """The scatter store writes exactly the values (and the bf16 rounding of fp32 values) into their slots."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(40, 2, 64, generator=g).to("cuda", dtype)
+    y = torch.randn(40, 2, 64, generator=g).to("cuda", dtype)
+    blocks = torch.randperm(30, generator=g)[:40 // 16 + 1].repeat_interleave(16)[:40].cuda()
+    offsets = (torch.arange(40) % 16).cuda()
+    pk = torch.zeros(2, 30, 16, 64, dtype=dtype, device="cuda")
+    pv = torch.zeros_like(pk)
+    store_tokens(x, blocks, offsets, pk, x2=y, pool2=pv)
+    assert torch.equal(pk[:, blocks, offsets], x.transpose(0, 1))
+    assert torch.equal(pv[:, blocks, offsets], y.transpose(0, 1))
+    stage = torch.zeros(2, 4, 16, 64, dtype=torch.bfloat16, device="cuda")
+    rows = torch.tensor([7, 3, 9], device="cuda")
+    store_tokens(x, torch.tensor([2, 2, 0], device="cuda"), torch.tensor([5, 6, 15], device="cuda"), stage,
+                 rows=rows)
+    assert torch.equal(stage[:, [2, 2, 0], [5, 6, 15]], x[rows].transpose(0, 1).bfloat16())
+
+
+# ---- INT8 caches: fused writes and decode ------------------------------------------------------------------------
+
+def make_cache(fmt, num_blocks, B, dtype, cfg):
+    m = BlockManager(num_blocks, B)
+    return m, QuantPagedKVCache(cfg, num_blocks, B, "cuda", dtype, "hip", fmt, m, n_stage=32)
+
+
+def write_chunks(m, cache, seq, k, v, chunks, layer=0):
+    """Append k, v [n, H, d] for `seq` in the given chunk sizes, one forward (begin + write) per chunk."""
+    pos = m.seq_len(seq) if seq in m.seq_ids() else 0
+    if seq not in m.seq_ids():
+        m.allocate(seq, 0)
+    i = 0
+    for n in chunks:
+        m.append_slots(seq, n)
+        meta = build_metadata(m, [(seq, pos, n)], cache.k.device)
+        cache.begin(n, meta)
+        cache.write(layer, k[i:i + n], v[i:i + n])
+        pos, i = pos + n, i + n
+
+
+def tiny_cfg(Hq, Hkv, D):
+    return ModelConfig(vocab_size=10, hidden_size=Hq * D, intermediate_size=16, num_layers=1, num_q_heads=Hq,
+                       num_kv_heads=Hkv, head_dim=D)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_fused_cache_writes_match_reference_cache(fmt):
+    """A chunked fill [5, 40, 1, 1, 30, 1, 5] (partial, interior, single-token, boundary) through the fused HIP
+    writes leaves the same pools as the torch quantizer path (reference tests/test_quant_cache.py:392-410)."""
+    cfg = tiny_cfg(14, 2, 64)
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(83, 2, 64, generator=g).bfloat16().cuda()
+    v = torch.randn(83, 2, 64, generator=g).bfloat16().cuda()
+    pools = []
+    for fused in (False, True):
+        m, cache = make_cache(fmt, 12, 16, torch.bfloat16, cfg)
+        cache.fused_writes = fused
+        write_chunks(m, cache, 0, k, v, [5, 40, 1, 1, 30, 1, 5])
+        torch.cuda.synchronize()
+        pools.append([cache.k.clone(), cache.v.clone(), cache.k_scale.clone(), cache.v_scale.clone()]
+                     + ([cache.stage.clone()] if fmt == "int8-kchannel" else []))
+    for a, b in zip(*pools):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("heads", list(HEADS))
+@pytest.mark.parametrize("B", [8, 16, 32])
+@pytest.mark.parametrize("splits", [1, None], ids=["single", "auto"])
+def test_kernel_matches_dequantized_reference(dtype, fmt, heads, B, splits):
+    """The decode kernel with fused dequantization equals attention over the cache's own dequantized K/V, for a
+    ragged batch with partial last blocks (format B reads them from staging)."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [1, 15, 16, 17, 33, 100, 700]
+    m, cache = make_cache(fmt, sum(-(-n // B) for n in lengths) * 2, B, dtype, tiny_cfg(Hq, Hkv, D))
+    g = torch.Generator().manual_seed(0)
+    for s in range(len(lengths)):
+        m.allocate(s, 0)
+    outlier = 1 + 5 * (torch.arange(D) % 13 == 0)
+    for s, n in enumerate(lengths):
+        k = (torch.randn(n, Hkv, D, generator=g) * outlier).to("cuda", dtype)
+        v = torch.randn(n, Hkv, D, generator=g).to("cuda", dtype)
+        write_chunks(m, cache, s, k, v, [n] if n < 50 else [37, n - 37])
+    meta = build_metadata(m, [(s, n - 1, 1) for s, n in enumerate(lengths)], "cuda")
+    cache.begin(len(lengths), meta)
+    q = torch.randn(len(lengths), Hq, D, generator=g).to("cuda", dtype)
+    print(f"case {fmt} {heads} B={B} {dtype} splits={splits}", flush=True)
+    out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                 max(lengths), num_splits=splits, quant=cache._kernel_quant(0))
+    got = out.double().cpu().numpy()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    # The oracle's fp32 dequantization of the cache's own int8 pools (what the kernel computes with).
+    kq, vq = cache.k[0].cpu().numpy(), cache.v[0].cpu().numpy()
+    ks, vs = cache.k_scale[0].cpu().numpy(), cache.v_scale[0].cpu().numpy()
+    v_deq = paged_ref.dequant_tokens(vq, vs)
+    k_deq = paged_ref.dequant_tokens(kq, ks) if fmt == "int8" else None
+    if fmt == "int8-kchannel":
+        stage, tails = as_np32(cache.stage[0]), cache._tails_dec.cpu().numpy()
+    for s, n in enumerate(lengths):
+        kd, vd = cache.gather(0, s)  # dequantized in the model dtype, as the reference's gather
+        ref64 = paged_ref.attend_one(as_np32(q[s]), as_np32(kd), as_np32(vd), D ** -0.5, np.float64)
+        np.testing.assert_allclose(got[s], ref64, rtol=tol, atol=tol, err_msg=f"sequence {s} (length {n})")
+        if dtype == torch.bfloat16:
+            table = meta.block_ids_cpu[s]
+            k32 = paged_ref.gather(k_deq, table, n) if fmt == "int8" else \
+                paged_ref.gather_kchannel(kq, ks, stage, table, n, int(tails[s]))
+            ref32 = paged_ref.attend_one(as_np32(q[s]), k32, paged_ref.gather(v_deq, table, n), D ** -0.5,
+                                         np.float32)
+            assert np.abs(got[s] - ref32).max() <= 8e-3, f"sequence {s}"
