@@ -1,0 +1,481 @@
+#!/usr/bin/env python3
+"""Paged-decode HBM throughput on one MI355X: the reference's headline kernel benchmark on its named config.
+
+Metric: paged-decode HBM GB/s and fraction of the 8 TB/s peak, and µs per call. Workload (config
+C2): one layer of Qwen2.5-0.5B attention (14 query heads, 2 KV heads, head_dim 64), 16-token blocks, batch 32 x
+8192 context, bf16 N(0, 1) Q/K/V from a fixed seed, block tables a random permutation of a 32768-block pool. A step
+is one paged_decode_attention call over the whole batch (the CU-count split policy with the fused split merge).
+
+Bytes per call are algorithmic: K and V actually read from the pool plus Q and O (512 B per token + 3,584 B per
+sequence for 0.5B); block tables and split partials are not counted. Calls rotate over 8 layers of a
+[8, 2, 32768, 16, 64] pool so each call streams memory the previous calls did not touch (the 256 MB MALL cannot
+serve it). Inputs are resident in HBM before the timed region.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--details/--no-details] [--no-cpu]
+
+Prints one JSON line. `roofline.achieved` divides the bytes by the decode kernel's average duration from HIP
+events around each launch; `cpu_baseline` times the CPU oracle's torch gather-then-attend (fp32) on the same
+inputs on this machine's host cores; `details` holds the other configs (single pass, batch 1, C1, C3, C4 INT8
+modes, the store kernels, the VALU kernel, the read-only streaming ceiling).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "small-inference_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "paged-decode HBM GB/s & % of 8 TB/s peak (B=32, 8k ctx, bf16/INT8); µs/call"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_c2_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---- workloads -------------------------------------------------------------------------------------------------
+
+class Decode:
+    """A paged-decode workload: pools of `layers` layers on the GPU, one DecodePlan, algorithmic bytes per call."""
+
+    def __init__(self, name, q, k, v, bt, ctx_t, lengths, scale, bytes_per_call, splits=None, quant=None,
+                 impl="auto", combine="fused", meta=None):
+        from engine.hip_decode import DecodePlan
+
+        self.name, self.q, self.k, self.v, self.bt, self.ctx_t = name, q, k, v, bt, ctx_t
+        self.lengths, self.scale, self.bytes = lengths, scale, bytes_per_call
+        self.quant = quant  # per-layer list of QuantKV or None
+        self.layers = k.shape[0]
+        self.out = torch.empty_like(q)
+        # One plan per layer, each bound to its layer's pools and scales: a call is one ctypes call + one launch.
+        self.plans = [DecodePlan(q, k[i], v[i], bt, ctx_t, scale, max(lengths), splits,
+                                 None if quant is None else quant[i], impl=impl, combine=combine)
+                      for i in range(self.layers)]
+        self.plan = self.plans[0]
+        self.k_ptrs = [k[i].data_ptr() for i in range(self.layers)]
+        self.v_ptrs = [v[i].data_ptr() for i in range(self.layers)]
+        self.out_ptr = self.out.data_ptr()
+        self.meta = dict(meta or {}, splits=self.plan.splits, chunk=self.plan.chunk, impl=impl, combine=combine)
+
+    def call(self, i: int) -> None:
+        layer = i % self.layers
+        rc = self.plans[layer].launch_raw(self.k_ptrs[layer], self.v_ptrs[layer], self.out_ptr)
+        if rc:
+            from engine import _hip
+            _hip.check(rc, self.name)
+
+
+def time_calls(fn, steps: int, warmup: int, per_launch: bool):
+    """(ms per call over a back-to-back region, mean µs per call from event pairs around each call or None)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    kern_us = None
+    if per_launch:
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            fn(warmup + steps + i)
+            b.record()
+        torch.cuda.synchronize()
+        kern_us = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
+    return ms, kern_us
+
+
+def lifo_tables(num_blocks: int, lengths: list[int], B: int, seed: int) -> list[list[int]]:
+    """Block tables from a fragmented pool: fill it with one-block sequences, free them in a seeded random order,
+    then allocate the sequences (the reference tests' LIFO-scattering pattern)."""
+    from engine.block_manager import BlockManager
+
+    m = BlockManager(num_blocks, B)
+    g = torch.Generator().manual_seed(seed)
+    for s in range(num_blocks):
+        m.allocate(1 << 30 | s, B)
+    for s in torch.randperm(num_blocks, generator=g).tolist():
+        m.free(1 << 30 | s)
+    for i, n in enumerate(lengths):
+        m.allocate(i, n)
+    return [m.block_table(i) for i in range(len(lengths))]
+
+
+def padded(tables: list[list[int]], lengths: list[int], B: int) -> torch.Tensor:
+    cut = [t[:-(-n // B)] for t, n in zip(tables, lengths)]
+    w = max(len(t) for t in cut)
+    return torch.tensor([t + [-1] * (w - len(t)) for t in cut], dtype=torch.int32, device="cuda")
+
+
+def bf16_decode(name, lengths, N, Hq=14, Hkv=2, D=64, B=16, layers=8, seed=0, tables=None, splits=None,
+                impl="auto", combine="fused"):
+    """bf16 pools [layers, Hkv, N, B, D] ~ N(0, 1), q ~ N(0, 1), scale 1/sqrt(D)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    k = torch.randn(layers, Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    v = torch.randn(layers, Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    q = torch.randn(len(lengths), Hq, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    if tables is None:
+        perm = torch.randperm(N, generator=torch.Generator().manual_seed(seed))
+        tables, at = [], 0
+        for n in lengths:
+            nb = -(-n // B)
+            tables.append(perm[at:at + nb].tolist())
+            at += nb
+    bt = padded(tables, lengths, B)
+    ctx_t = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    nbytes = 2 * Hkv * D * 2 * sum(lengths) + 2 * Hq * D * 2 * len(lengths)
+    wl = Decode(name, q, k, v, bt, ctx_t, lengths, D ** -0.5, nbytes, splits, impl=impl, combine=combine,
+                meta={"batch": len(lengths), "context": max(lengths), "pool_blocks": N})
+    wl.tables = tables
+    return wl
+
+
+def measure(wl, steps, warmup, per_launch=True) -> dict:
+    ms, kern_us = time_calls(wl.call, steps, warmup, per_launch)
+    r = {"us_per_call": round(ms * 1e3, 2), "gb_s": round(wl.bytes / (ms * 1e-3) / 1e9, 1),
+         "bytes_per_call": wl.bytes}
+    if kern_us is not None:
+        r["kernel_us"] = round(kern_us, 2)
+        r["kernel_gb_s"] = round(wl.bytes / (kern_us * 1e-6) / 1e9, 1)
+        r["frac_of_peak"] = round(r["kernel_gb_s"] / PEAK_GBS, 4)
+    r.update(wl.meta)
+    log(f"[bench] {wl.name}: {json.dumps(r)}")
+    return r
+
+
+def check_against_oracle(wl, layer=0, max_seqs=32) -> float:
+    """Max-abs error of the GPU output for `layer` against the oracle's fp32 gather-then-attend (first seqs)."""
+    import numpy as np
+    from oracle import paged_ref
+
+    wl.call(layer)  # rotation index == layer for the first `layers` calls
+    torch.cuda.synchronize()
+    got = wl.out.float().cpu().numpy()
+    S = min(max_seqs, len(wl.lengths))
+    err = 0.0
+    for s in range(S):
+        n, t = wl.lengths[s], wl.tables[s]
+        idx = torch.tensor(t[:-(-n // wl.k.shape[3])], device="cuda")
+        kk = wl.k[layer].index_select(1, idx).float().cpu().numpy()
+        vv = wl.v[layer].index_select(1, idx).float().cpu().numpy()
+        ref = paged_ref.attend_one(wl.q[s].float().cpu().numpy(), kk.reshape(kk.shape[0], -1, kk.shape[-1])[:, :n],
+                                   vv.reshape(vv.shape[0], -1, vv.shape[-1])[:, :n], wl.scale, np.float32)
+        err = max(err, float(np.abs(got[s] - ref).max()))
+    return err
+
+
+def cpu_baseline(wl, budget_s: float) -> dict:
+    """The CPU oracle's torch fp32 gather-then-attend on the same inputs (layer 0), on the host cores."""
+    from oracle import paged_ref
+
+    threads = torch.get_num_threads()
+    B = wl.k.shape[3]
+    used = sorted({b for t, n in zip(wl.tables, wl.lengths) for b in t[:-(-n // B)]})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.int64, device="cuda")
+    k_cpu = wl.k[0].index_select(1, idx).cpu()
+    v_cpu = wl.v[0].index_select(1, idx).cpu()
+    tables = [[remap[b] for b in t[:-(-n // B)]] for t, n in zip(wl.tables, wl.lengths)]
+    bt = torch.tensor([t + [-1] * (max(map(len, tables)) - len(t)) for t in tables], dtype=torch.int64)
+    q_cpu = wl.q.cpu()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    out = None
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        out = paged_ref.decode_torch_cpu(q_cpu, k_cpu, v_cpu, bt, wl.lengths, wl.scale)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    wl.call(0)
+    torch.cuda.synchronize()
+    err = float((wl.out.float().cpu() - out).abs().max())
+    r = {"value": round(wl.bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+         "us_per_call": round(med * 1e6, 1), "reps": len(times), "max_abs_vs_gpu": round(err, 5),
+         "sample": f"the full C2 batch ({len(wl.lengths)} x {max(wl.lengths)}), layer 0, oracle/paged_ref.py "
+                   f"decode_torch_cpu (fp32 gather-then-attend, torch {threads} threads), median of {len(times)}"}
+    log(f"[bench] cpu_baseline: {json.dumps(r)}")
+    return r
+
+
+# ---- detail workloads ----------------------------------------------------------------------------------------------
+
+def int8_decode(name, fmt, lengths, N, Hq=12, Hkv=2, D=128, B=16, layers=4, seed=0, impl="auto",
+                f32_channel_scales=False):
+    """1.5B-shaped INT8 pools built by the HIP quantize-and-store kernels from bf16 K ~ N(0, 1) with 4 of 128
+    channels per head scaled by U[20, 68] and V ~ N(0, 1) (config C4)."""
+    from engine.hip_decode import QuantKV
+    from engine.hip_quant import quantize_store_blocks, quantize_store_tokens
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    cpu_g = torch.Generator().manual_seed(seed)
+    kq = torch.empty(layers, Hkv, N, B, D, dtype=torch.int8, device="cuda")
+    vq = torch.empty_like(kq)
+    vs = torch.empty(layers, Hkv, N, B, dtype=torch.float16, device="cuda")
+    ks = torch.empty(layers, Hkv, N, B if fmt == "int8" else D, dtype=torch.float16, device="cuda")
+    tok_blocks = torch.arange(N * B, device="cuda") // B
+    tok_offs = torch.arange(N * B, device="cuda") % B
+    for layer in range(layers):
+        chan_scale = torch.ones(Hkv, 1, 1, D)
+        for h in range(Hkv):
+            ch = torch.randperm(D, generator=cpu_g)[:4]
+            chan_scale[h, 0, 0, ch] = 20 + 48 * torch.rand(4, generator=cpu_g)
+        kb = (torch.randn(Hkv, N, B, D, device="cuda", generator=g) * chan_scale.cuda()).bfloat16()
+        vb = torch.randn(Hkv, N, B, D, device="cuda", generator=g).bfloat16()
+        as_tokens = lambda x: x.permute(1, 2, 0, 3).reshape(N * B, Hkv, D)  # noqa: E731  (a strided view)
+        quantize_store_tokens(as_tokens(vb), tok_blocks, tok_offs, vq[layer], vs[layer])
+        if fmt == "int8":
+            quantize_store_tokens(as_tokens(kb), tok_blocks, tok_offs, kq[layer], ks[layer])
+        else:
+            ids = torch.arange(N, device="cuda")
+            quantize_store_blocks(kb, ids, ids, kq[layer], ks[layer])
+        del kb, vb
+    q = torch.randn(len(lengths), Hq, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    perm = torch.randperm(N, generator=cpu_g)
+    tables, at = [], 0
+    for n in lengths:
+        nb = -(-n // B)
+        tables.append(perm[at:at + nb].tolist())
+        at += nb
+    bt = padded(tables, lengths, B)
+    ctx_t = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    if fmt == "int8":
+        quant = [QuantKV(1, ks[i], vs[i]) for i in range(layers)]
+        per_token = 2 * Hkv * (D + 2)
+    else:
+        stage = torch.zeros(Hkv, 4, B, D, dtype=torch.bfloat16, device="cuda")
+        tails = torch.full((len(lengths),), -1, dtype=torch.int32, device="cuda")  # 4096 is block-aligned
+        if f32_channel_scales:  # the literal reading of C4(a): one fp32 scale per (head, channel), block stride 0
+            kscale = [ks[i][:, :1].float().expand(Hkv, N, D) for i in range(layers)]
+        else:
+            kscale = [ks[i] for i in range(layers)]
+        quant = [QuantKV(2, kscale[i], vs[i], stage, tails) for i in range(layers)]
+        per_token = Hkv * (D + 2) + Hkv * (D + 2 * D / B)
+    nbytes = int(per_token * sum(lengths)) + 2 * Hq * D * 2 * len(lengths)
+    wl = Decode(name, q, kq, vq, bt, ctx_t, lengths, D ** -0.5, nbytes, None, quant, impl=impl,
+                meta={"batch": len(lengths), "context": max(lengths), "format": fmt,
+                      "k_scales": "fp32 per (head, channel)" if f32_channel_scales else "fp16 per (block, channel)"
+                      if fmt != "int8" else "fp16 per token"})
+    wl.tables = tables
+    return wl
+
+
+def store_bench(steps: int) -> dict:
+    """C3's bf16 store of one new K/V token for each of 256 sequences, and C4's INT8 quantize-and-store of 64 new
+    tokens (K and V, 1.5B), with the C4 codes checked bit-exact against the C oracle."""
+    import numpy as np
+    from engine.hip_quant import quantize_store_tokens, store_tokens
+    from oracle import paged_ref
+
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(7)
+    # C3: 256 tokens of [2, 64] bf16 K and V into partially filled last blocks of a 200k-block pool
+    N = 200_000
+    pk = torch.zeros(2, N, 16, 64, dtype=torch.bfloat16, device="cuda")
+    pv = torch.zeros_like(pk)
+    x = torch.randn(256, 2, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    y = torch.randn(256, 2, 64, device="cuda", dtype=torch.bfloat16, generator=g)
+    blocks = torch.randperm(N, generator=torch.Generator().manual_seed(7))[:256].cuda()
+    offs = torch.randint(1, 16, (256,), generator=torch.Generator().manual_seed(8)).cuda()
+    ms, kus = time_calls(lambda i: store_tokens(x, blocks, offs, pk, x2=y, pool2=pv), steps, 20, True)
+    ok = bool(torch.equal(pk[:, blocks, offs], x.transpose(0, 1)) and torch.equal(pv[:, blocks, offs],
+                                                                                  y.transpose(0, 1)))
+    res["c3_store_bf16"] = {"us_per_call": round(ms * 1e3, 2), "kernel_us": round(kus, 2), "tokens": 256,
+                            "bytes_per_call": 4 * 256 * 2 * 64 * 2, "exact": ok}
+    # C4: 64 new tokens, K and V [64, 2, 128] bf16, per-token INT8 into a 32768-block pool
+    N = 32768
+    qk = torch.zeros(2, N, 16, 128, dtype=torch.int8, device="cuda")
+    qv = torch.zeros_like(qk)
+    sk = torch.zeros(2, N, 16, dtype=torch.float16, device="cuda")
+    sv = torch.zeros_like(sk)
+    kx = (torch.randn(64, 2, 128, device="cuda", generator=g) * 3).bfloat16()
+    vx = torch.randn(64, 2, 128, device="cuda", generator=g).bfloat16()
+    blocks = torch.randperm(N, generator=torch.Generator().manual_seed(9))[:64].cuda()
+    offs = torch.randint(0, 16, (64,), generator=torch.Generator().manual_seed(10)).cuda()
+
+    def qs(i):
+        quantize_store_tokens(kx, blocks, offs, qk, sk)
+        quantize_store_tokens(vx, blocks, offs, qv, sv)
+
+    ms, kus = time_calls(qs, steps, 20, True)
+    exact = True
+    for xx, qq, ss in ((kx, qk, sk), (vx, qv, sv)):
+        q_ref, s_ref = paged_ref.quantize_per_token(xx.float().cpu().numpy())
+        exact &= bool(np.array_equal(qq[:, blocks, offs].transpose(0, 1).cpu().numpy(), q_ref))
+        exact &= bool(np.array_equal(ss[:, blocks, offs].t().cpu().numpy().view(np.uint16), s_ref.view(np.uint16)))
+    res["c4_quantize_store_64"] = {"us_per_call": round(ms * 1e3, 2), "kernel_us_2_launches": round(kus, 2),
+                                   "tokens": 64, "bit_exact_vs_oracle": exact,
+                                   "bytes_per_call": 2 * (64 * 2 * 128 * 2 + 64 * 2 * 128 + 64 * 2 * 2)}
+    log(f"[bench] stores: {json.dumps(res)}")
+    return res
+
+
+def stream_ceiling(steps: int) -> dict:
+    """Read-only streaming ceiling of this GPU from the probe library (1 GiB buffers, 4 rotating)."""
+    lib = ctypes.CDLL(str(ROOT / "small-inference_amd" / "build" / "libsmallinf_probe.so"))
+    lib.sipa_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
+                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    nbytes = 1 << 30
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    best, sweep = {}, []
+    for wgs in (256, 512, 1024, 2048, 4096):
+        for unroll in (4, 8, 16):
+            for nt in (0, 1):
+                def rd(i, wgs=wgs, unroll=unroll, nt=nt):
+                    if lib.sipa_probe_read(bufs[i % 4].data_ptr(), nbytes, sink.data_ptr(), wgs, unroll, nt,
+                                           stream):
+                        raise RuntimeError("probe read launch failed")
+                ms, kus = time_calls(rd, max(8, steps // 20), 4, True)
+                gbs = nbytes / (kus * 1e-6) / 1e9
+                sweep.append((wgs, unroll, nt, round(gbs, 1)))
+                if gbs > best.get("gb_s", 0):
+                    best = {"gb_s": round(gbs, 1), "workgroups": wgs, "loads_in_flight_per_lane": unroll,
+                            "nontemporal": nt, "bytes": nbytes, "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    best["sweep"] = sweep
+    log(f"[bench] stream ceiling: {json.dumps(best)}")
+    del bufs
+    return best
+
+
+def details(steps: int, warmup: int) -> dict:
+    import numpy as np
+
+    out = {}
+    c2 = bf16_decode("c2_single_pass", [8192] * 32, 32768, splits=1)
+    out["c2_single_pass"] = measure(c2, steps, warmup)
+    out["c2_single_pass"]["max_abs_vs_oracle"] = round(check_against_oracle(c2), 5)
+    out["c2_separate_combine"] = measure(bf16_decode("c2_separate_combine", [8192] * 32, 32768, combine="kernel"),
+                                         steps, warmup)
+    out["c2_valu"] = measure(bf16_decode("c2_valu", [8192] * 32, 32768, impl="valu"), steps // 2, warmup)
+    del c2
+    torch.cuda.empty_cache()
+    for splits, label in ((1, "single_pass"), (None, "split")):
+        out[f"c2_batch1_{label}"] = measure(bf16_decode(f"c2_batch1_{label}", [8192], 8192, layers=64,
+                                                        splits=splits), steps, warmup)
+    c1_lengths = [1024]
+    c1 = bf16_decode("c1", c1_lengths, 4096, layers=64, tables=lifo_tables(4096, c1_lengths, 16, 0))
+    c1.scale = 1 / 8
+    out["c1_1x1024"] = measure(c1, steps, warmup)
+    out["c1_1x1024"]["max_abs_vs_oracle"] = round(check_against_oracle(c1), 5)
+    rng = np.random.default_rng(0)
+    c3_lengths = np.clip(np.rint(rng.lognormal(math.log(600), 1.0, 256)), 16, 8192).astype(int).tolist()
+    c3 = bf16_decode("c3_ragged256", c3_lengths, 200_000, layers=4)
+    out["c3_ragged256"] = measure(c3, steps, warmup)
+    out["c3_ragged256"]["sum_context"] = int(sum(c3_lengths))
+    out["c3_ragged256"]["max_abs_vs_oracle_first32"] = round(check_against_oracle(c3), 5)
+    del c3
+    torch.cuda.empty_cache()
+    c4_lengths = [4096] * 64
+    for fmt, f32s, key in (("int8", False, "c4b_int8_per_token"), ("int8-kchannel", False, "c4a_int8_kchannel"),
+                           ("int8-kchannel", True, "c4a_int8_kchannel_f32_head_channel_scales")):
+        wl = int8_decode(key, fmt, c4_lengths, 32768, f32_channel_scales=f32s)
+        out[key] = measure(wl, steps, warmup)
+        del wl
+        torch.cuda.empty_cache()
+    out.update(store_bench(steps))
+    out["stream_read_ceiling"] = stream_ceiling(steps)
+    return out
+
+
+# ---- main ------------------------------------------------------------------------------------------------------------
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--layers", type=int, default=8, help="pool layers the calls rotate over (defeats the MALL)")
+    ap.add_argument("--splits", type=int, default=None, help="force a split count (default: CU-count policy)")
+    ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "valu"])
+    ap.add_argument("--combine", default="fused", choices=["fused", "kernel"])
+    ap.add_argument("--details", dest="details", action="store_true", default=True)
+    ap.add_argument("--no-details", dest="details", action="store_false")
+    ap.add_argument("--no-cpu", dest="cpu", action="store_false", default=True)
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build runs the paged-decode kernels on a single MI355X and has no "
+              f"multi-GPU path (asked for --gpus {args.gpus}, WORLD_SIZE {world}). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    from engine.hip_decode import device_cu_count
+
+    cu = device_cu_count()
+    log(f"[bench] device {torch.cuda.get_device_name(0)}, {cu} CUs")
+
+    wl = bf16_decode("c2", [8192] * 32, 32768, layers=args.layers, splits=args.splits, impl=args.impl,
+                     combine=args.combine)
+    ms, _ = time_calls(wl.call, args.steps, args.warmup, per_launch=False)
+    _, kern_us = time_calls(wl.call, args.steps, 0, per_launch=True)
+    value = wl.bytes / (ms * 1e-3) / 1e9
+    achieved = wl.bytes / (kern_us * 1e-6) / 1e9
+    err = check_against_oracle(wl)
+    log(f"[bench] c2: {ms * 1e3:.2f} us/call region, {kern_us:.2f} us/launch events, {value:.1f} GB/s, "
+        f"max-abs vs oracle {err:.2e}, splits {wl.plan.splits} x {wl.plan.chunk} tokens")
+
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, random-permutation block tables)",
+        "config": {"workload": "C2: bf16 paged decode, batch 32 x 8192 context, Qwen2.5-0.5B attention shape "
+                               "(14 q / 2 kv heads, head_dim 64), 16-token blocks, 32768-block pool",
+                   "batch": 32, "context": 8192, "block_size": 16, "q_heads": 14, "kv_heads": 2, "head_dim": 64,
+                   "splits": wl.plan.splits, "split_tokens": wl.plan.chunk, "impl": args.impl,
+                   "combine": args.combine, "layers_rotated": args.layers, "cu_count": cu,
+                   "bytes_per_call": wl.bytes, "us_per_call": round(ms * 1e3, 2),
+                   "max_abs_vs_fp32_oracle": round(err, 5)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                     "kernel_us": round(kern_us, 2), "kernel": "sipa::decode_mfma_bf16<64>"
+                     if args.impl != "valu" else "sipa::decode_valu<1,0,64>"},
+    }
+    if args.cpu:
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
+    del wl
+    torch.cuda.empty_cache()
+    if args.details:
+        result["details"] = details(max(50, args.steps // 2), max(10, args.warmup // 2))
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -18,6 +18,8 @@ CSRC = PKG / "csrc"
 OUT_DIR = PKG / "build"
 LIB = OUT_DIR / "libsmallinf_hip.so"
 SOURCES = ["capi.hip", "decode.hip", "quant_store.hip"]
+PROBE_LIB = OUT_DIR / "libsmallinf_probe.so"  # measurement kernels for bench.py, outside the product ABI
+PROBE_SOURCES = ["probe.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_fma_f32 and kin); the kernels are written
@@ -34,20 +36,28 @@ def hipcc() -> str:
     return shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library; returns its path. Always recompiles."""
-    OUT_DIR.mkdir(exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-I", str(ROOT / "include"), *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+def _compile(sources: list[str], out: Path, verbose: bool) -> Path:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, "-I", str(ROOT / "include"), *[str(CSRC / s) for s in sources], "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
-    if verbose and proc.stderr.strip():
-        print(proc.stderr, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    # The host pass does not know the packed-fp32 feature flag and says so once per file; nothing else to show.
+    notes = [ln for ln in proc.stderr.splitlines() if ln.strip() and "packed-fp32-ops" not in ln]
+    if verbose and notes:
+        print("\n".join(notes), file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the decode-path library (and the bench's probe library); returns the main library's path.
+    Always recompiles."""
+    OUT_DIR.mkdir(exist_ok=True)
+    _compile(PROBE_SOURCES, PROBE_LIB, verbose)
+    return _compile(SOURCES, LIB, verbose)
 
 
 if __name__ == "__main__":

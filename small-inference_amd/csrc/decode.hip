@@ -37,6 +37,7 @@
 // as the reference uses for fp32 caches (engine/triton_decode.py:208-210).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "sipa_common.h"
@@ -44,6 +45,7 @@
 namespace sipa {
 
 constexpr float kNegInf = -__builtin_huge_valf();
+constexpr int kMaxSplitBlocks = 2048;  // block ids of one split the MFMA kernel stages in LDS (32768 tokens)
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -65,6 +67,19 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// The grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware hands workgroup L
+// to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads evenly over
+// them; and every sequence's first split (the only one a short sequence has) is dispatched before any second one.
+struct WorkItem {
+  int s, h, sp;
+};
+
+__device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
+  const int L = blockIdx.x;
+  const int sh = L % (a.S * a.Hkv);
+  return WorkItem{sh % a.S, sh / a.S, L / (a.S * a.Hkv)};
+}
+
 template <bool OUT_F32>
 __device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, int d, float v) {
   const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d;
@@ -74,20 +89,54 @@ __device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, in
     ((uint16_t*)a.out)[i] = f32_to_bf16_bits(v);
 }
 
-// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G).
-template <int D, bool OUT_F32>
+// Partials that another workgroup of the same launch merges are written and read with agent-scope atomic
+// accesses: on gfx950 these are global_store / global_load with the sc1 bit, which write through to and read from
+// the point of coherence of all XCDs. Ordering then needs only the completion of this workgroup's stores
+// (s_waitcnt vmcnt(0)) before its counter increment, not an agent-scope fence, which would write back and
+// invalidate the whole L2 of the XCD once per workgroup.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). COHERENT: the
+// partials were written by other workgroups of this launch (the fused merge). Up to 8 splits are loaded per
+// round (one memory round trip) and merged online, so the usual 2..8 splits cost a single round trip.
+template <int D, bool OUT_F32, bool COHERENT>
 __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
+  constexpr int kBatch = 8;
   const int G = a.G;
+  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
   for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
     const int g = idx / D, d = idx % D;
     const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
-    float M = kNegInf;
-    for (int j = 0; j < nvalid; ++j) M = fmaxf(M, a.pm[row0 + j]);
-    float num = 0.f, den = 0.f;
-    for (int j = 0; j < nvalid; ++j) {
-      const float w = fast_exp2(a.pm[row0 + j] - M);
-      num += w * a.part[(row0 + j) * D + d];
-      den += w * a.pl[row0 + j];
+    float M = kNegInf, num = 0.f, den = 0.f;
+    for (int j0 = 0; j0 < nvalid; j0 += kBatch) {
+      float mj[kBatch], lj[kBatch], pj[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = j0 + u;
+        const bool ok = j < nvalid;
+        mj[u] = ok ? ld(a.pm + row0 + j) : kNegInf;
+        lj[u] = ok ? ld(a.pl + row0 + j) : 0.f;
+        pj[u] = ok ? ld(a.part + (row0 + j) * D + d) : 0.f;
+      }
+      float mb = M;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mj[u]);
+      const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf)
+      num *= rescale;
+      den *= rescale;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float w = fast_exp2(mj[u] - mb);  // 0 for the padding entries (m = -inf)
+        num += w * pj[u];
+        den += w * lj[u];
+      }
+      M = mb;
     }
     store_out<OUT_F32>(a, s, h * G + g, d, num / den);
   }
@@ -117,29 +166,41 @@ __device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nval
       store_out<OUT_F32>(a, s, h * G + g, d, O / L);
     } else {
       const int64_t row = ((int64_t)s * a.Hq + h * G + g) * a.splits + sp;
-      a.part[row * D + d] = O;
-      if (d == 0) {
-        a.pm[row] = M;
-        a.pl[row] = L;
+      if (a.fused) {
+        store_coherent(a.part + row * D + d, O);
+        if (d == 0) {
+          store_coherent(a.pm + row, M);
+          store_coherent(a.pl + row, L);
+        }
+      } else {
+        a.part[row * D + d] = O;
+        if (d == 0) {
+          a.pm[row] = M;
+          a.pl[row] = L;
+        }
       }
     }
   }
   if (nvalid == 1 || !a.fused) return;
-  // Release this split's partial, count it, and let the last arriving split merge (acquire the others').
-  __threadfence();
+  // This workgroup's partial has reached the coherence point once its stores complete; then count it. The
+  // workgroup that brings the count to nvalid merges every partial of (s, h) and resets the counter.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = atomicAdd(a.counters + (int64_t)s * a.Hkv + h, 1);
+    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
     *last_flag = (prev == nvalid - 1);
   }
   __syncthreads();
   if (!*last_flag) return;
-  __threadfence();
-  combine_group<D, OUT_F32>(a, s, h, nvalid);
-  if (threadIdx.x == 0) a.counters[(int64_t)s * a.Hkv + h] = 0;  // ready for the next call
+  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- MFMA kernel: bf16, B = 16 ---------------------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
 struct MfmaSmem {
@@ -149,7 +210,17 @@ struct MfmaSmem {
   static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
 };
 
+// K/V are streamed once per call: nontemporal loads keep them from displacing anything in the caches.
+__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+
+// One 32-token tile (two blocks) of K and V in registers: K in the QK A-operand layout, V as 16-byte row chunks.
 template <int D>
+struct KVTile {
+  u32x4 k[2][D / 32];
+  u32x4 v[2][D / 32];
+};
+
+template <int D, int NB>  // NB: tiles in flight per wave (the register prefetch ring)
 __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a) {
   constexpr int KS = D / 32;  // QK k-steps per block
   constexpr int DT = D / 16;  // PV d-tiles
@@ -157,82 +228,100 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   constexpr int VP = MfmaSmem<D>::kVPitch;
   constexpr int CPR = D / 8;  // 16-byte chunks per token row
   __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
+  __shared__ int bids[kMaxSplitBlocks];  // this split's block ids
   __shared__ int last_flag;
 
-  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
-  const int ctx = a.ctx[s];
+  const WorkItem w = work_item(a);
+  const int sp = w.sp, h = w.h, s = w.s;
   const int start = sp * a.chunk;
-  if (start >= ctx) return;
-  const int end = min(start + a.chunk, ctx);
-  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
   const int G = a.G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
+  // Block ids, the query group and the context length are loaded together: the ids are fetched for the
+  // longest possible split (every table row covers max_ctx tokens) before ctx[s] is known, so the first K/V
+  // loads wait for one memory round trip instead of two.
+  constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
+  const int nb_spec = (min(a.chunk, a.max_ctx - start) + 15) >> 4;
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
+  int ids[kIdsPerThread];
+#pragma unroll
+  for (int i = 0; i < kIdsPerThread; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    ids[i] = (j < nb_spec) ? btr[j] : 0;
+  }
   bf16x8 qop[KS];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      uint4 u = *(const uint4*)(qrow + 32 * j + 8 * q4);
-      if (r >= G) u = make_uint4(0, 0, 0, 0);
+      u32x4 u = *(const u32x4*)(qrow + 32 * j + 8 * q4);
+      if (r >= G) u = u32x4{0, 0, 0, 0};
       qop[j] = __builtin_bit_cast(bf16x8, u);
     }
   }
+  const int ctx = a.ctx[s];
+  if (start >= ctx) return;
+  const int end = min(start + a.chunk, ctx);
+  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+#pragma unroll
+  for (int i = 0; i < kIdsPerThread; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    if (j < nb_spec) bids[j] = ids[i];
+  }
+  __syncthreads();  // block ids staged
 
   const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
   const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
-  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
   uint16_t* vw = (uint16_t*)smem + wave * 32 * VP;
+  const int ntile = (end - start + 31) >> 5;
+  const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;  // tiles wave, wave + 4, ...
+
+  auto tile_t0 = [&](int k) { return start + 32 * (wave + kWaves * k); };
+  // Branch-free: a tile's second block past the split's end re-reads the first block (its rows are masked), so
+  // the number of loads in flight is the same on every path and the compiler's wait counts can leave the
+  // other ring slots outstanding.
+  auto load_tile = [&](int k, KVTile<D>& tl) {
+    const int t0 = tile_t0(k);
+    const int bi = (t0 - start) >> 4;
+    const int b0 = bids[bi];
+    const int b1 = (t0 + 16 < end) ? bids[bi + 1] : b0;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int blk = mt ? b1 : b0;
+      const uint16_t* kb = kh + (int64_t)blk * a.kv_sn;
+      const uint16_t* vb = vh + (int64_t)blk * a.kv_sn;
+#pragma unroll
+      for (int j = 0; j < KS; ++j) tl.k[mt][j] = stream_load(kb + r * D + 32 * j + 8 * q4);
+#pragma unroll
+      for (int i = 0; i < VC; ++i) tl.v[mt][i] = stream_load(vb + 8 * (lane + 64 * i));
+    }
+  };
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 kc[2][KS], vc[2][VC], kn[2][KS], vn[2][VC];
-
-  auto load_tile = [&](int t0, uint4(&kr)[2][KS], uint4(&vr)[2][VC]) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int tb = t0 + 16 * mt;
-      if (tb < end) {
-        const int blk = btr[tb >> 4];
-        const uint16_t* kb = kh + (int64_t)blk * a.kv_sn;
-        const uint4* vb = (const uint4*)(vh + (int64_t)blk * a.kv_sn);
-#pragma unroll
-        for (int j = 0; j < KS; ++j) kr[mt][j] = *(const uint4*)(kb + r * D + 32 * j + 8 * q4);
-#pragma unroll
-        for (int i = 0; i < VC; ++i) vr[mt][i] = vb[lane + 64 * i];
-      } else {
-#pragma unroll
-        for (int j = 0; j < KS; ++j) kr[mt][j] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < VC; ++i) vr[mt][i] = make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-
-  int t0 = start + 32 * wave;
-  if (t0 < end) load_tile(t0, kc, vc);
-  for (; t0 < end; t0 += 32 * kWaves) {
-    const int tn = t0 + 32 * kWaves;
-    if (tn < end) load_tile(tn, kn, vn);
-
-    // V rows at or past the end of this split are masked (zero) so that 0-weight garbage cannot give NaN.
-    if (t0 + 32 > end) {
+  // Online softmax with a lazily updated max: scores are exponentiated against m_run, which is raised (and acc, l
+  // rescaled) only when some head's tile max exceeds it by more than 2^8; until then p <= 256, which fp32 acc/l
+  // and bf16 P hold without loss of relative precision, and the final acc / l is unchanged.
+  constexpr float kRescaleSlack = 8.f;
+  auto process_tile = [&](int t0, KVTile<D>& tl) {
+    const bool partial = t0 + 32 > end;  // wave-uniform
+    if (partial) {  // V rows at or past the end are zeroed so that 0-weight garbage cannot give NaN
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < VC; ++i)
-          if (t0 + 16 * mt + (lane + 64 * i) / CPR >= end) vc[mt][i] = make_uint4(0, 0, 0, 0);
+          if (t0 + 16 * mt + (lane + 64 * i) / CPR >= end) tl.v[mt][i] = u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < VC; ++i) {
         const int c = lane + 64 * i;
-        *(uint4*)(vw + (16 * mt + c / CPR) * VP + (c % CPR) * 8) = vc[mt][i];
+        *(u32x4*)(vw + (16 * mt + c / CPR) * VP + (c % CPR) * 8) = tl.v[mt][i];
       }
 
     f32x4 sc[2];
@@ -241,34 +330,38 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
       sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KS; ++j)
-        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kc[mt][j]), qop[j], sc[mt], 0,
+        sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tl.k[mt][j]), qop[j], sc[mt], 0,
                                                          0, 0);
     }
-    float mx = kNegInf;
+    if (partial) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 16 * mt + 4 * q4 + i;
-        sc[mt][i] = (t < end) ? sc[mt][i] * a.scale_log2 : kNegInf;
-        mx = fmaxf(mx, sc[mt][i]);
-      }
+        for (int i = 0; i < 4; ++i)
+          if (t0 + 16 * mt + 4 * q4 + i >= end) sc[mt][i] = kNegInf;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
+    mx *= a.scale_log2;  // raw scores -> exp2 domain (scale > 0 keeps the order)
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {  // rare after the first tile
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
     bf16x8 pop;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float p = fast_exp2(sc[i >> 2][i & 3] - m_new);
+      const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_run));
       psum += p;
       pop[i] = (__bf16)p;
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+    l_run += psum;
 
     wave_sync();  // the wave's V tile is in LDS
 #pragma unroll
@@ -280,13 +373,35 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[dt], 0, 0, 0);
     }
     wave_sync();  // reads done before the next tile overwrites the LDS tile
+  };
 
+  KVTile<D> ring[NB];
+  if (mine >= 2 * NB) {
+    // Pipelined: NB tiles in flight; in the steady state every consumed slot is refilled unconditionally.
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int j = 0; j < NB; ++j) load_tile(j, ring[j]);
+    int k0 = 0;
+    for (; k0 + 2 * NB <= mine; k0 += NB) {
 #pragma unroll
-      for (int j = 0; j < KS; ++j) kc[mt][j] = kn[mt][j];
+      for (int j = 0; j < NB; ++j) {
+        process_tile(tile_t0(k0 + j), ring[j]);
+        load_tile(k0 + j + NB, ring[j]);
+      }
+    }
+    // Drain: tiles k0 .. k0 + NB - 1 are loaded, fewer than NB more remain.
 #pragma unroll
-      for (int i = 0; i < VC; ++i) vc[mt][i] = vn[mt][i];
+    for (int j = 0; j < NB; ++j) {
+      process_tile(tile_t0(k0 + j), ring[j]);
+      if (k0 + j + NB < mine) load_tile(k0 + j + NB, ring[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      if (k0 + NB + j < mine) process_tile(tile_t0(k0 + NB + j), ring[j]);
+  } else {
+    // Short split: one tile at a time.
+    for (int k = 0; k < mine; ++k) {
+      load_tile(k, ring[0]);
+      process_tile(tile_t0(k), ring[0]);
     }
   }
 
@@ -353,7 +468,8 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
   __shared__ __align__(16) char smem[ValuSmem<D>::kBytes];
   __shared__ int last_flag;
 
-  const int sp = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const WorkItem w = work_item(a);
+  const int sp = w.sp, h = w.h, s = w.s;
   const int ctx = a.ctx[s];
   const int start = sp * a.chunk;
   if (start >= ctx) return;
@@ -507,7 +623,7 @@ __global__ void __launch_bounds__(kThreads) combine_splits(const DecodeArgs a) {
   const int h = blockIdx.x, s = blockIdx.y;
   const int nvalid = (a.ctx[s] + a.chunk - 1) / a.chunk;
   if (nvalid <= 1) return;  // the single split wrote the output itself
-  combine_group<D, OUT_F32>(a, s, h, nvalid);
+  combine_group<D, OUT_F32, false>(a, s, h, nvalid);
 }
 
 // ---- host side --------------------------------------------------------------------------------------------------
@@ -530,12 +646,15 @@ static WorkspaceLayout workspace_layout(int64_t S, int64_t Hq, int64_t Hkv, int6
 
 static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+// About one workgroup per CU: each workgroup pays a fixed cost of two dependent memory round trips before its
+// first tile and the split merge after its last, so a few long-running workgroups beat many short ones (measured
+// on MI355X, bf16 32 x 8192: 4 splits 27.9 us, 8 splits 29.2 us, 16 splits 44.6 us). Splits stay within
+// [kMinChunk, kMaxChunk] tokens; the cap spreads a long sequence of a ragged batch over several CUs.
 int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count) {
   if (S <= 0 || Hkv <= 0 || max_ctx <= 0) return 1;
   if (cu_count <= 0) cu_count = 256;
   const int64_t programs = (int64_t)S * Hkv;
-  const int64_t want = 4 * (int64_t)cu_count;  // workgroups: about four per CU
-  int64_t splits = (want + programs - 1) / programs;
+  int64_t splits = (cu_count + programs - 1) / programs;
   splits = std::min<int64_t>(splits, ceil_div(max_ctx, kMinChunk));
   splits = std::max<int64_t>(splits, ceil_div(max_ctx, kMaxChunk));
   return (int)std::max<int64_t>(1, std::min<int64_t>(splits, 1 << 20));
@@ -544,7 +663,8 @@ int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count) {
 int split_chunk_host(int max_ctx, int splits) {
   splits = std::max(1, splits);
   const int per = ceil_div(std::max(1, max_ctx), splits);
-  return ceil_div(per, kChunkAlign) * kChunkAlign;
+  // A split never exceeds the block ids the MFMA kernel stages in LDS (kMaxSplitBlocks blocks of 16 tokens).
+  return std::min(ceil_div(per, kChunkAlign) * kChunkAlign, kMaxSplitBlocks * 16);
 }
 
 template <typename Kernel>
@@ -585,6 +705,30 @@ static int dispatch_combine(int D, dim3 grid, const DecodeArgs& a, hipStream_t s
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Tiles each wave keeps in flight in the MFMA kernel. SIPA_PREFETCH_TILES overrides the default for tuning sweeps.
+static int prefetch_tiles(int D) {
+  const char* e = getenv("SIPA_PREFETCH_TILES");
+  const int env = e ? atoi(e) : 0;
+  if (env > 0) return env;
+  return 2;
+}
+
+static int launch_mfma(int D, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  if (D == 64) {
+    switch (nb) {
+      case 1: return launch(decode_mfma_bf16<64, 1>, grid, a, st);
+      case 2: return launch(decode_mfma_bf16<64, 2>, grid, a, st);
+      case 3: return launch(decode_mfma_bf16<64, 3>, grid, a, st);
+      default: return launch(decode_mfma_bf16<64, 4>, grid, a, st);
+    }
+  }
+  switch (nb) {
+    case 1: return launch(decode_mfma_bf16<128, 1>, grid, a, st);
+    case 2: return launch(decode_mfma_bf16<128, 2>, grid, a, st);
+    default: return launch(decode_mfma_bf16<128, 3>, grid, a, st);
+  }
+}
 
 }  // namespace sipa
 
@@ -686,6 +830,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.B = B;
   a.splits = splits;
   a.chunk = chunk;
+  a.max_ctx = p->max_context;
   a.fused = p->combine == SIPA_COMBINE_FUSED;
   a.scale_log2 = p->scale * 1.4426950408889634f;
 
@@ -710,10 +855,12 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
 
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid(splits, Hkv, S);
+  const int64_t wgs = (int64_t)S * Hkv * splits;
+  SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
+  const dim3 grid((unsigned)wgs);
   int rc;
   if (use_mfma)
-    rc = (D == 64) ? launch(decode_mfma_bf16<64>, grid, a, st) : launch(decode_mfma_bf16<128>, grid, a, st);
+    rc = launch_mfma(D, prefetch_tiles(D), grid, a, st);
   else if (p->q_dtype == SIPA_F32)
     rc = dispatch_valu<SIPA_F32>(D, mode, grid, a, st);
   else

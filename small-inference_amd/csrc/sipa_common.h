@@ -19,7 +19,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxGroup = 16;      // query heads per KV head the kernels accept (the MFMA tile height)
 constexpr int kChunkAlign = 64;    // split chunks are multiples of 64 tokens (the reference's TILE)
 constexpr int kMinChunk = 256;     // smallest split the CU-count policy makes
-constexpr int kMaxChunk = 512;     // largest split the policy makes when the grid is already full
+constexpr int kMaxChunk = 2048;    // largest split the policy makes when the grid is already full
 
 // ---- element conversions -------------------------------------------------------------------------------------
 
@@ -80,6 +80,7 @@ struct DecodeArgs {
   float* pl;          // [S, Hq, splits] split softmax denominators
   int32_t* counters;  // [S, Hkv] splits finished, for the last-arriving merge
   int32_t S, Hq, Hkv, G, B, splits, chunk;
+  int32_t max_ctx;    // every block-table row covers ceil(max_ctx / B) blocks
   int32_t ks_f32, vs_f32;
   int32_t fused;      // 1: the last split workgroup of a (sequence, KV head) merges the splits
   float scale_log2;   // softmax scale * log2(e): scores are kept in the exp2 domain

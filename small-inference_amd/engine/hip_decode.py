@@ -85,6 +85,126 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     return ws
 
 
+class DecodePlan:
+    """Validated launch parameters of one paged decode, reusable across layers and steps of the same shapes.
+
+    Building a plan does every shape, dtype and stride check and fills the C parameter block once; calling it
+    swaps in the per-call tensors (q, the layer's pools and scales, out) and costs one ctypes call and one kernel
+    launch. paged_decode_attention() builds a plan and runs it once; the caches build one per forward in begin()
+    and run it for every layer.
+    """
+
+    def __init__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 context_lens: torch.Tensor, scale: float, max_context: int, num_splits: int | None = None,
+                 quant: QuantKV | None = None, *, impl: str = "auto", combine: str = "fused"):
+        S, Hq, D = q.shape
+        Hkv, N, B, _ = k_cache.shape
+        assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and \
+            block_tables.stride(-1) == 1
+        assert TILE % B == 0, "tiles must be block-aligned"
+        _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens)
+        if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+            raise ValueError("block_tables and context_lens must be int32")
+        if impl not in _hip.IMPL or combine not in _hip.COMBINE:
+            raise ValueError(f"impl {impl!r} / combine {combine!r}")
+        self.shape, self.dtype, self.device = (S, Hq, D), q.dtype, q.device
+        self.pool_shape, self.pool_dtype = tuple(k_cache.shape), k_cache.dtype
+        self.quant_mode = 0 if quant is None else quant.mode
+        self._keep = [block_tables, context_lens.contiguous()]  # tensors the parameter block points into
+        self.lib = _hip.lib()
+        self.stream = _hip.stream_of(q)
+        self.requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
+        self.splits, self.chunk = split_plan(max_context, self.requested)
+
+        p = self.params = _hip.DecodeParams()
+        p.struct_size = ctypes.sizeof(_hip.DecodeParams)
+        p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = S, Hq, Hkv, D, B
+        p.num_blocks, p.max_context, p.num_splits = N, max_context, self.requested
+        p.q_dtype = _hip.dtype_code(q.dtype)
+        p.impl, p.combine = _hip.IMPL[impl], _hip.COMBINE[combine]
+        p.scale = float(scale)
+        p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
+        p.context_lens = self._keep[1].data_ptr()
+        p.kv_mode = self.quant_mode
+        if quant is None:
+            if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+                raise ValueError("without `quant` the pool must be in q's dtype")
+        else:
+            if k_cache.dtype != torch.int8 or v_cache.dtype != torch.int8:
+                raise ValueError("INT8 modes need int8 pools")
+            if quant.mode not in (1, 2):
+                raise ValueError(f"QuantKV.mode must be 1 or 2, got {quant.mode}")
+            if quant.mode == 2:
+                if quant.stage is None or quant.tail_slots is None:
+                    raise ValueError("mode 2 needs stage and tail_slots")
+                if quant.tail_slots.dtype != torch.int32:
+                    raise ValueError("tail_slots must be int32")
+                tails = quant.tail_slots.contiguous()
+                self._keep.append(tails)
+                p.tail_slots = tails.data_ptr()
+        if S > 0 and self.splits > 1:
+            nbytes = int(self.lib.sipa_decode_workspace_bytes(S, Hq, Hkv, D, self.requested))
+            ws = _workspace(q.device, self.stream, nbytes)
+            self._keep.append(ws)
+            p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+        self._bind(q, k_cache, v_cache, quant)
+
+    def _bind(self, q, k_cache, v_cache, quant) -> None:
+        """Point the parameter block at this call's tensors (same shapes and dtypes as the plan's)."""
+        if tuple(q.shape) != self.shape or q.dtype != self.dtype or q.stride(-1) != 1:
+            raise ValueError("q does not match the plan")
+        if tuple(k_cache.shape) != self.pool_shape or tuple(v_cache.shape) != self.pool_shape or \
+                k_cache.dtype != self.pool_dtype or v_cache.dtype != self.pool_dtype or \
+                not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("the pools do not match the plan")
+        self._q, self._k, self._v, self._quant = q, k_cache, v_cache, quant
+        p = self.params
+        p.q, p.q_stride_s, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+        p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
+        if self.quant_mode:
+            ks, vs = quant.k_scale, quant.v_scale
+            if ks.stride(-1) != 1 or vs.stride(-1) != 1:
+                raise ValueError("scales need a contiguous last dim")
+            p.k_scale, p.k_scale_dtype, p.ks_stride_h, p.ks_stride_n = \
+                ks.data_ptr(), _hip.dtype_code(ks.dtype), ks.stride(0), ks.stride(1)
+            p.v_scale, p.v_scale_dtype, p.vs_stride_h, p.vs_stride_n = \
+                vs.data_ptr(), _hip.dtype_code(vs.dtype), vs.stride(0), vs.stride(1)
+            if self.quant_mode == 2:
+                st = quant.stage
+                if st.dtype != torch.bfloat16 or st.stride(-1) != 1:
+                    raise ValueError("stage must be bf16 with a contiguous last dim")
+                p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = \
+                    st.data_ptr(), st.stride(0), st.stride(1), st.stride(2)
+
+    def __call__(self, q: torch.Tensor | None = None, k_cache: torch.Tensor | None = None,
+                 v_cache: torch.Tensor | None = None, quant: QuantKV | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """Run the decode; tensors left as None keep the ones last bound. Returns out ([S, Hq, D], q's dtype)."""
+        if q is not None or k_cache is not None or v_cache is not None or quant is not None:
+            self._bind(q if q is not None else self._q, k_cache if k_cache is not None else self._k,
+                       v_cache if v_cache is not None else self._v, quant if quant is not None else self._quant)
+        if out is None:
+            out = torch.empty(self.shape, device=self.device, dtype=self.dtype)
+        elif tuple(out.shape) != self.shape or out.dtype != self.dtype or out.stride(-1) != 1:
+            raise ValueError("out must be [S, Hq, D] in q's dtype with a contiguous last dim")
+        if self.shape[0] == 0:
+            return out
+        p = self.params
+        p.out, p.out_stride_s, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+        _hip.check(self.lib.sipa_decode(ctypes.byref(p), self.stream), "paged_decode_attention")
+        return out
+
+    def launch_raw(self, k_ptr: int, v_ptr: int, out_ptr: int) -> int:
+        """Lowest-overhead launch for benchmarks: swap the pool and output addresses only (pools with the bound
+        shapes, strides and dtypes; out a contiguous [S, Hq, D] tensor in q's dtype) and return the C return
+        code."""
+        p = self.params
+        p.k_cache, p.v_cache, p.out = k_ptr, v_ptr, out_ptr
+        p.out_stride_s, p.out_stride_h = self.shape[1] * self.shape[2], self.shape[2]
+        return self.lib.sipa_decode(ctypes.byref(p), self.stream)
+
+
 def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                            context_lens: torch.Tensor, scale: float, max_context: int,
                            num_splits: int | None = None, quant: QuantKV | None = None, *, impl: str = "auto",
@@ -96,75 +216,6 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     >= 1, the new token included); max_context = max(context_lens), known on the host. num_splits None picks from
     the CU count. Returns [S, Hq, D] in q's dtype (written into `out` if given).
     """
-    S, Hq, D = q.shape
-    Hkv, N, B, _ = k_cache.shape
-    assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and block_tables.stride(-1) == 1
-    assert TILE % B == 0, "tiles must be block-aligned"
-    _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens)
-    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
-        raise ValueError("block_tables and context_lens must be int32")
-    if not context_lens.is_contiguous():
-        context_lens = context_lens.contiguous()
-    if out is None:
-        out = torch.empty(S, Hq, D, device=q.device, dtype=q.dtype)
-    elif out.shape != (S, Hq, D) or out.dtype != q.dtype or out.stride(-1) != 1:
-        raise ValueError("out must be [S, Hq, D] in q's dtype with a contiguous last dim")
-    if S == 0:
-        return out
-
-    requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
-    splits, _ = split_plan(max_context, requested)
-    lib = _hip.lib()
-    stream = _hip.stream_of(q)
-
-    p = _hip.DecodeParams()
-    p.struct_size = ctypes.sizeof(_hip.DecodeParams)
-    p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = S, Hq, Hkv, D, B
-    p.num_blocks, p.max_context, p.num_splits = N, max_context, requested
-    p.q_dtype = _hip.dtype_code(q.dtype)
-    p.impl = _hip.IMPL[impl]
-    p.combine = _hip.COMBINE[combine]
-    p.scale = float(scale)
-    p.q, p.q_stride_s, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
-    p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
-    p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
-    p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
-    p.context_lens = context_lens.data_ptr()
-    p.out, p.out_stride_s, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
-    keep = []  # tensors that must outlive the call
-    if quant is None:
-        if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
-            raise ValueError("without `quant` the pool must be in q's dtype")
-        p.kv_mode = _hip.KV_PLAIN
-    else:
-        if k_cache.dtype != torch.int8 or v_cache.dtype != torch.int8:
-            raise ValueError("INT8 modes need int8 pools")
-        if quant.mode not in (1, 2):
-            raise ValueError(f"QuantKV.mode must be 1 or 2, got {quant.mode}")
-        ks, vs = quant.k_scale, quant.v_scale
-        if ks.stride(-1) != 1 or vs.stride(-1) != 1:
-            raise ValueError("scales need a contiguous last dim")
-        p.kv_mode = quant.mode
-        p.k_scale, p.k_scale_dtype, p.ks_stride_h, p.ks_stride_n = \
-            ks.data_ptr(), _hip.dtype_code(ks.dtype), ks.stride(0), ks.stride(1)
-        p.v_scale, p.v_scale_dtype, p.vs_stride_h, p.vs_stride_n = \
-            vs.data_ptr(), _hip.dtype_code(vs.dtype), vs.stride(0), vs.stride(1)
-        if quant.mode == 2:
-            st, tails = quant.stage, quant.tail_slots
-            if st is None or tails is None:
-                raise ValueError("mode 2 needs stage and tail_slots")
-            if st.dtype != torch.bfloat16 or st.stride(-1) != 1:
-                raise ValueError("stage must be bf16 with a contiguous last dim")
-            if tails.dtype != torch.int32:
-                raise ValueError("tail_slots must be int32")
-            tails = tails.contiguous()
-            keep.append(tails)
-            p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = st.data_ptr(), st.stride(0), st.stride(1), \
-                st.stride(2)
-            p.tail_slots = tails.data_ptr()
-    if splits > 1:
-        nbytes = int(lib.sipa_decode_workspace_bytes(S, Hq, Hkv, D, requested))
-        ws = _workspace(q.device, stream, nbytes)
-        p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
-    _hip.check(lib.sipa_decode(ctypes.byref(p), stream), "paged_decode_attention")
-    return out
+    plan = DecodePlan(q, k_cache, v_cache, block_tables, context_lens, scale, max_context, num_splits, quant,
+                      impl=impl, combine=combine)
+    return plan(out=out)

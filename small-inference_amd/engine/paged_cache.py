@@ -106,6 +106,8 @@ class PagedKVCache:
         self._allocate((cfg.num_layers, cfg.num_kv_heads, num_blocks, block_size, cfg.head_dim), device, dtype)
         self.meta: PagedMetadata | None = None
         self._decode = None
+        self._plan = None
+        self._plan_scale = None
         self._arange = torch.empty(0, dtype=torch.int64, device=device)
 
     def _allocate(self, shape: tuple, device: str | torch.device, dtype: torch.dtype) -> None:
@@ -128,6 +130,7 @@ class PagedKVCache:
             raise ValueError("a paged forward needs metadata for exactly its tokens")
         self.meta = meta
         self._decode = None
+        self._plan = None  # decode launch parameters, built by the first attend() of the forward
         if self.attn_backend not in KERNEL_BACKENDS:
             return
         if not self.on_gpu:
@@ -183,13 +186,18 @@ class PagedKVCache:
         if self._decode is None:
             outs = [self._attend_gather(layer, i, q, positions, scale) for i in range(m.num_seqs)]
             return outs[0] if len(outs) == 1 else torch.cat(outs)
-        from .hip_decode import paged_decode_attention
+        from .hip_decode import DecodePlan
 
         rows, bt, ctx, max_ctx = self._decode
         T, Hq, d = q.shape
         q_dec = q if rows is None else q[rows]
-        dec = paged_decode_attention(q_dec, self.k[layer], self.v[layer], bt, ctx, scale, max_ctx,
-                                     quant=self._kernel_quant(layer))
+        quant = self._kernel_quant(layer)
+        if self._plan is None or self._plan_scale != scale:  # first layer of the forward: validate once
+            self._plan = DecodePlan(q_dec, self.k[layer], self.v[layer], bt, ctx, scale, max_ctx, quant=quant)
+            self._plan_scale = scale
+            dec = self._plan()
+        else:
+            dec = self._plan(q=q_dec, k_cache=self.k[layer], v_cache=self.v[layer], quant=quant)
         if rows is None:
             return dec.view(T, Hq * d)
         out = torch.empty(T, Hq * d, device=q.device, dtype=q.dtype)

@@ -81,15 +81,17 @@ def test_store_entry_points_reject_bad_arguments():
 
 
 def test_split_policy_host_side():
-    """CU-count split policy: a full grid needs no split; small grids split up to >= 4 workgroups per CU with
-    splits of 256..512 tokens; long contexts are always cut to <= 512-token splits."""
+    """CU-count split policy: about one workgroup per CU, splits of 256..2048 tokens (64-token multiples); a
+    grid that is already full is not split unless a sequence is longer than 2048 tokens."""
     lib = _hip.lib()
     for S, Hkv, ctx in [(1, 2, 8192), (32, 2, 8192), (256, 2, 8192), (64, 2, 4096), (1, 2, 1024), (512, 2, 300)]:
         req = lib.sipa_choose_splits(S, Hkv, ctx, 256)
         chunk = lib.sipa_split_chunk(ctx, req)
         launched = -(-ctx // chunk)
-        assert chunk % 64 == 0 and chunk <= max(512, 64)
-        assert S * Hkv * launched >= min(1024, S * Hkv * -(-ctx // 256)), (S, Hkv, ctx, req, chunk)
-    assert lib.sipa_choose_splits(32, 2, 8192, 256) == 16
-    assert lib.sipa_split_chunk(8192, 16) == 512
+        assert chunk % 64 == 0 and chunk <= 2048
+        assert S * Hkv * launched >= min(256, S * Hkv * -(-ctx // 256)), (S, Hkv, ctx, req, chunk)
+    assert lib.sipa_choose_splits(32, 2, 8192, 256) == 4
+    assert lib.sipa_split_chunk(8192, 4) == 2048
+    assert lib.sipa_choose_splits(256, 2, 8192, 256) == 4      # long sequences still split at 2048 tokens
+    assert lib.sipa_choose_splits(512, 2, 300, 256) == 1
     assert lib.sipa_decode_workspace_bytes(32, 14, 2, 64, 1) == 0
