@@ -40,185 +40,9 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "sipa_common.h"
+#include "decode_common.h"
 
 namespace sipa {
-
-constexpr float kNegInf = -__builtin_huge_valf();
-constexpr int kMaxSplitBlocks = 2048;  // block ids of one split the MFMA kernel stages in LDS (32768 tokens)
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-// The grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware hands workgroup L
-// to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads evenly over
-// them; and every sequence's first split (the only one a short sequence has) is dispatched before any second one.
-struct WorkItem {
-  int s, h, sp;
-};
-
-__device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
-  const int L = blockIdx.x;
-  const int sh = L % (a.S * a.Hkv);
-  return WorkItem{sh % a.S, sh / a.S, L / (a.S * a.Hkv)};
-}
-
-template <bool OUT_F32>
-__device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, int d, float v) {
-  const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d;
-  if (OUT_F32)
-    ((float*)a.out)[i] = v;
-  else
-    ((uint16_t*)a.out)[i] = f32_to_bf16_bits(v);
-}
-
-// Partials that another workgroup of the same launch merges are written and read with agent-scope atomic
-// accesses: on gfx950 these are global_store / global_load with the sc1 bit, which write through to and read from
-// the point of coherence of all XCDs. Ordering then needs only the completion of this workgroup's stores
-// (s_waitcnt vmcnt(0)) before its counter increment, not an agent-scope fence, which would write back and
-// invalidate the whole L2 of the XCD once per workgroup.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_coherent(float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). COHERENT: the
-// partials were written by other workgroups of this launch (the fused merge). Up to 8 splits are loaded per
-// round (one memory round trip) and merged online, so the usual 2..8 splits cost a single round trip.
-template <int D, bool OUT_F32, bool COHERENT>
-__device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
-  constexpr int kBatch = 8;
-  const int G = a.G;
-  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-    const int g = idx / D, d = idx % D;
-    const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
-    float M = kNegInf, num = 0.f, den = 0.f;
-    for (int j0 = 0; j0 < nvalid; j0 += kBatch) {
-      float mj[kBatch], lj[kBatch], pj[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int j = j0 + u;
-        const bool ok = j < nvalid;
-        mj[u] = ok ? ld(a.pm + row0 + j) : kNegInf;
-        lj[u] = ok ? ld(a.pl + row0 + j) : 0.f;
-        pj[u] = ok ? ld(a.part + (row0 + j) * D + d) : 0.f;
-      }
-      float mb = M;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mj[u]);
-      const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf)
-      num *= rescale;
-      den *= rescale;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const float w = fast_exp2(mj[u] - mb);  // 0 for the padding entries (m = -inf)
-        num += w * pj[u];
-        den += w * lj[u];
-      }
-      M = mb;
-    }
-    store_out<OUT_F32>(a, s, h * G + g, d, num / den);
-  }
-}
-
-// Merge the four waves' states (ms, ls [4][16], accs [4][16][D] in LDS, after a barrier) and write the output
-// (whole sequence in this workgroup) or the split partial; with fused merging, the last split workgroup of
-// (s, h) to arrive then combines all partials.
-template <int D, bool OUT_F32>
-__device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nvalid, const float* ms,
-                             const float* ls, const float* accs, int* last_flag) {
-  const int G = a.G;
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-    const int g = idx / D, d = idx % D;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ms[w * kMaxGroup + g]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = ms[w * kMaxGroup + g];
-      const float e = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);  // a wave with no tokens drops out
-      L += e * ls[w * kMaxGroup + g];
-      O += e * accs[(w * kMaxGroup + g) * D + d];
-    }
-    if (nvalid == 1) {
-      store_out<OUT_F32>(a, s, h * G + g, d, O / L);
-    } else {
-      const int64_t row = ((int64_t)s * a.Hq + h * G + g) * a.splits + sp;
-      if (a.fused) {
-        store_coherent(a.part + row * D + d, O);
-        if (d == 0) {
-          store_coherent(a.pm + row, M);
-          store_coherent(a.pl + row, L);
-        }
-      } else {
-        a.part[row * D + d] = O;
-        if (d == 0) {
-          a.pm[row] = M;
-          a.pl[row] = L;
-        }
-      }
-    }
-  }
-  if (nvalid == 1 || !a.fused) return;
-  // This workgroup's partial has reached the coherence point once its stores complete; then count it. The
-  // workgroup that brings the count to nvalid merges every partial of (s, h) and resets the counter.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    *last_flag = (prev == nvalid - 1);
-  }
-  __syncthreads();
-  if (!*last_flag) return;
-  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---- MFMA kernel: bf16, B = 16 ---------------------------------------------------------------------------------
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <int D>
-struct MfmaSmem {
-  static constexpr int kVPitch = D + 8;                                // bf16 elements per LDS row of V
-  static constexpr int kVBytes = kWaves * 32 * kVPitch * 2;            // per-wave [32 tok][D] V tiles
-  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * D) * 4;
-  static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
-};
-
-// K/V are streamed once per call: nontemporal loads keep them from displacing anything in the caches.
-__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) { return __builtin_nontemporal_load((const u32x4*)p); }
-
-// One 32-token tile (two blocks) of K and V in registers: K in the QK A-operand layout, V as 16-byte row chunks.
-template <int D>
-struct KVTile {
-  u32x4 k[2][D / 32];
-  u32x4 v[2][D / 32];
-};
 
 template <int D, int NB>  // NB: tiles in flight per wave (the register prefetch ring)
 __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a) {
@@ -238,18 +62,8 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
-  // Block ids, the query group and the context length are loaded together: the ids are fetched for the
-  // longest possible split (every table row covers max_ctx tokens) before ctx[s] is known, so the first K/V
-  // loads wait for one memory round trip instead of two.
-  constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
-  const int nb_spec = (min(a.chunk, a.max_ctx - start) + 15) >> 4;
-  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
   int ids[kIdsPerThread];
-#pragma unroll
-  for (int i = 0; i < kIdsPerThread; ++i) {
-    const int j = threadIdx.x + kThreads * i;
-    ids[i] = (j < nb_spec) ? btr[j] : 0;
-  }
+  const int nb_spec = fetch_split_ids(a, s, start, ids);
   bf16x8 qop[KS];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
@@ -264,11 +78,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   if (start >= ctx) return;
   const int end = min(start + a.chunk, ctx);
   const int nvalid = (ctx + a.chunk - 1) / a.chunk;
-#pragma unroll
-  for (int i = 0; i < kIdsPerThread; ++i) {
-    const int j = threadIdx.x + kThreads * i;
-    if (j < nb_spec) bids[j] = ids[i];
-  }
+  commit_split_ids(nb_spec, ids, bids);
   __syncthreads();  // block ids staged
 
   const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
@@ -405,20 +215,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
     }
   }
 
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  __syncthreads();  // every wave is done with its V tile: the LDS becomes the merge buffer
-  float* ms = (float*)smem;
-  float* ls = ms + kWaves * kMaxGroup;
-  float* accs = ls + kWaves * kMaxGroup;
-  if (q4 == 0) {
-    ms[wave * kMaxGroup + r] = m_run;
-    ls[wave * kMaxGroup + r] = l_run;
-  }
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) *(f32x4*)(accs + (wave * kMaxGroup + r) * D + 16 * dt + 4 * q4) = acc[dt];
-  __syncthreads();
-  finish_split<D, false>(a, s, h, sp, nvalid, ms, ls, accs, &last_flag);
+  mfma_epilogue<D, false>(a, s, h, sp, nvalid, m_run, l_run, acc, smem, &last_flag);
 }
 
 // ---- VALU kernel: any supported shape, fp32 / bf16, KV modes 0 / 1 / 2 -----------------------------------------
@@ -847,11 +644,31 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
     a.part = (float*)(base + w.part);
   }
 
+  // The MFMA kernels: bf16 query, 16-token blocks, head_dim 64 / 128, 16-byte aligned rows, and for INT8 pools
+  // fp16 scales laid out for 8-byte (per-token) and 16-byte (per-channel) vector loads.
   const bool q_aligned = aligned16(p->q) && p->q_stride_s % 8 == 0 && p->q_stride_h % 8 == 0;
-  const bool mfma_ok = p->q_dtype == SIPA_BF16 && mode == SIPA_KV_PLAIN && B == 16 && (D == 64 || D == 128) &&
-                       q_aligned;
+  bool mfma_ok = p->q_dtype == SIPA_BF16 && B == 16 && (D == 64 || D == 128) && q_aligned;
+  int int8_variant = 0;
+  if (mfma_ok && mode != SIPA_KV_PLAIN) {
+    auto tok_scales_ok = [](const void* ptr, int dt, int64_t sh, int64_t sn) {
+      return dt == SIPA_F16 && ((uintptr_t)ptr & 7) == 0 && sh % 4 == 0 && sn % 4 == 0;
+    };
+    const bool vs_ok = tok_scales_ok(p->v_scale, p->v_scale_dtype, p->vs_stride_h, p->vs_stride_n);
+    if (mode == SIPA_KV_INT8_TOKEN) {
+      int8_variant = 1;
+      mfma_ok = vs_ok && tok_scales_ok(p->k_scale, p->k_scale_dtype, p->ks_stride_h, p->ks_stride_n);
+    } else if (p->ks_stride_n == 0) {
+      int8_variant = 3;
+      mfma_ok = vs_ok;
+    } else {
+      int8_variant = 2;
+      mfma_ok = vs_ok && p->k_scale_dtype == SIPA_F16 && aligned16(p->k_scale) && p->ks_stride_h % 8 == 0 &&
+                p->ks_stride_n % 8 == 0;
+    }
+  }
   SIPA_CHECK(p->impl != SIPA_IMPL_MFMA || mfma_ok, SIPA_EUNSUPPORTED,
-             "the MFMA kernel needs bf16, kv_mode 0, block 16, head_dim 64/128 and 16-byte aligned q rows");
+             "the MFMA kernels need a bf16 query, block 16, head_dim 64/128, 16-byte aligned rows and fp16 scales "
+             "(or fp32 channel scales with a zero block stride)");
   const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
 
   hipStream_t st = (hipStream_t)stream;
@@ -859,8 +676,10 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   const dim3 grid((unsigned)wgs);
   int rc;
-  if (use_mfma)
+  if (use_mfma && mode == SIPA_KV_PLAIN)
     rc = launch_mfma(D, prefetch_tiles(D), grid, a, st);
+  else if (use_mfma)
+    rc = launch_mfma_int8(D, int8_variant, prefetch_tiles(D), grid, a, st);
   else if (p->q_dtype == SIPA_F32)
     rc = dispatch_valu<SIPA_F32>(D, mode, grid, a, st);
   else

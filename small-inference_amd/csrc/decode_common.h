@@ -1,0 +1,239 @@
+// Device code shared by the decode kernels (decode.hip: bf16 MFMA, VALU, combine; decode_int8.hip: INT8 MFMA):
+// grid-to-work mapping, the split merge (LDS merge of the waves, coherent partials, last-arriving combine), and
+// the MFMA kernels' common prologue and epilogue.
+#pragma once
+
+#include "sipa_common.h"
+
+namespace sipa {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr int kMaxSplitBlocks = 2048;  // block ids of one split the MFMA kernel stages in LDS (32768 tokens)
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// The grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware hands workgroup L
+// to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads evenly over
+// them; and every sequence's first split (the only one a short sequence has) is dispatched before any second one.
+struct WorkItem {
+  int s, h, sp;
+};
+
+__device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
+  const int L = blockIdx.x;
+  const int sh = L % (a.S * a.Hkv);
+  return WorkItem{sh % a.S, sh / a.S, L / (a.S * a.Hkv)};
+}
+
+template <bool OUT_F32>
+__device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, int d, float v) {
+  const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d;
+  if (OUT_F32)
+    ((float*)a.out)[i] = v;
+  else
+    ((uint16_t*)a.out)[i] = f32_to_bf16_bits(v);
+}
+
+// Partials that another workgroup of the same launch merges are written and read with agent-scope atomic
+// accesses: on gfx950 these are global_store / global_load with the sc1 bit, which write through to and read from
+// the point of coherence of all XCDs. Ordering then needs only the completion of this workgroup's stores
+// (s_waitcnt vmcnt(0)) before its counter increment, not an agent-scope fence, which would write back and
+// invalidate the whole L2 of the XCD once per workgroup.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). COHERENT: the
+// partials were written by other workgroups of this launch (the fused merge). Up to 8 splits are loaded per
+// round (one memory round trip) and merged online, so the usual 2..8 splits cost a single round trip.
+template <int D, bool OUT_F32, bool COHERENT>
+__device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
+  constexpr int kBatch = 8;
+  const int G = a.G;
+  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
+    float M = kNegInf, num = 0.f, den = 0.f;
+    for (int j0 = 0; j0 < nvalid; j0 += kBatch) {
+      float mj[kBatch], lj[kBatch], pj[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = j0 + u;
+        const bool ok = j < nvalid;
+        mj[u] = ok ? ld(a.pm + row0 + j) : kNegInf;
+        lj[u] = ok ? ld(a.pl + row0 + j) : 0.f;
+        pj[u] = ok ? ld(a.part + (row0 + j) * D + d) : 0.f;
+      }
+      float mb = M;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mj[u]);
+      const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf)
+      num *= rescale;
+      den *= rescale;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float w = fast_exp2(mj[u] - mb);  // 0 for the padding entries (m = -inf)
+        num += w * pj[u];
+        den += w * lj[u];
+      }
+      M = mb;
+    }
+    store_out<OUT_F32>(a, s, h * G + g, d, num / den);
+  }
+}
+
+// Merge the four waves' states (ms, ls [4][16], accs [4][16][D] in LDS, after a barrier) and write the output
+// (whole sequence in this workgroup) or the split partial; with fused merging, the last split workgroup of
+// (s, h) to arrive then combines all partials.
+template <int D, bool OUT_F32>
+__device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nvalid, const float* ms,
+                             const float* ls, const float* accs, int* last_flag) {
+  const int G = a.G;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ms[w * kMaxGroup + g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = ms[w * kMaxGroup + g];
+      const float e = (mw == kNegInf) ? 0.f : fast_exp2(mw - M);  // a wave with no tokens drops out
+      L += e * ls[w * kMaxGroup + g];
+      O += e * accs[(w * kMaxGroup + g) * D + d];
+    }
+    if (nvalid == 1) {
+      store_out<OUT_F32>(a, s, h * G + g, d, O / L);
+    } else {
+      const int64_t row = ((int64_t)s * a.Hq + h * G + g) * a.splits + sp;
+      if (a.fused) {
+        store_coherent(a.part + row * D + d, O);
+        if (d == 0) {
+          store_coherent(a.pm + row, M);
+          store_coherent(a.pl + row, L);
+        }
+      } else {
+        a.part[row * D + d] = O;
+        if (d == 0) {
+          a.pm[row] = M;
+          a.pl[row] = L;
+        }
+      }
+    }
+  }
+  if (nvalid == 1 || !a.fused) return;
+  // This workgroup's partial has reached the coherence point once its stores complete; then count it. The
+  // workgroup that brings the count to nvalid merges every partial of (s, h) and resets the counter.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = (prev == nvalid - 1);
+  }
+  __syncthreads();
+  if (!*last_flag) return;
+  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- MFMA kernels --------------------------------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct MfmaSmem {
+  static constexpr int kVPitch = D + 8;                                // bf16 elements per LDS row of V
+  static constexpr int kVBytes = kWaves * 32 * kVPitch * 2;            // per-wave [32 tok][D] V tiles
+  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * D) * 4;
+  static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
+};
+
+// K/V are streamed once per call: nontemporal loads keep them from displacing anything in the caches.
+__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+
+// One 32-token tile (two blocks) of K and V in registers: K in the QK A-operand layout, V as 16-byte row chunks.
+template <int D>
+struct KVTile {
+  u32x4 k[2][D / 32];
+  u32x4 v[2][D / 32];
+};
+
+// ---- prologue / epilogue shared by the MFMA kernels ----------------------------------------------------------
+
+// Issue the loads of a split's block ids for the longest possible split (every table row covers max_ctx tokens)
+// before ctx[s] is known, so that the first K/V loads wait for one memory round trip instead of two.
+constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
+
+__device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int (&ids)[kIdsPerThread]) {
+  const int nb_spec = (min(a.chunk, a.max_ctx - start) + 15) >> 4;
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
+#pragma unroll
+  for (int i = 0; i < kIdsPerThread; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    ids[i] = (j < nb_spec) ? btr[j] : 0;
+  }
+  return nb_spec;
+}
+
+__device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[kIdsPerThread], int* bids) {
+#pragma unroll
+  for (int i = 0; i < kIdsPerThread; ++i) {
+    const int j = threadIdx.x + kThreads * i;
+    if (j < nb_spec) bids[j] = ids[i];
+  }
+}
+
+// MFMA epilogue: each wave's softmax state (m_run per lane for head g = r, l_run partial per lane, acc in the
+// O^T accumulator layout: lane (r, q4) holds head r, channels 16 dt + 4 q4 + i) is merged through LDS and the
+// split finished (output, or partial + merge).
+template <int D, bool OUT_F32>
+__device__ __forceinline__ void mfma_epilogue(const DecodeArgs& a, int s, int h, int sp, int nvalid, float m_run,
+                                              float l_run, const f32x4 (&acc)[D / 16], char* smem,
+                                              int* last_flag) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  __syncthreads();  // every wave is done with its LDS tiles: the LDS becomes the merge buffer
+  float* ms = (float*)smem;
+  float* ls = ms + kWaves * kMaxGroup;
+  float* accs = ls + kWaves * kMaxGroup;
+  if (q4 == 0) {
+    ms[wave * kMaxGroup + r] = m_run;
+    ls[wave * kMaxGroup + r] = l_run;
+  }
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) *(f32x4*)(accs + (wave * kMaxGroup + r) * D + 16 * dt + 4 * q4) = acc[dt];
+  __syncthreads();
+  finish_split<D, OUT_F32>(a, s, h, sp, nvalid, ms, ls, accs, last_flag);
+}
+
+// INT8 MFMA kernels (decode_int8.hip). mode: 1 per-token K scales, 2 per-(block, channel) K scales,
+// 3 per-(head, channel) K scales (mode 2 with a zero block stride). nb: tiles in flight per wave.
+int launch_mfma_int8(int D, int mode, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st);
+
+}  // namespace sipa

@@ -1,0 +1,320 @@
+// Paged decode over INT8 K/V pools on the matrix cores (gfx950), dequantization fused into the operands.
+//
+// Reference: engine/triton_decode.py:93-117,126-130 (KV_MODE 1 and 2) and engine/quant_cache.py (the formats):
+//   mode 1 (format "int8"): K and V int8 [Hkv, N, B, D], fp16 scales per token [Hkv, N, B] each;
+//   mode 2 (format "int8-kchannel"): K int8 with fp16 scales per (block, channel) [Hkv, N, D] (a zero block stride
+//     gives one scale per (head, channel)), each sequence's partial last block of K in a bf16 staging slot;
+//     V as in mode 1.
+// Same work decomposition, prefetch ring, online softmax and split merge as the bf16 kernel (decode.hip); the
+// differences are the operands, per 16-token block (one MFMA M-tile):
+//   S^T = K_int . Q^T on v_mfma_f32_16x16x32_f16. int8 codes become fp16 exactly (the byte, biased by 128, is
+//     placed under the exponent of 1024 with v_perm_b32, then 1152 is subtracted); the bf16 query is exact in
+//     fp16 over fp16's normal range. Mode 1 multiplies the fp32 scores by the per-token K scale, as the reference
+//     does (score_t = (q . k_int_t) s_t). Mode 2 folds the block's channel scales into the query instead,
+//     Q' = q * s_c, carried as two fp16 operands (an exact high part and a low part, relative error about 2^-14,
+//     two MFMAs per k-step): one fp16 rounding of Q' (2^-11) is too coarse when outlier channels make the q.k
+//     terms large and the softmax peaked. The staged partial block uses v_mfma_f32_16x16x32_bf16 with the bf16
+//     query and bf16 staged K (exact products).
+//   O^T += V_int^T . P'^T on the fp16 MFMA with the per-token V scale folded into P (P' = p s_v, fp16), as the
+//     reference does (acc += (p s_v) v_int; l keeps the unscaled p). The V tile goes to LDS already converted to
+//     fp16 and is read back transposed.
+// Each lane loads a contiguous D/4-byte piece of a K row (channels (D/4) q4 .. (D/4)(q4+1)), so the query operand
+// uses that channel order too: k-slot 8 j + i of lane group q4 is channel (D/4) q4 + 8 j + i.
+#include "decode_common.h"
+
+namespace sipa {
+
+// 4 int8 codes (one 32-bit word) -> 4 fp16 values, exact.
+__device__ __forceinline__ void codes_to_f16(uint32_t w, f16x2& lo, f16x2& hi) {
+  const uint32_t u = w ^ 0x80808080u;  // code + 128 in each byte
+  const f16x2 bias = {(_Float16)1152.f, (_Float16)1152.f};
+  lo = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+  hi = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+}
+
+__device__ __forceinline__ f16x8 codes8_to_f16(uint32_t w0, uint32_t w1) {
+  f16x2 a, b, c, d;
+  codes_to_f16(w0, a, b);
+  codes_to_f16(w1, c, d);
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) { return f16_bits_to_f32(bits16 & 0xffffu); }
+
+template <int D>
+struct Int8Tile {
+  u32x4 k[2][D / 64];   // K codes: lane (r, q4) holds token r's channels (D/4) q4 .. (D/4)(q4+1)
+  u32x4 v[2][D / 64];   // V codes as 16-byte row chunks
+  uint2 ks[2];          // mode 1: K scales of tokens 4 q4 .. 4 q4 + 3 (fp16)
+  uint2 vs[2];          // V scales of the same tokens (fp16)
+  u32x4 kc[2][D / 32];  // mode 2: the block's channel scales of the lane's channels (fp16)
+};
+
+// MODE 1: per-token K scales; 2: per-(block, channel) K scales; 3: mode 2 with one channel scale per (head,
+// channel) for every block (a zero block stride), folded into the query once.
+template <int D, int MODE, int NB>
+__global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a) {
+  constexpr int KS = D / 32;   // QK k-steps per block
+  constexpr int DT = D / 16;   // PV d-tiles
+  constexpr int KL = D / 64;   // 16-byte K loads per lane per block
+  constexpr int VC = D / 64;   // 16-byte V chunks (16 codes) per lane per block
+  constexpr int VP = MfmaSmem<D>::kVPitch;
+  constexpr int CPR = D / 16;  // 16-code chunks per token row
+  constexpr int QW = D / 4;    // channels per lane group
+  __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
+  __shared__ int bids[kMaxSplitBlocks];
+  __shared__ int last_flag;
+
+  const WorkItem w = work_item(a);
+  const int sp = w.sp, h = w.h, s = w.s;
+  const int start = sp * a.chunk;
+  const int G = a.G;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+
+  int ids[kIdsPerThread];
+  const int nb_spec = fetch_split_ids(a, s, start, ids);
+  bf16x8 qb[KS];  // the query group in bf16 (staged block of mode 2), channel order of the int8 K layout
+  {
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      u32x4 u = *(const u32x4*)(qrow + QW * q4 + 8 * j);
+      if (r >= G) u = u32x4{0, 0, 0, 0};
+      qb[j] = __builtin_bit_cast(bf16x8, u);
+    }
+  }
+  constexpr bool kconst = MODE == 3;  // one channel scale per (head, channel) for every block
+  // qh: the query in fp16 (modes 1, 2), or the high part of Q' = q * s (mode 3) with ql its low part,
+  // fp16(Q' - qh), so that qh + ql carries Q' to about 2^-22.
+  f16x8 qh[KS], ql[KS];
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float qf = (float)qb[j][i];
+      if (kconst) {
+        const int64_t ci = (int64_t)h * a.ks_sh + QW * q4 + 8 * j + i;
+        qf *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
+      }
+      qh[j][i] = (_Float16)qf;
+      ql[j][i] = (_Float16)(qf - (float)qh[j][i]);
+    }
+  }
+  const int ctx = a.ctx[s];
+  if (start >= ctx) return;
+  const int end = min(start + a.chunk, ctx);
+  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
+  const int tail = (MODE >= 2) ? a.tail[s] : -1;       // staging slot of the partial last block, -1 if none
+  commit_split_ids(nb_spec, ids, bids);
+  __syncthreads();
+
+  const int8_t* kh = (const int8_t*)a.k + (int64_t)h * a.kv_sh;
+  const int8_t* vh = (const int8_t*)a.v + (int64_t)h * a.kv_sh;
+  const uint16_t* ksh = (const uint16_t*)a.ks + (int64_t)h * a.ks_sh;
+  const uint16_t* vsh = (const uint16_t*)a.vs + (int64_t)h * a.vs_sh;
+  _Float16* vw = (_Float16*)smem + wave * 32 * VP;
+  const int ntile = (end - start + 31) >> 5;
+  const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;
+  auto tile_t0 = [&](int k) { return start + 32 * (wave + kWaves * k); };
+
+  auto load_tile = [&](int k, Int8Tile<D>& tl) {
+    const int t0 = tile_t0(k);
+    const int bi = (t0 - start) >> 4;
+    const int b0 = bids[bi];
+    const int b1 = (t0 + 16 < end) ? bids[bi + 1] : b0;  // branch-free: a missing second block re-reads the first
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int64_t blk = mt ? b1 : b0;
+      const int8_t* kb = kh + blk * a.kv_sn;
+      const int8_t* vb = vh + blk * a.kv_sn;
+#pragma unroll
+      for (int j = 0; j < KL; ++j) tl.k[mt][j] = __builtin_nontemporal_load((const u32x4*)(kb + r * D + QW * q4 + 16 * j));
+#pragma unroll
+      for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
+      tl.vs[mt] = *(const uint2*)(vsh + blk * a.vs_sn + 4 * q4);
+      if (MODE == 1) tl.ks[mt] = *(const uint2*)(ksh + blk * a.ks_sn + 4 * q4);
+      if (MODE == 2 && !kconst) {
+#pragma unroll
+        for (int j = 0; j < KS; ++j) tl.kc[mt][j] = *(const u32x4*)(ksh + blk * a.ks_sn + QW * q4 + 8 * j);
+      }
+    }
+  };
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // p <= 2^4 against the lazily raised max, so that p * s_v (s_v <= 65504 / 127) stays within fp16.
+  constexpr float kRescaleSlack = 4.f;
+  auto process_tile = [&](int t0, Int8Tile<D>& tl) {
+    const bool partial = t0 + 32 > end;
+    // V codes -> fp16 -> LDS (rows at or past the end are zero).
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < VC; ++i) {
+        const int c = lane + 64 * i;
+        const int row = c / CPR;
+        u32x4 wv = tl.v[mt][i];
+        if (partial && t0 + 16 * mt + row >= end) wv = u32x4{0, 0, 0, 0};
+        const f16x8 lo = codes8_to_f16(wv[0], wv[1]);
+        const f16x8 hi = codes8_to_f16(wv[2], wv[3]);
+        _Float16* dst = vw + (16 * mt + row) * VP + (c % CPR) * 16;
+        *(f16x8*)dst = lo;
+        *(f16x8*)(dst + 8) = hi;
+      }
+
+    f32x4 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int tb = t0 + 16 * mt;
+      if (MODE >= 2 && tail >= 0 && tb == n_quant && tb < end) {
+        // The sequence's partial last block: bf16 K from its staging slot, exact bf16 products.
+        const uint16_t* st = (const uint16_t*)a.stage + (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn +
+                             (int64_t)r * a.st_sb + QW * q4;
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4*)(st + 8 * j)),
+                                                           qb[j], sc[mt], 0, 0, 0);
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const u32x4 kw = tl.k[mt][j >> 1];
+        const f16x8 kop = codes8_to_f16(kw[2 * (j & 1)], kw[2 * (j & 1) + 1]);
+        if (MODE == 1) {
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qh[j], sc[mt], 0, 0, 0);
+        } else if (MODE == 3) {
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qh[j], sc[mt], 0, 0, 0);
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, ql[j], sc[mt], 0, 0, 0);
+        } else {
+          // Q' = q * s with the block's fp16 channel scales s, as an exact high part plus a low part: s_hi keeps
+          // the top 3 significant bits of s (sign, exponent, 2 mantissa bits), so q * s_hi (8 x 3 bits) is exact
+          // in fp16; s_lo = s - s_hi is exact and q * s_lo is rounded relative to that small remainder only.
+          const u32x4 cw = tl.kc[mt][j];
+          const f16x8 s_all = __builtin_bit_cast(f16x8, cw);
+          const f16x8 s_hi = __builtin_bit_cast(f16x8, cw & 0xff00ff00u);
+          const f16x8 q_hi = qh[j] * s_hi;
+          const f16x8 q_lo = qh[j] * (s_all - s_hi);
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, q_hi, sc[mt], 0, 0, 0);
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, q_lo, sc[mt], 0, 0, 0);
+        }
+      }
+      if (MODE == 1) {
+        const uint2 kw = tl.ks[mt];
+        sc[mt][0] *= h2f(kw.x);
+        sc[mt][1] *= h2f(kw.x >> 16);
+        sc[mt][2] *= h2f(kw.y);
+        sc[mt][3] *= h2f(kw.y >> 16);
+      }
+    }
+    if (partial) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (t0 + 16 * mt + 4 * q4 + i >= end) sc[mt][i] = kNegInf;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx *= a.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    f16x8 pop;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int mt = i >> 2, e = i & 3;
+      const float p = fast_exp2(fmaf(sc[mt][e], a.scale_log2, -m_run));
+      psum += p;
+      const uint32_t vsw = (e < 2) ? tl.vs[mt].x : tl.vs[mt].y;
+      pop[i] = (_Float16)(p * h2f(vsw >> (16 * (e & 1))));
+    }
+    l_run += psum;
+
+    wave_sync();  // the wave's V tile is in LDS
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      f16x8 vop;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vop[i] = vw[(16 * (i >> 2) + 4 * q4 + (i & 3)) * VP + 16 * dt + r];
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, acc[dt], 0, 0, 0);
+    }
+    wave_sync();
+  };
+
+  Int8Tile<D> ring[NB];
+  if (mine >= 2 * NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) load_tile(j, ring[j]);
+    int k0 = 0;
+    for (; k0 + 2 * NB <= mine; k0 += NB) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        process_tile(tile_t0(k0 + j), ring[j]);
+        load_tile(k0 + j + NB, ring[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      process_tile(tile_t0(k0 + j), ring[j]);
+      if (k0 + j + NB < mine) load_tile(k0 + j + NB, ring[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      if (k0 + NB + j < mine) process_tile(tile_t0(k0 + NB + j), ring[j]);
+  } else {
+    for (int k = 0; k < mine; ++k) {
+      load_tile(k, ring[0]);
+      process_tile(tile_t0(k), ring[0]);
+    }
+  }
+
+  mfma_epilogue<D, false>(a, s, h, sp, nvalid, m_run, l_run, acc, smem, &last_flag);
+}
+
+template <typename Kernel>
+static int launch_int8(Kernel k, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k, grid, dim3(kThreads), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIPA_EHIP, "int8 decode launch failed: %s", hipGetErrorString(e));
+  return SIPA_OK;
+}
+
+template <int D, int MODE>
+static int launch_int8_depth(int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  switch (nb) {
+    case 1: return launch_int8(decode_mfma_int8<D, MODE, 1>, grid, a, st);
+    default: return launch_int8(decode_mfma_int8<D, MODE, 2>, grid, a, st);
+  }
+}
+
+// mode: 1, 2, or 3 (mode 2 with a zero block stride of the channel scales).
+int launch_mfma_int8(int D, int mode, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  if (D == 64) {
+    switch (mode) {
+      case 1: return launch_int8_depth<64, 1>(nb, grid, a, st);
+      case 2: return launch_int8_depth<64, 2>(nb, grid, a, st);
+      default: return launch_int8_depth<64, 3>(nb, grid, a, st);
+    }
+  }
+  switch (mode) {
+    case 1: return launch_int8_depth<128, 1>(nb, grid, a, st);
+    case 2: return launch_int8_depth<128, 2>(nb, grid, a, st);
+    default: return launch_int8_depth<128, 3>(nb, grid, a, st);
+  }
+}
+
+}  // namespace sipa

@@ -59,3 +59,16 @@ def compact_pool(k: torch.Tensor, tables: list[list[int]], lengths: list[int], B
     idx = torch.tensor(used, dtype=torch.int64, device=k.device)
     small = k.index_select(1, idx).float().cpu().numpy()
     return small, [[remap[b] for b in t[:-(-n // B)]] for t, n in zip(tables, lengths)]
+
+
+def bf16_half_ulp(x: np.ndarray) -> np.ndarray:
+    """Half a bf16 unit in the last place at |x| (8 significant bits): the rounding error any bf16 output may
+    carry on top of the arithmetic's own error."""
+    ax = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(ax)) - 8)
+
+
+def bf16_error_beyond_rounding(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| - half_ulp_bf16(got): how far a bf16 output lies from the reference beyond its own output
+    rounding (<= the error of the fp32 result before rounding)."""
+    return float((np.abs(got - ref) - bf16_half_ulp(got)).max())
