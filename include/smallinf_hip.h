@@ -110,13 +110,14 @@ int32_t sipa_device_cu_count(int32_t device);
 
 /*
  * Splits per sequence for a call. Replaces the reference's 20-SM policy choose_splits (reference
- * engine/triton_decode.py:164-172) with one sized from the CU count: enough (sequence, KV head, split)
- * workgroups to fill every CU several times, each split at most SIPA_MAX_CHUNK tokens so that a long
- * sequence in a ragged batch is spread over many CUs.
+ * engine/triton_decode.py:164-172) with one sized from the CU count: about one (sequence, KV head, split)
+ * workgroup per CU, ceil(cu_count / (num_seqs * num_kv_heads)) splits, but no split under 256 tokens of
+ * max_context and none over 2048 (so a long sequence in a ragged batch is spread over many CUs).
  */
 int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count);
 
-/* Tokens per split for a call with num_splits splits (a multiple of the 32-token tile). */
+/* Tokens per split for a call with num_splits splits: ceil(max_context / num_splits) rounded up to a multiple
+ * of 64 tokens, at most 32768. Calls launch ceil(max_context / chunk) splits, which may be fewer than asked. */
 int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits);
 
 /* Workspace bytes sipa_decode needs for these sizes (0 when num_splits resolves to 1). */

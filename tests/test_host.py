@@ -1,0 +1,326 @@
+"""Host-side logic of the drop-in path on the CPU: block bookkeeping, per-forward metadata, the cache's write /
+gather on CPU pools, the INT8 staging plan, and pool budgets. Mirrors the reference's tests/test_block_manager.py,
+tests/test_paged.py:41-76,132-137 and tests/test_quant_cache.py:42-115; known answers come from
+tests/golden/reference_known_answers.json.
+"""
+
+import json
+import random
+from pathlib import Path
+
+import pytest
+import torch
+
+from engine.block_manager import BlockManager, OutOfBlocks
+from engine.config import QWEN2_5_0_5B, ModelConfig
+from engine.paged_cache import PagedKVCache, build_metadata
+from engine.quant_cache import QuantPagedKVCache, blocks_for_budget, kv_bytes_per_token
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+TINY = ModelConfig(vocab_size=97, hidden_size=32, intermediate_size=64, num_layers=2, num_q_heads=4,
+                   num_kv_heads=2, head_dim=16)
+
+
+# ---- block manager ------------------------------------------------------------------------------------------------
+
+def test_allocate_append_known_answer():
+    ka = GOLDEN["block_manager_allocate_append"]
+    m = BlockManager(ka["num_blocks"], ka["block_size"])
+    for op, seq, arg, *want in ka["ops"]:
+        if op == "allocate":
+            assert m.allocate(seq, arg) == want[0]
+            assert m.block_table(seq) == ka["table_after_first_allocate"]
+        elif op == "append_slot":
+            assert m.append_slot(seq) == arg
+        else:
+            assert m.block_table(seq) == ka["table_before_last_append"] and m.seq_len(seq) == 9
+            assert m.append_slots(seq, arg) == want[0]
+    m.check_invariants()
+
+
+def test_lifo_reuse_known_answer():
+    ka = GOLDEN["block_manager_lifo"]
+    m = BlockManager(ka["num_blocks"], ka["block_size"])
+    for s in range(4):
+        m.allocate(s, 8)
+    assert [m.block_table(s)[0] // 2 for s in range(4)] == ka["allocate_each_8_tokens"]
+    for s in ka["free"]:
+        m.free(s)
+    m.allocate(9, 16)
+    t = m.block_table(9)
+    assert sorted(t) == ka["then_allocate_16_tokens_table_sorted"] and t != sorted(t)
+    assert t == [6, 7, 2, 3]  # sequence 3's blocks first (freed last), each sequence's in its old table order
+
+
+def test_zero_length_and_errors():
+    m = BlockManager(num_blocks=2, block_size=4)
+    assert m.allocate(0, 0) == [] and m.block_table(0) == []
+    assert m.append_slots(0, 8) == list(range(8))
+    with pytest.raises(OutOfBlocks):
+        m.append_slot(0)
+    with pytest.raises(OutOfBlocks):
+        m.allocate(1, 1)
+    with pytest.raises(ValueError):
+        m.allocate(0, 1)
+    assert m.seq_len(0) == 8 and m.num_free_blocks() == 0
+    assert not m.can_allocate(1) and not m.can_append(0)
+    m.free(0)
+    assert m.can_allocate(8) and not m.can_allocate(8, watermark_blocks=1)
+    m.check_invariants()
+
+
+def test_check_invariants_catches_corruption():
+    m = BlockManager(num_blocks=4, block_size=4)
+    m.allocate(0, 4)
+    m._free.append(m.block_table(0)[0])
+    with pytest.raises(AssertionError):
+        m.check_invariants()
+    m = BlockManager(num_blocks=4, block_size=4)
+    m._free.pop()
+    with pytest.raises(AssertionError):
+        m.check_invariants()
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_randomized_no_leaks(seed):
+    """Random allocate / append / free, some failing: bookkeeping stays consistent, live slots are disjoint and
+    match a shadow model, and freeing everything returns every block exactly once."""
+    rng = random.Random(seed)
+    B = rng.choice([1, 4, 16])
+    m = BlockManager(num_blocks=rng.randint(4, 64), block_size=B)
+    shadow: dict[int, list[int]] = {}
+    next_id = 0
+    for _ in range(400):
+        op = rng.random()
+        if op < 0.3 or not shadow:
+            n = rng.randint(0, 3 * B)
+            if m.can_allocate(n):
+                shadow[next_id] = m.allocate(next_id, n)
+            else:
+                with pytest.raises(OutOfBlocks):
+                    m.allocate(next_id, n)
+            next_id += 1
+        elif op < 0.8:
+            s, n = rng.choice(list(shadow)), rng.choice([1, 1, 1, rng.randint(1, 2 * B)])
+            if m.can_append(s, n):
+                shadow[s] += m.append_slots(s, n)
+            else:
+                before = (m.block_table(s), m.num_free_blocks())
+                with pytest.raises(OutOfBlocks):
+                    m.append_slots(s, n)
+                assert (m.block_table(s), m.num_free_blocks()) == before
+        else:
+            s = rng.choice(list(shadow))
+            m.free(s)
+            del shadow[s]
+        m.check_invariants()
+        live = [x for slots in shadow.values() for x in slots]
+        assert len(live) == len(set(live))
+        for s, slots in shadow.items():
+            assert m.slots(s, 0, m.seq_len(s)) == slots
+    for s in list(shadow):
+        m.free(s)
+    assert sorted(m._free) == list(range(m.num_blocks))
+
+
+# ---- metadata -----------------------------------------------------------------------------------------------------
+
+def test_metadata_known_answer():
+    ka = GOLDEN["metadata_packed_batch"]
+    m = BlockManager(ka["num_blocks"], ka["block_size"])
+    for op, seq, n in ka["setup"]:
+        getattr(m, op)(seq, n)
+    meta = build_metadata(m, [tuple(b) for b in ka["batch"]], "cpu")
+    assert meta.num_tokens == ka["num_tokens"] and meta.query_starts == ka["query_starts"]
+    assert meta.context_lens == ka["context_lens"] and meta.positions.tolist() == ka["positions"]
+    assert meta.slot_mapping.tolist() == ka["slot_mapping"] and meta.slots_cpu == ka["slot_mapping"]
+    assert meta.slot_blocks.tolist() == ka["slot_blocks"] and meta.slot_offsets.tolist() == ka["slot_offsets"]
+    assert [b.tolist() for b in meta.block_ids] == ka["block_ids"] and meta.block_ids_cpu == ka["block_ids"]
+    assert meta.block_tables.tolist() == ka["block_tables"] and meta.block_tables.dtype == torch.int32
+    assert meta.context_lens_t.tolist() == ka["context_lens_t"] and meta.context_lens_t.dtype == torch.int32
+    assert meta.last_token_indices.tolist() == ka["last_token_indices"]
+    with pytest.raises(ValueError):
+        build_metadata(m, [(0, 8, 1)], "cpu")  # position 8 has no slot yet
+
+
+def fragmented(num_blocks, B, seed=0):
+    m = BlockManager(num_blocks, B)
+    for s in range(num_blocks):
+        m.allocate(100 + s, B)
+    for s in random.Random(seed).sample(range(num_blocks), num_blocks):
+        m.free(100 + s)
+    return m
+
+
+def test_write_then_gather_roundtrip():
+    """K/V written at shuffled slots come back from gather() in position order (CPU pool, torch indexing)."""
+    m = fragmented(10, 4)
+    cache = PagedKVCache(TINY, 10, 4, "cpu", torch.float64)
+    m.allocate(7, 11)
+    meta = build_metadata(m, [(7, 0, 11)], "cpu")
+    cache.begin(11, meta)
+    k = torch.randn(11, 2, 16, dtype=torch.float64)
+    v = torch.randn_like(k)
+    cache.write(1, k, v)
+    gk, gv = cache.gather(1, 0)
+    assert torch.equal(gk, k.transpose(0, 1)) and torch.equal(gv, v.transpose(0, 1))
+    t = m.block_table(7)
+    assert any(b != a + 1 for a, b in zip(t, t[1:]))
+
+
+def test_kernel_backend_refuses_cpu_pool():
+    """The HIP backends run only on GPU pools: a CPU pool fails loudly instead of falling back."""
+    m = BlockManager(4, 4)
+    m.allocate(0, 3)
+    for backend in ("hip", "triton"):
+        cache = PagedKVCache(TINY, 4, 4, "cpu", torch.float32, attn_backend=backend)
+        with pytest.raises(ValueError, match="GPU"):
+            cache.begin(3, build_metadata(m, [(0, 0, 3)], "cpu"))
+    with pytest.raises(ValueError):
+        PagedKVCache(TINY, 4, 4, "cpu", torch.float32, attn_backend="flash")
+
+
+def test_gather_backend_attend_matches_oracle():
+    """attend() on the gather backend for a mixed prefill + decode batch equals causal softmax attention."""
+    from oracle import paged_ref
+
+    torch.manual_seed(1)
+    m = fragmented(16, 4)
+    cache = PagedKVCache(TINY, 16, 4, "cpu", torch.float64)
+    m.allocate(0, 9)
+    m.allocate(1, 5)
+    meta = build_metadata(m, [(0, 0, 9), (1, 0, 5)], "cpu")
+    cache.begin(14, meta)
+    k, v = torch.randn(14, 2, 16, dtype=torch.float64), torch.randn(14, 2, 16, dtype=torch.float64)
+    cache.write(0, k, v)
+    m.append_slot(0)
+    meta = build_metadata(m, [(0, 9, 1), (1, 3, 2)], "cpu")  # one decode row, one 2-token chunk (rewrite 3, 4)
+    cache.begin(3, meta)
+    k2, v2 = torch.randn(3, 2, 16, dtype=torch.float64), torch.randn(3, 2, 16, dtype=torch.float64)
+    cache.write(0, k2, v2)
+    q = torch.randn(3, 4, 16, dtype=torch.float64)
+    out = cache.attend(0, q, meta.positions, 0.25).view(3, 4, 16)
+    keys0 = torch.cat([k[:9], k2[:1]]).transpose(0, 1).numpy()
+    vals0 = torch.cat([v[:9], v2[:1]]).transpose(0, 1).numpy()
+    torch.testing.assert_close(out[0], torch.from_numpy(paged_ref.attend_one(q[0].numpy(), keys0, vals0, 0.25)))
+    keys1 = torch.cat([k[9:12], k2[1:]]).transpose(0, 1).numpy()
+    vals1 = torch.cat([v[9:12], v2[1:]]).transpose(0, 1).numpy()
+    for r, n in ((1, 4), (2, 5)):  # causal: row at position p sees keys 0..p
+        want = paged_ref.attend_one(q[r].numpy(), keys1[:, :n], vals1[:, :n], 0.25)
+        torch.testing.assert_close(out[r], torch.from_numpy(want))
+
+
+# ---- INT8 caches ----------------------------------------------------------------------------------------------------
+
+def make_quant_cache(fmt, num_blocks=24, B=4):
+    m = BlockManager(num_blocks, B)
+    return m, QuantPagedKVCache(TINY, num_blocks, B, "cpu", torch.float32, "gather", fmt, m, n_stage=32)
+
+
+def write_chunks(m, cache, seq, k, v, chunks, layer=0):
+    pos = m.seq_len(seq) if seq in m.seq_ids() else 0
+    if seq not in m.seq_ids():
+        m.allocate(seq, 0)
+    i = 0
+    for n in chunks:
+        m.append_slots(seq, n)
+        meta = build_metadata(m, [(seq, pos, n)], "cpu")
+        cache.begin(n, meta)
+        cache.write(layer, k[i:i + n], v[i:i + n])
+        pos, i = pos + n, i + n
+    return meta
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int8-kchannel"])
+def test_quant_roundtrip_across_chunks(fmt):
+    """Gathered K/V are within half a quantization step of the originals through chunked writes that cross block
+    boundaries; format B's partial last block is only bf16-rounded."""
+    torch.manual_seed(0)
+    n = 23
+    k = torch.randn(n, 2, 16) * torch.rand(1, 2, 16) * 4
+    v = torch.randn(n, 2, 16)
+    m, cache = make_quant_cache(fmt)
+    write_chunks(m, cache, 0, k, v, [1, 6, 9, 7])
+    gk, gv = cache.gather(0, 0)
+    assert gk.shape == (2, n, 16)
+    v_step = v.abs().amax(-1).t()[..., None] / 127
+    assert ((gv - v.transpose(0, 1)).abs() <= v_step * 0.51 + 1e-6).all()
+    kt = k.transpose(0, 1)
+    if fmt == "int8":
+        k_step = k.abs().amax(-1).t()[..., None] / 127
+        assert ((gk - kt).abs() <= k_step * 0.51 + 1e-6).all()
+    else:
+        blocks = kt[:, :20].reshape(2, 5, 4, 16).to(torch.bfloat16).float()
+        step = blocks.abs().amax(2, keepdim=True) / 127
+        assert ((gk[:, :20].reshape(2, 5, 4, 16) - blocks).abs() <= step * 0.51 + 1e-6).all()
+        assert torch.equal(gk[:, 20:], kt[:, 20:].to(torch.bfloat16).float())
+
+
+def test_kchannel_blocks_do_not_depend_on_chunking():
+    """A block's int8 codes and channel scales are the same whether it was staged token by token or written whole."""
+    torch.manual_seed(2)
+    k, v = torch.randn(16, 2, 16) * 3, torch.randn(16, 2, 16)
+    pools = []
+    for chunks in ([16], [1] * 16, [3, 5, 8], [4, 4, 4, 4]):
+        m, cache = make_quant_cache("int8-kchannel")
+        write_chunks(m, cache, 0, k, v, chunks)
+        t = m.block_table(0)
+        pools.append((cache.k[0][:, t].clone(), cache.k_scale[0][:, t].clone()))
+    for kq, ks in pools[1:]:
+        assert torch.equal(kq, pools[0][0]) and torch.equal(ks, pools[0][1])
+
+
+def test_staging_slots_follow_partial_blocks():
+    """Format B keeps a staging slot exactly for each live sequence's partial last block over random appends and
+    frees: no leaks, no double assignment."""
+    rng = random.Random(0)
+    m, cache = make_quant_cache("int8-kchannel", num_blocks=64, B=4)
+    live = {}
+    for step in range(300):
+        if live and rng.random() < 0.2:
+            s = rng.choice(list(live))
+            m.free(s)
+            del live[s]
+        else:
+            s = rng.choice(list(live)) if live and rng.random() < 0.7 else 1000 + step
+            n = rng.randint(1, 9)
+            if (s in live and not m.can_append(s, n)) or (s not in live and not m.can_allocate(n)):
+                continue
+            write_chunks(m, cache, s, torch.randn(n, 2, 16), torch.randn(n, 2, 16), [n])
+            live[s] = m.seq_len(s)
+        partial = {m.block_table(s)[-1] for s, length in live.items() if length % 4}
+        assert set(cache._stage_of) == partial
+        assert len(cache._free_stage) + len(cache._stage_of) == cache.n_stage
+        assert len(set(cache._free_stage)) == len(cache._free_stage)
+    for s in list(live):
+        m.free(s)
+    assert cache._stage_of == {} and len(cache._free_stage) == cache.n_stage
+
+
+def test_bytes_and_budget():
+    ka = GOLDEN["budgets"]
+    cfg = ModelConfig(**ka["qwen2_5_0_5b"])
+    assert cfg == QWEN2_5_0_5B
+    for fmt, want in ka["kv_bytes_per_token"].items():
+        assert kv_bytes_per_token(cfg, fmt) == want
+    gib2 = 2 * 2 ** 30
+    assert PagedKVCache.blocks_for_budget(cfg, gib2, 16) == ka["blocks_2_gib"]["bf16"]
+    assert blocks_for_budget(cfg, "bf16", gib2, 16) == ka["blocks_2_gib"]["bf16"]
+    assert blocks_for_budget(cfg, "int8", gib2, 16) == ka["blocks_2_gib"]["int8"]
+    assert blocks_for_budget(cfg, "int8-kchannel", gib2, 16, n_stage=128) > \
+        ka["blocks_2_gib"]["int8-kchannel_n_stage_128_more_than"]
+
+
+def test_torch_quantizer_bounds():
+    """engine.quant (the CPU-pool quantizer) keeps the reference's bounds: per-channel beats per-token on
+    outlier channels (reference tests/test_quant.py:39-51)."""
+    from engine.quant import dequantize, quantize_per_channel, quantize_per_token, relative_error
+
+    torch.manual_seed(0)
+    x = torch.randn(64, 128)
+    x[:, :4] *= 50
+    qt, st = quantize_per_token(x)
+    qc, sc = quantize_per_channel(x, dim=0)
+    e_tok = relative_error(x, dequantize(qt, st[:, None]))
+    e_ch = relative_error(x, dequantize(qc, sc[None, :]))
+    assert e_ch < e_tok / 3
