@@ -10,11 +10,13 @@ the library binds to, so torch's device pointers and streams are valid in our la
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch  # noqa: F401  (load torch's HIP runtime before the library; see the module docstring)
 
-LIB_PATH = Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so"
+# SIPA_LIB overrides the location (for copies of these modules placed inside another package).
+LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
 ABI_VERSION = 1
 
 # element types (SIPA_F32 ...)

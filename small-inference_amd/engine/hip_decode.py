@@ -2,13 +2,14 @@
 engine/triton_decode.py (paged_decode_attention, choose_splits, QuantKV; reference :164-238).
 
 One query token per sequence, K/V read in place from the [Hkv, N, B, D] pool of one layer through the block
-tables. The split count comes from the GPU's CU count instead of the reference's 20-SM constants: enough
-(sequence, KV head, split) workgroups to fill the 256 CUs several times over, splits of at most 512 tokens so that
-ragged batches balance. A split past a sequence's end does no work; the last split workgroup of a (sequence, KV
-head) to finish merges the partials (combine="fused"), or a second kernel does (combine="kernel").
+tables. The split count comes from the GPU's CU count instead of the reference's 20-SM constants: about one
+(sequence, KV head, split) workgroup per CU, splits of 256 to 2048 tokens, so that long sequences in ragged
+batches spread over many CUs. A split past a sequence's end does no work; the last split workgroup of a
+(sequence, KV head) to finish merges the partials (combine="fused"), or a second kernel does (combine="kernel").
 
-Kernels: bf16 pools with 16-token blocks and head_dim 64/128 run the MFMA kernel; everything else (fp32 models,
-other block sizes or head dims, and both INT8 modes) runs the VALU kernel. impl="valu" / "mfma" forces one.
+Kernels: bf16 queries with 16-token blocks and head_dim 64/128 run the MFMA kernels (bf16 pools, and both INT8
+formats with fp16 or constant scales); everything else (fp32 models, other block sizes or head dims) runs the
+VALU kernel. impl="valu" / "mfma" forces one.
 """
 
 from __future__ import annotations

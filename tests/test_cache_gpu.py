@@ -1,0 +1,105 @@
+"""The drop-in interface end to end on the GPU: begin / write / attend of PagedKVCache and QuantPagedKVCache with
+attn_backend "triton" (the reference engine's default name, served by the HIP kernels) over mixed batches of
+decode rows and prefill chunks, as engine/model.py:145-146 drives it (reference tests/test_paged.py:186-205).
+
+Checked against the oracle: each row's softmax attention over the cache contents gathered back to fp32 (for the
+INT8 caches, the dequantized contents), causal within a chunk. Tolerances: fp32 caches 1e-5; bf16 decode rows
+(the HIP kernel) 8e-3 max-abs; bf16 prefill rows 3e-2, since they run the reference's gather path, which computes
+scores and probabilities in the model dtype (engine/attention.py).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import fragmented_manager
+from engine.config import ModelConfig
+from engine.paged_cache import PagedKVCache, build_metadata
+from engine.quant_cache import QuantPagedKVCache
+from oracle import paged_ref
+
+pytestmark = pytest.mark.gpu
+
+CFG = {64: ModelConfig(vocab_size=97, hidden_size=896, intermediate_size=64, num_layers=2, num_q_heads=14,
+                       num_kv_heads=2, head_dim=64),
+       128: ModelConfig(vocab_size=97, hidden_size=1536, intermediate_size=64, num_layers=2, num_q_heads=12,
+                        num_kv_heads=2, head_dim=128)}
+
+
+def forward(m, cache, batch, layer, gen, dtype):
+    """One forward over batch [(seq, start, n)]: metadata, begin, write random k/v, attend random q."""
+    cfg = cache.cfg
+    meta = build_metadata(m, batch, "cuda")
+    T = meta.num_tokens
+    cache.begin(T, meta)
+    k = torch.randn(T, cfg.num_kv_heads, cfg.head_dim, generator=gen).to("cuda", dtype)
+    v = torch.randn(T, cfg.num_kv_heads, cfg.head_dim, generator=gen).to("cuda", dtype)
+    q = torch.randn(T, cfg.num_q_heads, cfg.head_dim, generator=gen).to("cuda", dtype)
+    cache.write(layer, k, v)
+    out = cache.attend(layer, q, meta.positions, cfg.head_dim ** -0.5)
+    return meta, q, out
+
+
+def reference(cache, meta, q, layer):
+    """Oracle: per sequence, gather the cache back (dequantized, fp32) and attend causally."""
+    cfg, d = cache.cfg, cache.cfg.head_dim
+    saved, cache.dtype = cache.dtype, torch.float32
+    try:
+        rows = []
+        for i in range(meta.num_seqs):
+            k, v = cache.gather(layer, i)
+            k, v = k.float().cpu().numpy(), v.float().cpu().numpy()
+            a, b = meta.query_starts[i], meta.query_starts[i + 1]
+            ctx = meta.context_lens[i]
+            for r in range(a, b):
+                n = ctx - (b - 1 - r)  # causal: the row at position ctx - 1 - (b - 1 - r) sees n keys
+                rows.append(paged_ref.attend_one(q[r].float().cpu().numpy(), k[:, :n], v[:, :n], d ** -0.5,
+                                                 np.float32))
+    finally:
+        cache.dtype = saved
+    return np.stack(rows).reshape(len(rows), cfg.num_q_heads * d)
+
+
+def run_mixed(make_cache, dtype, D, seed):
+    gen = torch.Generator().manual_seed(seed)
+    m = fragmented_manager(256, 16, gen)
+    cache = make_cache(m)
+    print(f"case {type(cache).__name__} {getattr(cache, 'fmt', 'model')} {dtype} D={D} seed={seed}", flush=True)
+    for layer in range(2):
+        for s, n in ((1, 70), (2, 300), (3, 16)):
+            if s not in m.seq_ids():
+                m.allocate(s, n)
+        forward(m, cache, [(1, 0, 70), (2, 0, 300), (3, 0, 16)], layer, gen, dtype)
+    for step in range(3):  # decode steps mixed with a prefill chunk of a new sequence
+        for s in (1, 2, 3):
+            m.append_slot(s)
+        batch = [(1, m.seq_len(1) - 1, 1), (2, m.seq_len(2) - 1, 1), (3, m.seq_len(3) - 1, 1)]
+        if step == 1:
+            m.allocate(4, 0)
+            m.append_slots(4, 21)
+            batch.insert(1, (4, 0, 21))
+        for layer in range(2):
+            meta, q, out = forward(m, cache, batch, layer, gen, dtype)
+            torch.cuda.synchronize()
+            ref = reference(cache, meta, q, layer)
+            err = np.abs(out.float().cpu().numpy() - ref).max(axis=1)
+            chunk = {r for a, b in zip(meta.query_starts, meta.query_starts[1:]) if b - a > 1 for r in range(a, b)}
+            dec = np.array([r not in chunk for r in range(meta.num_tokens)])
+            tol_dec, tol_chunk = (1e-5, 1e-5) if dtype == torch.float32 else (8e-3, 3e-2)
+            assert err[dec].max() <= tol_dec, f"step {step} layer {layer}: decode rows {err[dec].max():.3e}"
+            if (~dec).any():
+                assert err[~dec].max() <= tol_chunk, f"step {step} layer {layer}: chunk {err[~dec].max():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_cache_mixed_batches(dtype, D):
+    run_mixed(lambda m: PagedKVCache(CFG[D], 256, 16, "cuda", dtype, attn_backend="triton"), dtype, D, seed=D)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int8-kchannel"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_quant_cache_mixed_batches(fmt, dtype, D):
+    run_mixed(lambda m: QuantPagedKVCache(CFG[D], 256, 16, "cuda", dtype, "triton", fmt, m, n_stage=16),
+              dtype, D, seed=7 + D)
