@@ -591,6 +591,8 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
 
   int chunk = 0;
   const int splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, &chunk);
+  SIPA_CHECK((int64_t)(Hq / Hkv) * splits * D * 4 < INT32_MAX, SIPA_EUNSUPPORTED,
+             "%d splits: a KV head's partial rows exceed 2 GiB", splits);
 
   DecodeArgs a;
   memset(&a, 0, sizeof(a));

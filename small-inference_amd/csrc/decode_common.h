@@ -52,9 +52,10 @@ __device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, in
     ((uint16_t*)a.out)[i] = f32_to_bf16_bits(v);
 }
 
-// Partials that another workgroup of the same launch merges are written and read with agent-scope atomic
-// accesses: on gfx950 these are global_store / global_load with the sc1 bit, which write through to and read from
-// the point of coherence of all XCDs. Ordering then needs only the completion of this workgroup's stores
+// Partials that another workgroup of the same launch merges are written and read with agent-scope accesses:
+// relaxed agent-scope atomics, which gfx950 executes as global_store / global_load with the sc1 bit, or buffer
+// loads and stores with that same bit (partial_rows below); both write through to and read from the point of
+// coherence of all XCDs. Ordering then needs only the completion of this workgroup's stores
 // (s_waitcnt vmcnt(0)) before its counter increment, not an agent-scope fence, which would write back and
 // invalidate the whole L2 of the XCD once per workgroup.
 __device__ __forceinline__ void store_coherent(float* p, float v) {
@@ -65,44 +66,98 @@ __device__ __forceinline__ float load_coherent(float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). COHERENT: the
-// partials were written by other workgroups of this launch (the fused merge). Up to 8 splits are loaded per
-// round (one memory round trip) and merged online, so the usual 2..8 splits cost a single round trip.
+template <bool OUT_F32>
+__device__ __forceinline__ void store_out4(const DecodeArgs& a, int s, int hq, int d0, f32x4 v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_out<OUT_F32>(a, s, hq, d0 + i, v[i]);
+}
+
+// The partial rows of one (s, h): [G][splits][D] floats from part + ((s Hq + h G) splits) D, as a raw buffer
+// resource (gfx9 descriptor word 3). Loads and stores through it with the sc1 cache-policy bit (aux 16) are
+// agent-coherent, like the relaxed agent-scope atomics above, but move 16 bytes per lane in one instruction.
+constexpr int kAuxSc1 = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rows(const DecodeArgs& a, int s, int h, int D) {
+  float* base = a.part + ((int64_t)s * a.Hq + (int64_t)h * a.G) * a.splits * D;
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, a.G * a.splits * D * 4, 0x00020000);
+}
+
+// One round of the merge: up to KB splits j0 .. j0 + KB - 1 of row0, every load issued before the first is used.
+// Entries past nvalid re-read the last split and get weight 0 (branch-free).
+template <int KB, int D, bool COHERENT>
+__device__ __forceinline__ void combine_round(const DecodeArgs& a, __amdgpu_buffer_rsrc_t rows, int64_t row0,
+                                              int g, int c, int j0, int nvalid, float& M, float& den, f32x4& num) {
+  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
+  float mj[KB], lj[KB];
+  f32x4 pj[KB];
+#pragma unroll
+  for (int u = 0; u < KB; ++u) {
+    const int j = min(j0 + u, nvalid - 1);
+    mj[u] = ld(a.pm + row0 + j);
+    lj[u] = ld(a.pl + row0 + j);
+    if (COHERENT)
+      pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, ((g * a.splits + j) * D + 4 * c) * 4, 0, kAuxSc1);
+    else
+      pj[u] = *(const f32x4*)(a.part + (row0 + j) * D + 4 * c);
+  }
+#pragma unroll
+  for (int u = 0; u < KB; ++u)
+    if (j0 + u >= nvalid) mj[u] = kNegInf;
+  float mb = M;
+#pragma unroll
+  for (int u = 0; u < KB; ++u) mb = fmaxf(mb, mj[u]);
+  const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf)
+  den *= rescale;
+  num *= rescale;
+#pragma unroll
+  for (int u = 0; u < KB; ++u) {
+    const float w = fast_exp2(mj[u] - mb);  // 0 for the padding entries (m = -inf)
+    den += w * lj[u];
+    num += w * pj[u];
+  }
+  M = mb;
+}
+
+// Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). One thread per
+// (query head, 4-channel quad), so all loads of a round are in flight together; 4 (nvalid <= 4) or 8 splits per
+// round, merged online, so the usual 2..8 splits cost one memory round trip. COHERENT: the partials were written
+// by other workgroups of this launch (the fused merge).
 template <int D, bool OUT_F32, bool COHERENT>
 __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
-  constexpr int kBatch = 8;
+  constexpr int Q = D / 4;
   const int G = a.G;
-  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-    const int g = idx / D, d = idx % D;
+  const __amdgpu_buffer_rsrc_t rows = partial_rows(a, s, h, D);
+  for (int idx = threadIdx.x; idx < G * Q; idx += kThreads) {
+    const int g = idx / Q, c = idx % Q;
     const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
-    float M = kNegInf, num = 0.f, den = 0.f;
-    for (int j0 = 0; j0 < nvalid; j0 += kBatch) {
-      float mj[kBatch], lj[kBatch], pj[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int j = j0 + u;
-        const bool ok = j < nvalid;
-        mj[u] = ok ? ld(a.pm + row0 + j) : kNegInf;
-        lj[u] = ok ? ld(a.pl + row0 + j) : 0.f;
-        pj[u] = ok ? ld(a.part + (row0 + j) * D + d) : 0.f;
-      }
-      float mb = M;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mj[u]);
-      const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf)
-      num *= rescale;
-      den *= rescale;
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const float w = fast_exp2(mj[u] - mb);  // 0 for the padding entries (m = -inf)
-        num += w * pj[u];
-        den += w * lj[u];
-      }
-      M = mb;
+    float M = kNegInf, den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    if (nvalid <= 4) {
+      combine_round<4, D, COHERENT>(a, rows, row0, g, c, 0, nvalid, M, den, num);
+    } else {
+      for (int j0 = 0; j0 < nvalid; j0 += 8) combine_round<8, D, COHERENT>(a, rows, row0, g, c, j0, nvalid, M, den, num);
     }
-    store_out<OUT_F32>(a, s, h * G + g, d, num / den);
+    store_out4<OUT_F32>(a, s, h * G + g, 4 * c, num / den);
   }
+}
+
+// After this workgroup's partial stores are issued: once they have completed (reached the point of coherence),
+// count the partial; the workgroup that brings the count of (s, h) to nvalid merges every partial and resets the
+// counter for the next launch.
+template <int D, bool OUT_F32>
+__device__ void publish_and_merge(const DecodeArgs& a, int s, int h, int nvalid, int* last_flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = (prev == nvalid - 1);
+  }
+  __syncthreads();
+  if (!*last_flag) return;
+  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge the four waves' states (ms, ls [4][16], accs [4][16][D] in LDS, after a barrier) and write the output
@@ -145,20 +200,7 @@ __device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nval
     }
   }
   if (nvalid == 1 || !a.fused) return;
-  // This workgroup's partial has reached the coherence point once its stores complete; then count it. The
-  // workgroup that brings the count to nvalid merges every partial of (s, h) and resets the counter.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    *last_flag = (prev == nvalid - 1);
-  }
-  __syncthreads();
-  if (!*last_flag) return;
-  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  publish_and_merge<D, OUT_F32>(a, s, h, nvalid, last_flag);
 }
 
 // ---- MFMA kernels --------------------------------------------------------------------------------------------
@@ -169,7 +211,8 @@ template <int D>
 struct MfmaSmem {
   static constexpr int kVPitch = D + 8;                                // bf16 elements per LDS row of V
   static constexpr int kVBytes = kWaves * 32 * kVPitch * 2;            // per-wave [32 tok][D] V tiles
-  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * D) * 4;
+  static constexpr int kMergePitch = D + 4;                           // floats per LDS row of a wave's O^T
+  static constexpr int kMergeBytes = (2 * kWaves * kMaxGroup + kWaves * kMaxGroup * kMergePitch) * 4;
   static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
 };
 
@@ -209,27 +252,74 @@ __device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[k
 }
 
 // MFMA epilogue: each wave's softmax state (m_run per lane for head g = r, l_run partial per lane, acc in the
-// O^T accumulator layout: lane (r, q4) holds head r, channels 16 dt + 4 q4 + i) is merged through LDS and the
-// split finished (output, or partial + merge).
+// O^T accumulator layout: lane (r, q4) holds head r, channels 16 dt + 4 q4 + i) goes to LDS; then thread
+// (wave, r, q4) merges the four waves for head r and the channel quads 4 wave + q4 + 16 j, with all its LDS reads
+// in flight together, and writes the output (whole sequence in this workgroup) or the split partial.
 template <int D, bool OUT_F32>
 __device__ __forceinline__ void mfma_epilogue(const DecodeArgs& a, int s, int h, int sp, int nvalid, float m_run,
                                               float l_run, const f32x4 (&acc)[D / 16], char* smem,
                                               int* last_flag) {
+  constexpr int P = MfmaSmem<D>::kMergePitch;
+  constexpr int J = D / 64;  // channel quads per thread
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
   __syncthreads();  // every wave is done with its LDS tiles: the LDS becomes the merge buffer
-  float* ms = (float*)smem;
-  float* ls = ms + kWaves * kMaxGroup;
-  float* accs = ls + kWaves * kMaxGroup;
-  if (q4 == 0) {
-    ms[wave * kMaxGroup + r] = m_run;
-    ls[wave * kMaxGroup + r] = l_run;
-  }
+  float2* ml = (float2*)smem;                       // [kWaves][16] (m, l)
+  float* accs = (float*)(ml + kWaves * kMaxGroup);  // [kWaves][16][P]
+  if (q4 == 0) ml[wave * kMaxGroup + r] = float2{m_run, l_run};
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) *(f32x4*)(accs + (wave * kMaxGroup + r) * D + 16 * dt + 4 * q4) = acc[dt];
+  for (int dt = 0; dt < D / 16; ++dt) *(f32x4*)(accs + (wave * kMaxGroup + r) * P + 16 * dt + 4 * q4) = acc[dt];
   __syncthreads();
-  finish_split<D, OUT_F32>(a, s, h, sp, nvalid, ms, ls, accs, last_flag);
+  const int G = a.G;
+  if (r < G) {
+    float2 mw[kWaves];
+    f32x4 aw[J][kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = ml[w * kMaxGroup + r];
+#pragma unroll
+      for (int j = 0; j < J; ++j) aw[j][w] = *(const f32x4*)(accs + (w * kMaxGroup + r) * P + 4 * (4 * wave + q4 + 16 * j));
+    }
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[w].x);
+    float L = 0.f;
+    f32x4 O[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) O[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = (mw[w].x == kNegInf) ? 0.f : fast_exp2(mw[w].x - M);  // a wave with no tokens drops out
+      L += e * mw[w].y;
+#pragma unroll
+      for (int j = 0; j < J; ++j) O[j] += e * aw[j][w];
+    }
+    const int64_t row = ((int64_t)s * a.Hq + h * G + r) * a.splits + sp;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int d0 = 4 * (4 * wave + q4 + 16 * j);
+      if (nvalid == 1) {
+        store_out4<OUT_F32>(a, s, h * G + r, d0, O[j] / L);
+      } else if (a.fused) {
+        __builtin_amdgcn_raw_buffer_store_b128(O[j], partial_rows(a, s, h, D), ((r * a.splits + sp) * D + d0) * 4, 0,
+                                               kAuxSc1);
+      } else {
+        *(f32x4*)(a.part + row * D + d0) = O[j];
+      }
+    }
+    if (nvalid > 1 && wave == 0 && q4 == 0) {
+      if (a.fused) {
+        store_coherent(a.pm + row, M);
+        store_coherent(a.pl + row, L);
+      } else {
+        a.pm[row] = M;
+        a.pl[row] = L;
+      }
+    }
+  }
+  if (nvalid == 1 || !a.fused) return;
+  publish_and_merge<D, OUT_F32>(a, s, h, nvalid, last_flag);
 }
 
 // INT8 MFMA kernels (decode_int8.hip). mode: 1 per-token K scales, 2 per-(block, channel) K scales,
