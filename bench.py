@@ -53,7 +53,7 @@ class Decode:
     """A paged-decode workload: pools of `layers` layers on the GPU, one DecodePlan, algorithmic bytes per call."""
 
     def __init__(self, name, q, k, v, bt, ctx_t, lengths, scale, bytes_per_call, splits=None, quant=None,
-                 impl="auto", combine="fused", meta=None):
+                 impl="auto", combine="fused", meta=None, work_list="auto"):
         from engine.hip_decode import DecodePlan
 
         self.name, self.q, self.k, self.v, self.bt, self.ctx_t = name, q, k, v, bt, ctx_t
@@ -63,13 +63,16 @@ class Decode:
         self.out = torch.empty_like(q)
         # One plan per layer, each bound to its layer's pools and scales: a call is one ctypes call + one launch.
         self.plans = [DecodePlan(q, k[i], v[i], bt, ctx_t, scale, max(lengths), splits,
-                                 None if quant is None else quant[i], impl=impl, combine=combine)
+                                 None if quant is None else quant[i], impl=impl, combine=combine,
+                                 host_context_lens=list(lengths), work_list=work_list)
                       for i in range(self.layers)]
         self.plan = self.plans[0]
         self.k_ptrs = [k[i].data_ptr() for i in range(self.layers)]
         self.v_ptrs = [v[i].data_ptr() for i in range(self.layers)]
         self.out_ptr = self.out.data_ptr()
         self.meta = dict(meta or {}, splits=self.plan.splits, chunk=self.plan.chunk, impl=impl, combine=combine)
+        if self.plan.items is not None:
+            self.meta.update(work_items=int(self.plan.items.shape[0]), combine="fused")
 
     def call(self, i: int) -> None:
         layer = i % self.layers
@@ -126,7 +129,7 @@ def padded(tables: list[list[int]], lengths: list[int], B: int) -> torch.Tensor:
 
 
 def bf16_decode(name, lengths, N, Hq=14, Hkv=2, D=64, B=16, layers=8, seed=0, tables=None, splits=None,
-                impl="auto", combine="fused"):
+                impl="auto", combine="fused", work_list="auto"):
     """bf16 pools [layers, Hkv, N, B, D] ~ N(0, 1), q ~ N(0, 1), scale 1/sqrt(D)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     k = torch.randn(layers, Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
@@ -143,7 +146,7 @@ def bf16_decode(name, lengths, N, Hq=14, Hkv=2, D=64, B=16, layers=8, seed=0, ta
     ctx_t = torch.tensor(lengths, dtype=torch.int32, device="cuda")
     nbytes = 2 * Hkv * D * 2 * sum(lengths) + 2 * Hq * D * 2 * len(lengths)
     wl = Decode(name, q, k, v, bt, ctx_t, lengths, D ** -0.5, nbytes, splits, impl=impl, combine=combine,
-                meta={"batch": len(lengths), "context": max(lengths), "pool_blocks": N})
+                meta={"batch": len(lengths), "context": max(lengths), "pool_blocks": N}, work_list=work_list)
     wl.tables = tables
     return wl
 
@@ -378,11 +381,13 @@ def details(steps: int, warmup: int) -> dict:
     out["c1_1x1024"]["max_abs_vs_oracle"] = round(check_against_oracle(c1), 5)
     rng = np.random.default_rng(0)
     c3_lengths = np.clip(np.rint(rng.lognormal(math.log(600), 1.0, 256)), 16, 8192).astype(int).tolist()
-    c3 = bf16_decode("c3_ragged256", c3_lengths, 200_000, layers=4)
-    out["c3_ragged256"] = measure(c3, steps, warmup)
-    out["c3_ragged256"]["sum_context"] = int(sum(c3_lengths))
-    out["c3_ragged256"]["max_abs_vs_oracle_first32"] = round(check_against_oracle(c3), 5)
-    del c3
+    for key, wlist in (("c3_ragged256", "auto"), ("c3_ragged256_split_grid", "off")):
+        c3 = bf16_decode(key, c3_lengths, 200_000, layers=4, work_list=wlist)
+        out[key] = measure(c3, steps, warmup)
+        out[key]["sum_context"] = int(sum(c3_lengths))
+        out[key]["max_abs_vs_oracle_first32"] = round(check_against_oracle(c3), 5)
+        del c3
+        torch.cuda.empty_cache()
     torch.cuda.empty_cache()
     c4_lengths = [4096] * 64
     for fmt, f32s, key in (("int8", False, "c4b_int8_per_token"), ("int8-kchannel", False, "c4a_int8_kchannel"),

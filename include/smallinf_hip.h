@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 1
+#define SIPA_ABI_VERSION 2
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -100,6 +100,15 @@ typedef struct sipa_decode_params {
      zero again. Calls that share one workspace must be ordered (one stream). May be NULL when 1 split runs. */
   void* workspace;
   int64_t workspace_bytes;
+  /* Optional work list (fields read only when struct_size covers them): num_items > 0 launches one workgroup
+     per item instead of the (sequence, KV head, split) grid. Items are 8 int32 each, 16-byte aligned, in device
+     memory: {seq, kv_head, split, splits_of_pair, start, end, 0, 0}, the pair's tokens [start, end) and its
+     splits numbered 0 .. splits_of_pair - 1. num_splits must be the largest splits_of_pair (it sizes the
+     workspace); splits are always merged by the last-arriving workgroup. Built by sipa_build_work_list from the
+     host-side context lengths; a list that does not match context_lens gives wrong results (every access stays
+     in bounds). */
+  const int32_t* work_items;
+  int32_t num_items;
 } sipa_decode_params;
 
 int32_t sipa_abi_version(void);
@@ -125,6 +134,19 @@ int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32
                                     int32_t head_dim, int32_t num_splits);
 
 int32_t sipa_decode(const sipa_decode_params* p, void* stream);
+
+/*
+ * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,
+ * split)): every (sequence, KV head) pair is cut into ceil(ctx / piece) splits of near-equal length, piece about
+ * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, 256 .. 32768), and the items are
+ * ordered longest first, so the longest work starts first and consecutive workgroups spread over the XCDs.
+ * context_lens_host [num_seqs] (each >= 1) are the lengths the decode call will read. Writes at most capacity
+ * items (8 int32 each) to items_out and the largest split count of a pair to *max_splits; returns the number of
+ * items, or a negative SIPA_E* code (items_out may be NULL to ask for the count).
+ */
+int32_t sipa_build_work_list(const int32_t* context_lens_host, int32_t num_seqs, int32_t num_kv_heads,
+                             int32_t cu_count, int32_t items_per_cu, int32_t* items_out, int32_t capacity,
+                             int32_t* max_splits);
 
 /*
  * Per-token INT8 quantize-and-store (reference engine/triton_quant.py:24-39,61-71 and the quantizer

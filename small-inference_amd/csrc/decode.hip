@@ -39,6 +39,8 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <cstddef>
+#include <vector>
 
 #include "decode_common.h"
 
@@ -57,13 +59,13 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
 
   const WorkItem w = work_item(a);
   const int sp = w.sp, h = w.h, s = w.s;
-  const int start = sp * a.chunk;
+  const int start = w.start;
   const int G = a.G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
   int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(a, s, start, ids);
+  const int nb_spec = fetch_split_ids(a, s, start, w.end, ids);
   bf16x8 qop[KS];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
@@ -75,9 +77,9 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
     }
   }
   const int ctx = a.ctx[s];
-  if (start >= ctx) return;
-  const int end = min(start + a.chunk, ctx);
-  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
+  const int end = max(start, min(w.end, ctx));
+  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   commit_split_ids(nb_spec, ids, bids);
   __syncthreads();  // block ids staged
 
@@ -268,10 +270,10 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
   const WorkItem w = work_item(a);
   const int sp = w.sp, h = w.h, s = w.s;
   const int ctx = a.ctx[s];
-  const int start = sp * a.chunk;
-  if (start >= ctx) return;
-  const int end = min(start + a.chunk, ctx);
-  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  const int start = w.start;
+  if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
+  const int end = max(start, min(w.end, ctx));
+  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   const int G = a.G, B = a.B;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -547,6 +549,50 @@ static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int* chunk
   return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
 }
 
+extern "C" int32_t sipa_build_work_list(const int32_t* ctx, int32_t S, int32_t Hkv, int32_t cu_count,
+                                        int32_t items_per_cu, int32_t* items, int32_t capacity,
+                                        int32_t* max_splits) {
+  SIPA_CHECK(ctx != nullptr && S >= 0 && Hkv > 0, SIPA_EINVAL, "work list: bad arguments");
+  if (cu_count <= 0) cu_count = 256;
+  if (items_per_cu <= 0) items_per_cu = 2;
+  int64_t total = 0;
+  for (int s = 0; s < S; ++s) {
+    SIPA_CHECK(ctx[s] >= 1, SIPA_EINVAL, "context length %d of sequence %d < 1", ctx[s], s);
+    total += ctx[s];
+  }
+  total *= Hkv;
+  int64_t piece = (total + (int64_t)cu_count * items_per_cu - 1) / ((int64_t)cu_count * items_per_cu);
+  piece = std::min<int64_t>(std::max<int64_t>((piece + kChunkAlign - 1) / kChunkAlign * kChunkAlign, kMinChunk),
+                            kMaxSplitBlocks * 16);
+  struct Item {
+    int32_t s, h, sp, n, start, end;
+  };
+  std::vector<Item> v;
+  int32_t maxn = 1;
+  for (int s = 0; s < S; ++s) {
+    // near-equal pieces of the pair, each a multiple of 64 tokens (block- and tile-aligned starts)
+    const int64_t n0 = (ctx[s] + piece - 1) / piece;
+    const int64_t per = ((ctx[s] + n0 - 1) / n0 + kChunkAlign - 1) / kChunkAlign * kChunkAlign;
+    const int32_t n = (int32_t)((ctx[s] + per - 1) / per);
+    maxn = std::max(maxn, n);
+    for (int h = 0; h < Hkv; ++h)
+      for (int k = 0; k < n; ++k)
+        v.push_back(Item{s, h, k, n, (int32_t)(k * per), (int32_t)std::min<int64_t>((k + 1) * per, ctx[s])});
+  }
+  SIPA_CHECK(v.size() <= 0x7fffffff, SIPA_EINVAL, "work list too long");
+  if (max_splits) *max_splits = maxn;
+  if (items == nullptr) return (int32_t)v.size();
+  SIPA_CHECK((int64_t)v.size() <= capacity, SIPA_EINVAL, "work list of %d items exceeds capacity %d",
+             (int)v.size(), capacity);
+  std::stable_sort(v.begin(), v.end(), [](const Item& x, const Item& y) { return x.end - x.start > y.end - y.start; });
+  for (size_t i = 0; i < v.size(); ++i) {
+    int32_t* o = items + 8 * i;
+    o[0] = v[i].s, o[1] = v[i].h, o[2] = v[i].sp, o[3] = v[i].n, o[4] = v[i].start, o[5] = v[i].end;
+    o[6] = o[7] = 0;
+  }
+  return (int32_t)v.size();
+}
+
 extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                                                int32_t head_dim, int32_t num_splits) {
   if (num_splits <= 1) return 0;
@@ -555,7 +601,9 @@ extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_h
 
 extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   SIPA_CHECK(p != nullptr, SIPA_EINVAL, "params is NULL");
-  SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params), SIPA_EINVAL,
+  // Callers built against the first ABI pass the struct without the work-list fields.
+  const int32_t size_v1 = (int32_t)offsetof(sipa_decode_params, work_items);
+  SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params) || p->struct_size == size_v1, SIPA_EINVAL,
              "struct_size %d does not match this library's sipa_decode_params (%d bytes)", p->struct_size,
              (int)sizeof(sipa_decode_params));
   const int S = p->num_seqs, Hq = p->num_q_heads, Hkv = p->num_kv_heads, D = p->head_dim, B = p->block_size;
@@ -589,8 +637,17 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
                SIPA_EINVAL, "staging must be 16-byte aligned with strides multiple of 8");
   }
 
-  int chunk = 0;
-  const int splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, &chunk);
+  const int n_items = p->struct_size == size_v1 ? 0 : p->num_items;
+  SIPA_CHECK(n_items >= 0, SIPA_EINVAL, "num_items %d < 0", n_items);
+  int chunk = 0, splits = 1;
+  if (n_items > 0) {
+    SIPA_CHECK(p->work_items != nullptr && aligned16(p->work_items), SIPA_EINVAL,
+               "work_items must be a 16-byte aligned device array");
+    SIPA_CHECK(p->num_splits >= 1, SIPA_EINVAL, "with a work list, num_splits must be its largest split count");
+    splits = p->num_splits;
+  } else {
+    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, &chunk);
+  }
   SIPA_CHECK((int64_t)(Hq / Hkv) * splits * D * 4 < INT32_MAX, SIPA_EUNSUPPORTED,
              "%d splits: a KV head's partial rows exceed 2 GiB", splits);
 
@@ -630,7 +687,8 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.splits = splits;
   a.chunk = chunk;
   a.max_ctx = p->max_context;
-  a.fused = p->combine == SIPA_COMBINE_FUSED;
+  a.items = n_items > 0 ? p->work_items : nullptr;
+  a.fused = n_items > 0 || p->combine == SIPA_COMBINE_FUSED;  // a work list always merges in place
   a.scale_log2 = p->scale * 1.4426950408889634f;
 
   if (splits > 1) {
@@ -674,7 +732,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
 
   hipStream_t st = (hipStream_t)stream;
-  const int64_t wgs = (int64_t)S * Hkv * splits;
+  const int64_t wgs = n_items > 0 ? (int64_t)n_items : (int64_t)S * Hkv * splits;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   const dim3 grid((unsigned)wgs);
   int rc;

@@ -30,17 +30,35 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// The grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware hands workgroup L
-// to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads evenly over
-// them; and every sequence's first split (the only one a short sequence has) is dispatched before any second one.
+// Without a work list the grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware
+// hands workgroup L to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads
+// evenly over them; and every sequence's first split (the only one a short sequence has) is dispatched before any
+// second one. With a work list, workgroup L takes item L: {sequence, KV head, split, splits of that pair, start,
+// end}. Item fields are clamped into range, so a list that does not match the context lengths gives wrong
+// results but no out-of-bounds access.
 struct WorkItem {
   int s, h, sp;
+  int start, end;  // tokens [start, end) before clamping to the context length
+  int nvalid;      // splits of (s, h) that hold tokens (work list); -1: derived from the context length
 };
 
 __device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
   const int L = blockIdx.x;
+  if (a.items != nullptr) {
+    const int4* it = (const int4*)(a.items + 8 * (int64_t)L);
+    const int4 x = it[0], y = it[1];
+    WorkItem w;
+    w.s = min(max(x.x, 0), a.S - 1);
+    w.h = min(max(x.y, 0), a.Hkv - 1);
+    w.sp = min(max(x.z, 0), a.splits - 1);
+    w.nvalid = min(max(x.w, 1), a.splits);
+    w.start = min(max(y.x, 0), a.max_ctx);
+    w.end = min(max(y.y, w.start), min(a.max_ctx, w.start + kMaxSplitBlocks * 16));
+    return w;
+  }
   const int sh = L % (a.S * a.Hkv);
-  return WorkItem{sh % a.S, sh / a.S, L / (a.S * a.Hkv)};
+  const int sp = L / (a.S * a.Hkv);
+  return WorkItem{sh % a.S, sh / a.S, sp, sp * a.chunk, min(sp * a.chunk + a.chunk, a.max_ctx), -1};
 }
 
 template <bool OUT_F32>
@@ -232,8 +250,9 @@ struct KVTile {
 // before ctx[s] is known, so that the first K/V loads wait for one memory round trip instead of two.
 constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
 
-__device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int (&ids)[kIdsPerThread]) {
-  const int nb_spec = (min(a.chunk, a.max_ctx - start) + 15) >> 4;
+__device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int end_spec,
+                                               int (&ids)[kIdsPerThread]) {
+  const int nb_spec = (end_spec - start + 15) >> 4;
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
 #pragma unroll
   for (int i = 0; i < kIdsPerThread; ++i) {

@@ -67,13 +67,13 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
 
   const WorkItem w = work_item(a);
   const int sp = w.sp, h = w.h, s = w.s;
-  const int start = sp * a.chunk;
+  const int start = w.start;
   const int G = a.G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
   int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(a, s, start, ids);
+  const int nb_spec = fetch_split_ids(a, s, start, w.end, ids);
   bf16x8 qb[KS];  // the query group in bf16 (staged block of mode 2), channel order of the int8 K layout
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
@@ -102,9 +102,9 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
     }
   }
   const int ctx = a.ctx[s];
-  if (start >= ctx) return;
-  const int end = min(start + a.chunk, ctx);
-  const int nvalid = (ctx + a.chunk - 1) / a.chunk;
+  if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
+  const int end = max(start, min(w.end, ctx));
+  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
   const int tail = (MODE >= 2) ? a.tail[s] : -1;       // staging slot of the partial last block, -1 if none
   commit_split_ids(nb_spec, ids, bids);

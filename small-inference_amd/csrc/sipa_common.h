@@ -75,6 +75,7 @@ struct DecodeArgs {
   const void* stage;
   int64_t st_sh, st_sn, st_sb;
   const int32_t* tail;
+  const int32_t* items;  // work list (8 int32 per workgroup), or NULL for the (sequence, KV head, split) grid
   float* part;        // [S, Hq, splits, D] unnormalised split outputs
   float* pm;          // [S, Hq, splits] split running max (log2 domain)
   float* pl;          // [S, Hq, splits] split softmax denominators

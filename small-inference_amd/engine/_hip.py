@@ -17,7 +17,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library; see th
 
 # SIPA_LIB overrides the location (for copies of these modules placed inside another package).
 LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # element types (SIPA_F32 ...)
 F32, BF16, F16, I8 = 0, 1, 2, 3
@@ -46,6 +46,7 @@ class DecodeParams(ctypes.Structure):
         ("v_scale", vp), ("v_scale_dtype", i32), ("vs_stride_h", i64), ("vs_stride_n", i64),
         ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64),
         ("tail_slots", vp), ("workspace", vp), ("workspace_bytes", i64),
+        ("work_items", vp), ("num_items", i32),
     ]
 
 
@@ -58,6 +59,7 @@ SIGNATURES = {
     "sipa_split_chunk": (i32, [i32, i32]),
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
+    "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, vp, i32, vp]),
     "sipa_quantize_store_tokens": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, i64, i64,
                                          vp]),
     "sipa_quantize_store_blocks": (i32, [vp, i32, i64, i64, i64, vp, vp, i32, i32, i32, i32, vp, i64, i64, vp, i64,

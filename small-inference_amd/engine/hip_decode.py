@@ -18,6 +18,7 @@ import ctypes
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _hip
@@ -60,9 +61,34 @@ def device_cu_count(device: torch.device | int | None = None) -> int:
 
 
 def choose_splits(num_seqs: int, num_kv_heads: int, max_context: int, cu_count: int | None = None) -> int:
-    """Splits per sequence for a call: about four workgroups per CU, splits of 256 to 512 tokens."""
+    """Splits per sequence for a call: about one workgroup per CU, splits of 256 to 2048 tokens."""
     cu = device_cu_count() if cu_count is None else cu_count
     return int(_hip.lib().sipa_choose_splits(num_seqs, num_kv_heads, max_context, cu))
+
+
+def build_work_list(context_lens: list[int], num_kv_heads: int, cu_count: int | None = None,
+                    items_per_cu: int = 2) -> tuple[np.ndarray, int]:
+    """Work list for a ragged batch from host-side context lengths: ([n, 8] int32 items, largest split count of
+    a pair). Each (sequence, KV head) pair is cut into near-equal pieces of about sum(ctx) * Hkv /
+    (cu_count * items_per_cu) tokens; items are ordered longest first."""
+    cu = device_cu_count() if cu_count is None else cu_count
+    ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
+    lib, maxs = _hip.lib(), ctypes.c_int32(0)
+    n = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, None, 0, None)
+    if n < 0:
+        _hip.check(n, "build_work_list")
+    items = np.zeros((n, 8), dtype=np.int32)
+    rc = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, items.ctypes.data, n,
+                                  ctypes.byref(maxs))
+    if rc < 0:
+        _hip.check(rc, "build_work_list")
+    return items, int(maxs.value)
+
+
+def is_ragged(context_lens: list[int]) -> bool:
+    """Whether a batch gains from a work list: its lengths are far from uniform (total under 80% of
+    num_seqs * max_context)."""
+    return len(context_lens) > 1 and sum(context_lens) < 0.8 * len(context_lens) * max(context_lens)
 
 
 def split_plan(max_context: int, num_splits: int) -> tuple[int, int]:
@@ -97,7 +123,8 @@ class DecodePlan:
 
     def __init__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                  context_lens: torch.Tensor, scale: float, max_context: int, num_splits: int | None = None,
-                 quant: QuantKV | None = None, *, impl: str = "auto", combine: str = "fused"):
+                 quant: QuantKV | None = None, *, impl: str = "auto", combine: str = "fused",
+                 host_context_lens: list[int] | None = None, work_list: str = "auto"):
         S, Hq, D = q.shape
         Hkv, N, B, _ = k_cache.shape
         assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and \
@@ -114,8 +141,24 @@ class DecodePlan:
         self._keep = [block_tables, context_lens.contiguous()]  # tensors the parameter block points into
         self.lib = _hip.lib()
         self.stream = _hip.stream_of(q)
-        self.requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
-        self.splits, self.chunk = split_plan(max_context, self.requested)
+        if work_list not in ("auto", "on", "off"):
+            raise ValueError(f"work_list {work_list!r}")
+        use_list = work_list == "on" or (work_list == "auto" and num_splits is None and
+                                         host_context_lens is not None and is_ragged(host_context_lens))
+        if use_list and host_context_lens is None:
+            raise ValueError("work_list='on' needs host_context_lens")
+        self.items = None
+        if use_list:
+            if len(host_context_lens) != S or max(host_context_lens, default=0) > max_context:
+                raise ValueError("host_context_lens must hold S lengths, none above max_context")
+            items, max_splits = build_work_list(host_context_lens, Hkv, device_cu_count(q.device))
+            self.items = torch.from_numpy(items).to(q.device)
+            self._keep.append(self.items)
+            self.requested = self.splits = max_splits
+            self.chunk = None
+        else:
+            self.requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
+            self.splits, self.chunk = split_plan(max_context, self.requested)
 
         p = self.params = _hip.DecodeParams()
         p.struct_size = ctypes.sizeof(_hip.DecodeParams)
@@ -127,6 +170,8 @@ class DecodePlan:
         p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
         p.context_lens = self._keep[1].data_ptr()
         p.kv_mode = self.quant_mode
+        if self.items is not None:
+            p.work_items, p.num_items = self.items.data_ptr(), self.items.shape[0]
         if quant is None:
             if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
                 raise ValueError("without `quant` the pool must be in q's dtype")
@@ -209,14 +254,19 @@ class DecodePlan:
 def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                            context_lens: torch.Tensor, scale: float, max_context: int,
                            num_splits: int | None = None, quant: QuantKV | None = None, *, impl: str = "auto",
-                           combine: str = "fused", out: torch.Tensor | None = None) -> torch.Tensor:
+                           combine: str = "fused", out: torch.Tensor | None = None,
+                           host_context_lens: list[int] | None = None, work_list: str = "auto") -> torch.Tensor:
     """Attention of one query token per sequence over its paged context.
 
     q [S, Hq, D] (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, B, D], one layer of the
     pool, contiguous (int8 when `quant` is given); block_tables [S, max_blocks] int32; context_lens [S] int32 (each
     >= 1, the new token included); max_context = max(context_lens), known on the host. num_splits None picks from
     the CU count. Returns [S, Hq, D] in q's dtype (written into `out` if given).
+
+    host_context_lens: the same lengths as a host list, when the caller has them (the caches do). A ragged batch
+    then runs from a work list (work_list="auto"; "on" forces it, "off" keeps the split grid): near-equal pieces,
+    longest first, always merged by the last-arriving workgroup.
     """
     plan = DecodePlan(q, k_cache, v_cache, block_tables, context_lens, scale, max_context, num_splits, quant,
-                      impl=impl, combine=combine)
+                      impl=impl, combine=combine, host_context_lens=host_context_lens, work_list=work_list)
     return plan(out=out)

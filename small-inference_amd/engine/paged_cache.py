@@ -145,7 +145,7 @@ class PagedKVCache:
             else:
                 idx = torch.tensor(dec, device=meta.positions.device)
                 rows, bt, ctx = meta.last_token_indices[idx], meta.block_tables[idx], meta.context_lens_t[idx]
-            self._decode = (rows, bt, ctx, max(meta.context_lens[i] for i in dec))
+            self._decode = (rows, bt, ctx, [meta.context_lens[i] for i in dec])
             self._decode_seqs = dec
 
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -188,12 +188,14 @@ class PagedKVCache:
             return outs[0] if len(outs) == 1 else torch.cat(outs)
         from .hip_decode import DecodePlan
 
-        rows, bt, ctx, max_ctx = self._decode
+        rows, bt, ctx, lens = self._decode
         T, Hq, d = q.shape
         q_dec = q if rows is None else q[rows]
         quant = self._kernel_quant(layer)
         if self._plan is None or self._plan_scale != scale:  # first layer of the forward: validate once
-            self._plan = DecodePlan(q_dec, self.k[layer], self.v[layer], bt, ctx, scale, max_ctx, quant=quant)
+            # The host-side lengths let a ragged batch run from a work list (built once, used by every layer).
+            self._plan = DecodePlan(q_dec, self.k[layer], self.v[layer], bt, ctx, scale, max(lens), quant=quant,
+                                    host_context_lens=lens)
             self._plan_scale = scale
             dec = self._plan()
         else:

@@ -28,8 +28,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_and_struct_layout():
     assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION
-    # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives.
-    assert ctypes.sizeof(_hip.DecodeParams) == _hip.DecodeParams.workspace_bytes.offset + 8
+    # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives; the
+    # work-list fields come last (a first-ABI caller's struct ends at workspace_bytes).
+    assert _hip.DecodeParams.work_items.offset == _hip.DecodeParams.workspace_bytes.offset + 8
+    assert ctypes.sizeof(_hip.DecodeParams) == _hip.DecodeParams.num_items.offset + 8
 
 
 def bad_params(**over):
@@ -95,3 +97,54 @@ def test_split_policy_host_side():
     assert lib.sipa_choose_splits(256, 2, 8192, 256) == 4      # long sequences still split at 2048 tokens
     assert lib.sipa_choose_splits(512, 2, 300, 256) == 1
     assert lib.sipa_decode_workspace_bytes(32, 14, 2, 64, 1) == 0
+
+
+def work_list(lengths, Hkv, cu=256, per_cu=2):
+    lib = _hip.lib()
+    ctx = (ctypes.c_int32 * len(lengths))(*lengths)
+    n = lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, None, 0, None)
+    assert n > 0
+    items = (ctypes.c_int32 * (8 * n))()
+    maxs = ctypes.c_int32(0)
+    assert lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, items, n, ctypes.byref(maxs)) == n
+    return [tuple(items[8 * i:8 * i + 8]) for i in range(n)], maxs.value
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_work_list_partitions_every_pair(seed):
+    """Each (sequence, KV head) pair is cut into pieces that tile [0, ctx) exactly, start on 64-token boundaries
+    and are numbered 0 .. n-1 with n recorded in every item; items are ordered longest first."""
+    import random
+
+    rng = random.Random(seed)
+    lengths = [max(1, min(40000, int(rng.lognormvariate(6.4, 1.2)))) for _ in range(rng.randint(1, 300))]
+    Hkv = rng.choice([1, 2, 4])
+    items, maxs = work_list(lengths, Hkv)
+    sizes = [e - b for (_, _, _, _, b, e, _, _) in items]
+    assert sizes == sorted(sizes, reverse=True)
+    pieces = {}
+    for s, h, sp, n, b, e, z0, z1 in items:
+        assert z0 == z1 == 0 and 0 <= b < e <= lengths[s] and b % 64 == 0 and 1 <= n <= maxs
+        pieces.setdefault((s, h), []).append((sp, n, b, e))
+    assert set(pieces) == {(s, h) for s in range(len(lengths)) for h in range(Hkv)}
+    for (s, h), ps in pieces.items():
+        ps.sort()
+        assert [p[0] for p in ps] == list(range(len(ps))) and all(p[1] == len(ps) for p in ps)
+        assert ps[0][2] == 0 and ps[-1][3] == lengths[s]
+        assert all(a[3] == b[2] for a, b in zip(ps, ps[1:]))
+        assert all(p[3] - p[2] <= 32768 for p in ps)
+    assert maxs == max(len(ps) for ps in pieces.values())
+
+
+def test_work_list_piece_size_and_errors():
+    """Pieces are about total / (cu * items_per_cu) tokens, at least 256; bad lengths and short buffers fail."""
+    items, maxs = work_list([8192] * 32, 2, cu=256, per_cu=2)  # 524288 token-heads / 512 -> 1024-token pieces
+    assert len(items) == 512 and maxs == 8 and {e - b for *_, b, e, _, _ in items} == {1024}
+    items, maxs = work_list([100, 50], 2)
+    assert len(items) == 4 and maxs == 1
+    lib = _hip.lib()
+    bad = (ctypes.c_int32 * 2)(5, 0)
+    assert lib.sipa_build_work_list(bad, 2, 2, 256, 2, None, 0, None) == _hip.EINVAL
+    ok = (ctypes.c_int32 * 2)(5000, 7)
+    small = (ctypes.c_int32 * 8)()
+    assert lib.sipa_build_work_list(ok, 2, 2, 256, 2, small, 1, None) == _hip.EINVAL

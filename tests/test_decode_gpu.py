@@ -20,14 +20,14 @@ from engine.hip_decode import choose_splits, paged_decode_attention, split_plan
 pytestmark = pytest.mark.gpu
 
 
-def run(lengths, heads, B, dtype, splits, impl="auto", combine="fused", seed=0):
+def run(lengths, heads, B, dtype, splits, impl="auto", combine="fused", seed=0, work_list="off"):
     Hq, Hkv, D = HEADS[heads]
     q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, B, dtype, seed)
     scale = D ** -0.5
-    print(f"case lengths={lengths[:8]} heads={heads} B={B} {dtype} splits={splits} impl={impl} {combine}",
-          flush=True)
+    print(f"case lengths={lengths[:8]} heads={heads} B={B} {dtype} splits={splits} impl={impl} {combine} "
+          f"work_list={work_list}", flush=True)
     out = paged_decode_attention(q, k, v, bt, ctx, scale, max(lengths), num_splits=splits, impl=impl,
-                                 combine=combine)
+                                 combine=combine, host_context_lens=lengths, work_list=work_list)
     torch.cuda.synchronize()
     got = out.double().cpu().numpy()
     ref64 = oracle_decode(q, k, v, tables, lengths, scale, np.float64)
@@ -115,3 +115,18 @@ def test_strided_q_view():
     out = paged_decode_attention(qkv[:, :Hq], k, v, bt, ctx, D ** -0.5, max(RAGGED))
     ref = oracle_decode(q, k, v, tables, RAGGED, D ** -0.5, np.float32)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 8e-3
+
+
+@pytest.mark.parametrize("heads", list(HEADS))
+@pytest.mark.parametrize("impl,dtype", [("mfma", torch.bfloat16), ("valu", torch.bfloat16), ("valu", torch.float32)],
+                         ids=["mfma-bf16", "valu-bf16", "valu-fp32"])
+@pytest.mark.parametrize("lengths", [RAGGED, [1, 5000, 64, 65, 20000, 3, 129]], ids=["ragged", "long"])
+def test_work_list_matches_oracle(heads, impl, dtype, lengths):
+    """Ragged batches run from a host-built work list (near-equal pieces, longest first, merged in place)."""
+    run(lengths, heads, 16, dtype, None, impl=impl, work_list="on")
+
+
+def test_work_list_block_sizes():
+    """Work lists with 8- and 32-token blocks (VALU kernel): pieces start on 64-token boundaries."""
+    for B in (8, 32):
+        run(RAGGED + [3000], "0.5B", B, torch.float32, None, work_list="on")

@@ -282,7 +282,7 @@ def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("heads", list(HEADS))
 @pytest.mark.parametrize("impl", ["mfma", "valu"])
-@pytest.mark.parametrize("splits", [1, 3, None], ids=["single", "split3", "auto"])
+@pytest.mark.parametrize("splits", [1, 3, None, "list"], ids=["single", "split3", "auto", "worklist"])
 def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     """Both INT8 kernels against the oracle's fp32 dequantize-then-attend, outlier K channels (4 per head scaled
     by U[20, 68], as config C4), ragged lengths with partial last blocks, max-abs 8e-3."""
@@ -290,8 +290,11 @@ def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     lengths = [1, 15, 16, 17, 33, 100, 700, 2100]
     q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=5)
     print(f"case {fmt} {heads} {impl} splits={splits}", flush=True)
+    lists = dict(host_context_lens=lengths, work_list="on") if splits == "list" else {}
+    if splits == "list":
+        splits = None
     out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
-                                 max(lengths), num_splits=splits, quant=quant, impl=impl)
+                                 max(lengths), num_splits=splits, quant=quant, impl=impl, **lists)
     got = out.double().cpu().numpy()
     ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
                     for s in range(len(lengths))])
@@ -303,7 +306,7 @@ def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     assert beyond <= 8e-3, f"error beyond bf16 output rounding {beyond:.3e} (raw max-abs {raw:.3e})"
     if impl == "valu":  # the same case with an fp32 query and output: the fp32 math itself, no rounding allowance
         out32 = paged_decode_attention(q.float(), cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t,
-                                       D ** -0.5, max(lengths), num_splits=splits, quant=quant)
+                                       D ** -0.5, max(lengths), num_splits=splits, quant=quant, **lists)
         err32 = np.abs(out32.double().cpu().numpy() - ref).max()
         assert err32 <= 8e-3, f"fp32 max-abs {err32:.3e}"
 
