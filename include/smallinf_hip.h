@@ -124,6 +124,8 @@ int32_t sipa_device_cu_count(int32_t device);
  * max_context and none over 2048 (so a long sequence in a ragged batch is spread over many CUs).
  */
 int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count);
+/* sipa_decode with num_splits <= 0 applies it with cu_count = the device's CUs for bf16/fp32 pools and twice
+ * that for INT8 pools, whose kernels run two workgroups per CU. */
 
 /* Tokens per split for a call with num_splits splits: ceil(max_context / num_splits) rounded up to a multiple
  * of 64 tokens, at most 32768. Calls launch ceil(max_context / chunk) splits, which may be fewer than asked. */

@@ -542,9 +542,10 @@ extern "C" int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits) {
   return split_chunk_host(max_context, num_splits);
 }
 
-static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int* chunk) {
+// wgs_per_cu: workgroups of the chosen kernel that run on one CU at once (the INT8 kernels fit two).
+static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int wgs_per_cu, int* chunk) {
   int splits = requested;
-  if (splits <= 0) splits = choose_splits_host(S, Hkv, max_ctx, sipa_device_cu_count(-1));
+  if (splits <= 0) splits = choose_splits_host(S, Hkv, max_ctx, wgs_per_cu * sipa_device_cu_count(-1));
   *chunk = split_chunk_host(max_ctx, splits);
   return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
 }
@@ -646,7 +647,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
     SIPA_CHECK(p->num_splits >= 1, SIPA_EINVAL, "with a work list, num_splits must be its largest split count");
     splits = p->num_splits;
   } else {
-    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, &chunk);
+    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, mode == SIPA_KV_PLAIN ? 1 : 2, &chunk);
   }
   SIPA_CHECK((int64_t)(Hq / Hkv) * splits * D * 4 < INT32_MAX, SIPA_EUNSUPPORTED,
              "%d splits: a KV head's partial rows exceed 2 GiB", splits);

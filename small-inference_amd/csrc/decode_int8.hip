@@ -47,13 +47,13 @@ struct Int8Tile {
   u32x4 v[2][D / 64];   // V codes as 16-byte row chunks
   uint2 ks[2];          // mode 1: K scales of tokens 4 q4 .. 4 q4 + 3 (fp16)
   uint2 vs[2];          // V scales of the same tokens (fp16)
-  u32x4 kc[2][D / 32];  // mode 2: the block's channel scales of the lane's channels (fp16)
+  uint32_t kc[2];       // mode 2: one 32-bit word (2 fp16 channel scales) of the block's D scales per lane
 };
 
 // MODE 1: per-token K scales; 2: per-(block, channel) K scales; 3: mode 2 with one channel scale per (head,
 // channel) for every block (a zero block stride), folded into the query once.
 template <int D, int MODE, int NB>
-__global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs a) {
   constexpr int KS = D / 32;   // QK k-steps per block
   constexpr int DT = D / 16;   // PV d-tiles
   constexpr int KL = D / 64;   // 16-byte K loads per lane per block
@@ -62,6 +62,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
   constexpr int CPR = D / 16;  // 16-code chunks per token row
   constexpr int QW = D / 4;    // channels per lane group
   __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
+  __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
 
@@ -74,16 +75,16 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
 
   int ids[kIdsPerThread];
   const int nb_spec = fetch_split_ids(a, s, start, w.end, ids);
-  bf16x8 qb[KS];  // the query group in bf16 (staged block of mode 2), channel order of the int8 K layout
-  {
-    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
+  // The query group in bf16, channel order of the int8 K layout: k-step j of lane (r, q4) (zero for r >= G).
+  const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
+  auto load_qb = [&](int j) {
+    u32x4 u = *(const u32x4*)(qrow + QW * q4 + 8 * j);
+    if (r >= G) u = u32x4{0, 0, 0, 0};
+    return __builtin_bit_cast(bf16x8, u);
+  };
+  bf16x8 qb[KS];
 #pragma unroll
-    for (int j = 0; j < KS; ++j) {
-      u32x4 u = *(const u32x4*)(qrow + QW * q4 + 8 * j);
-      if (r >= G) u = u32x4{0, 0, 0, 0};
-      qb[j] = __builtin_bit_cast(bf16x8, u);
-    }
-  }
+  for (int j = 0; j < KS; ++j) qb[j] = load_qb(j);
   constexpr bool kconst = MODE == 3;  // one channel scale per (head, channel) for every block
   // qh: the query in fp16 (modes 1, 2), or the high part of Q' = q * s (mode 3) with ql its low part,
   // fp16(Q' - qh), so that qh + ql carries Q' to about 2^-22.
@@ -135,10 +136,8 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
       for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
       tl.vs[mt] = *(const uint2*)(vsh + blk * a.vs_sn + 4 * q4);
       if (MODE == 1) tl.ks[mt] = *(const uint2*)(ksh + blk * a.ks_sn + 4 * q4);
-      if (MODE == 2 && !kconst) {
-#pragma unroll
-        for (int j = 0; j < KS; ++j) tl.kc[mt][j] = *(const u32x4*)(ksh + blk * a.ks_sn + QW * q4 + 8 * j);
-      }
+      if (MODE == 2)  // lane L holds channels 2L, 2L + 1 (lanes past D / 2 repeat the first half)
+        tl.kc[mt] = *(const uint32_t*)(ksh + blk * a.ks_sn + 2 * (lane % (D / 2)));
     }
   };
 
@@ -149,8 +148,14 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
 
   // p <= 2^4 against the lazily raised max, so that p * s_v (s_v <= 65504 / 127) stays within fp16.
   constexpr float kRescaleSlack = 4.f;
+  uint32_t* kcw = kcs + (MODE == 2 ? wave * 2 * 64 : 0);
   auto process_tile = [&](int t0, Int8Tile<D>& tl) {
     const bool partial = t0 + 32 > end;
+    if (MODE == 2) {  // the tile's channel scales go through LDS: each lane then reads the 8 D / 32 it needs
+      kcw[lane] = tl.kc[0];
+      kcw[64 + lane] = tl.kc[1];
+      wave_sync();
+    }
     // V codes -> fp16 -> LDS (rows at or past the end are zero).
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -179,7 +184,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
 #pragma unroll
         for (int j = 0; j < KS; ++j)
           sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4*)(st + 8 * j)),
-                                                           qb[j], sc[mt], 0, 0, 0);
+                                                           load_qb(j), sc[mt], 0, 0, 0);  // reloaded: rare
         continue;
       }
 #pragma unroll
@@ -195,7 +200,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_int8(const DecodeArgs a)
           // Q' = q * s with the block's fp16 channel scales s, as an exact high part plus a low part: s_hi keeps
           // the top 3 significant bits of s (sign, exponent, 2 mantissa bits), so q * s_hi (8 x 3 bits) is exact
           // in fp16; s_lo = s - s_hi is exact and q * s_lo is rounded relative to that small remainder only.
-          const u32x4 cw = tl.kc[mt][j];
+          const u32x4 cw = *(const u32x4*)(kcw + 64 * mt + (QW * q4 + 8 * j) / 2);
           const f16x8 s_all = __builtin_bit_cast(f16x8, cw);
           const f16x8 s_hi = __builtin_bit_cast(f16x8, cw & 0xff00ff00u);
           const f16x8 q_hi = qh[j] * s_hi;

@@ -157,7 +157,9 @@ class DecodePlan:
             self.requested = self.splits = max_splits
             self.chunk = None
         else:
-            self.requested = num_splits or choose_splits(S, Hkv, max_context, device_cu_count(q.device))
+            # The INT8 kernels run two workgroups per CU: size their grid for twice the CUs.
+            wgs_per_cu = 1 if quant is None else 2
+            self.requested = num_splits or choose_splits(S, Hkv, max_context, wgs_per_cu * device_cu_count(q.device))
             self.splits, self.chunk = split_plan(max_context, self.requested)
 
         p = self.params = _hip.DecodeParams()
