@@ -86,6 +86,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
   const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
   uint16_t* vw = (uint16_t*)smem + wave * 32 * VP;
+  const int tr_off = tr16_offset(r, q4, VP);
   const int ntile = (end - start + 31) >> 5;
   const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;  // tiles wave, wave + 4, ...
 
@@ -178,10 +179,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
     wave_sync();  // the wave's V tile is in LDS
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      bf16x8 vop;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        vop[i] = __builtin_bit_cast(__bf16, vw[(16 * (i >> 2) + 4 * q4 + (i & 3)) * VP + 16 * dt + r]);
+      const bf16x8 vop = read_v_operand<bf16x8>(vw, tr_off, VP, 16 * dt);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[dt], 0, 0, 0);
     }
     wave_sync();  // reads done before the next tile overwrites the LDS tile

@@ -224,6 +224,27 @@ __device__ void finish_split(const DecodeArgs& a, int s, int h, int sp, int nval
 // ---- MFMA kernels --------------------------------------------------------------------------------------------
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each group of 16 lanes, lane j passes the address of a
+// 4-element (8-byte) chunk M[j]; lane i receives M[4 k + i / 4][i % 4], k = 0..3. With lane j of group q4 pointing
+// at row 4 q4 + j / 4, columns c0 + 4 (j % 4) .. + 3 of a row-major tile, lane (r, q4) receives rows
+// 4 q4 .. 4 q4 + 3 of column c0 + r: the A-operand order of the P.V MFMA.
+__device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+}
+
+// Lane (r, q4)'s element offset into a row-major [32][pitch] 16-bit tile for lds_read_tr16: row 4 q4 + r / 4,
+// column 4 (r % 4).
+__device__ __forceinline__ int tr16_offset(int r, int q4, int pitch) { return (4 * q4 + (r >> 2)) * pitch + 4 * (r & 3); }
+
+// The 8 k-slots of the P.V A operand for columns c0 .. c0 + 15: slot i is row 16 (i / 4) + 4 q4 + i % 4.
+template <typename T8>
+__device__ __forceinline__ T8 read_v_operand(const uint16_t* tile, int tr_off, int pitch, int c0) {
+  const i16x4 lo = lds_read_tr16(tile + tr_off + c0);
+  const i16x4 hi = lds_read_tr16(tile + tr_off + 16 * pitch + c0);
+  return __builtin_bit_cast(T8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 template <int D>
 struct MfmaSmem {

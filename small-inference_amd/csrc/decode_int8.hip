@@ -116,6 +116,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const uint16_t* ksh = (const uint16_t*)a.ks + (int64_t)h * a.ks_sh;
   const uint16_t* vsh = (const uint16_t*)a.vs + (int64_t)h * a.vs_sh;
   _Float16* vw = (_Float16*)smem + wave * 32 * VP;
+  const int tr_off = tr16_offset(r, q4, VP);
   const int ntile = (end - start + 31) >> 5;
   const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;
   auto tile_t0 = [&](int k) { return start + 32 * (wave + kWaves * k); };
@@ -252,9 +253,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     wave_sync();  // the wave's V tile is in LDS
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      f16x8 vop;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vop[i] = vw[(16 * (i >> 2) + 4 * q4 + (i & 3)) * VP + 16 * dt + r];
+      const f16x8 vop = read_v_operand<f16x8>((const uint16_t*)vw, tr_off, VP, 16 * dt);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, acc[dt], 0, 0, 0);
     }
     wave_sync();
