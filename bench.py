@@ -401,6 +401,93 @@ def details(steps: int, warmup: int) -> dict:
     return out
 
 
+def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fraction: float = 0.85,
+                      fmt: str = "bf16", seed: int = 0) -> dict:
+    """Config C5: packed decode steps of a random-init Qwen2.5-0.5B-shaped model (engine/model.py, torch GEMMs)
+    through the paged cache with the HIP store and decode kernels, batch 512, contexts ~ U[1024, 16384], over a
+    pool sized to `pool_fraction` of free HBM with scattered block ids. Reports host metadata time, GPU step time,
+    tokens/s and the share of the step spent in the 24 decode-attention launches."""
+    import random
+    import time
+
+    from engine.block_manager import BlockManager
+    from engine.config import QWEN2_5_0_5B as cfg
+    from engine.model import Qwen2Model
+    from engine.paged_cache import PagedKVCache, build_metadata
+    from engine.quant_cache import QuantPagedKVCache, kv_bytes_per_token
+
+    rng = random.Random(seed)
+    ctx = [rng.randint(1024, 16384) for _ in range(batch)]
+    B = 16
+    free, _ = torch.cuda.mem_get_info()
+    per_block = int(B * kv_bytes_per_token(cfg, fmt))
+    N = int(free * pool_fraction) // per_block
+    need = sum(-(-(n + steps + warmup) // B) for n in ctx)
+    if N < need:
+        raise RuntimeError(f"pool of {N} blocks cannot hold the batch ({need} blocks)")
+    m = BlockManager(N, B)
+    rng.shuffle(m._free)  # a long-running pool: every table scattered over the whole pool
+    if fmt == "bf16":
+        cache = PagedKVCache(cfg, N, B, "cuda", torch.bfloat16, attn_backend="triton")
+    else:
+        cache = QuantPagedKVCache(cfg, N, B, "cuda", torch.bfloat16, "triton", fmt, m, n_stage=2 * batch)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for t in (cache.k, cache.v):  # the contexts' K/V: unit-variance values (the INT8 pools: random codes)
+        if t.dtype == torch.int8:
+            t.random_(-127, 128, generator=gen)
+        else:
+            t.normal_(generator=gen)
+    if fmt != "bf16":
+        for t in (cache.k_scale, cache.v_scale):
+            t.fill_(1.0 / 64)
+    for s, n in enumerate(ctx):
+        m.allocate(s, n)
+    model = Qwen2Model(cfg, "cuda", torch.bfloat16, seed=seed, max_positions=16384 + steps + warmup + 1)
+    ids = torch.randint(0, cfg.vocab_size, (batch,), device="cuda", generator=gen)
+    host_ms, gpu_ms, attn_ms = [], [], []
+    for step in range(warmup + steps):
+        t0 = time.perf_counter()
+        batch_desc = []
+        for s in range(batch):
+            m.append_slot(s)
+            batch_desc.append((s, ctx[s], 1))
+            ctx[s] += 1
+        meta = build_metadata(m, batch_desc, "cuda")
+        t1 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        logits = model.forward(ids, meta.positions, cache, meta)
+        ids = logits.argmax(-1)
+        e1.record()
+        torch.cuda.synchronize()
+        if step < warmup:
+            continue
+        host_ms.append((t1 - t0) * 1e3)
+        gpu_ms.append(e0.elapsed_time(e1))
+        # The same step's 24 decode launches alone, through the plan the forward built (q from a random tensor).
+        plan = cache._plan
+        q = torch.randn(batch, cfg.num_q_heads, cfg.head_dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+        out = torch.empty_like(q)
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        for layer in range(cfg.num_layers):
+            plan(q=q, k_cache=cache.k[layer], v_cache=cache.v[layer], quant=cache._kernel_quant(layer), out=out)
+        a1.record()
+        torch.cuda.synchronize()
+        attn_ms.append(a0.elapsed_time(a1))
+    med = lambda xs: sorted(xs)[len(xs) // 2]  # noqa: E731
+    g, h, a = med(gpu_ms), med(host_ms), med(attn_ms)
+    kv_bytes = 2 * cfg.num_layers * cfg.num_kv_heads * cfg.head_dim * (2 if fmt == "bf16" else 1) * sum(ctx)
+    r = {"format": fmt, "batch": batch, "context_mean": round(sum(ctx) / batch), "pool_blocks": N,
+         "pool_gb": round(N * per_block / 1e9, 1), "gpu_step_ms": round(g, 3), "host_metadata_ms": round(h, 3),
+         "tokens_per_s_gpu": round(batch / (g * 1e-3)), "tokens_per_s_with_host": round(batch / ((g + h) * 1e-3)),
+         "attention_ms": round(a, 3), "attention_share": round(a / g, 3),
+         "attention_kv_gb_s": round(kv_bytes / (a * 1e-3) / 1e9, 1), "work_list": plan.items is not None,
+         "steps": steps}
+    log(f"[bench] c5_decode_step_{fmt}: {json.dumps(r)}")
+    return r
+
+
 def calibrate_copy(mib: int) -> int:
     """A plain device copy of a known size, 10 launches: rocprof's per-dispatch FETCH_SIZE and WRITE_SIZE of this
     kernel against its exact byte count give the scale factor applied to the decode kernel's counters."""
@@ -434,6 +521,8 @@ def main() -> int:
     ap.add_argument("--no-details", dest="details", action="store_false")
     ap.add_argument("--no-cpu", dest="cpu", action="store_false", default=True)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
+    ap.add_argument("--c5", action="store_true", help="only run config C5 (decode steps of a random-init 0.5B "
+                    "model at batch 512 through the paged cache) and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the probe library's plain copy kernel over MIB MiB, 10 times (the reference "
                          "point for rocprof's FETCH_SIZE / WRITE_SIZE counters), and print its byte count")
@@ -452,6 +541,13 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.c5:
+        res = {}
+        for fmt in ("bf16", "int8"):
+            res[fmt] = decode_step_bench(fmt=fmt)
+            torch.cuda.empty_cache()
+        print(json.dumps({"c5_decode_step": res}), flush=True)
+        return 0
     from engine.hip_decode import device_cu_count
 
     cu = device_cu_count()

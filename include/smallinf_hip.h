@@ -194,10 +194,12 @@ int32_t sipa_quantize_store_block_rows(const void* x, int32_t x_dtype, int64_t x
  * engine/quant_cache.py:139-141,165-167 for the bf16 staging slots):
  *   pool[h, blocks[i], offsets[i], :] = convert(x[rows ? rows[i] : i, h, :])   for i < n, h < H.
  * x in x_dtype, pool in pool_dtype (SIPA_F32 / SIPA_BF16 / SIPA_F16; conversion rounds to nearest even).
- * A second tensor pair (x2, pool2) with the same shapes is stored in the same launch when x2 != NULL.
+ * A second tensor pair (x2, pool2) with the same shapes and dtypes (x2 with its own row and head strides, pool2
+ * with pool's strides) is stored in the same launch when x2 != NULL.
  */
 int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dtype, int64_t x_stride_t,
-                          int64_t x_stride_h, const int64_t* rows, int32_t n, int32_t H, int32_t D,
+                          int64_t x_stride_h, int64_t x2_stride_t, int64_t x2_stride_h, const int64_t* rows,
+                          int32_t n, int32_t H, int32_t D,
                           const int64_t* blocks, const int64_t* offsets, void* pool, void* pool2,
                           int32_t pool_dtype, int64_t p_stride_h, int64_t p_stride_n, int64_t p_stride_b,
                           void* stream);

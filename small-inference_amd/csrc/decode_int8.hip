@@ -301,7 +301,8 @@ template <int D, int MODE>
 static int launch_int8_depth(int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
   switch (nb) {
     case 1: return launch_int8(decode_mfma_int8<D, MODE, 1>, grid, a, st);
-    default: return launch_int8(decode_mfma_int8<D, MODE, 2>, grid, a, st);
+    case 2: return launch_int8(decode_mfma_int8<D, MODE, 2>, grid, a, st);
+    default: return launch_int8(decode_mfma_int8<D, MODE, 3>, grid, a, st);
   }
 }
 

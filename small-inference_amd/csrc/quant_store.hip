@@ -104,6 +104,7 @@ struct StoreArgs {
   const void* x;
   const void* x2;
   int64_t x_st, x_sh;
+  int64_t x2_st, x2_sh;
   const int64_t* rows;
   const int64_t* blocks;
   const int64_t* offsets;
@@ -123,7 +124,8 @@ __global__ void __launch_bounds__(256) store_tokens_kernel(const StoreArgs a) {
     const int64_t xi = row * a.x_st + (int64_t)h * a.x_sh + d;
     const int64_t pi = (int64_t)h * a.p_sh + a.blocks[i] * a.p_sn + a.offsets[i] * a.p_sb + d;
     store_from_f32(a.pool, pi, a.p_dtype, load_as_f32(a.x, xi, a.x_dtype));
-    if (a.x2) store_from_f32(a.pool2, pi, a.p_dtype, load_as_f32(a.x2, xi, a.x_dtype));
+    if (a.x2)
+      store_from_f32(a.pool2, pi, a.p_dtype, load_as_f32(a.x2, row * a.x2_st + (int64_t)h * a.x2_sh + d, a.x_dtype));
   }
 }
 
@@ -205,7 +207,8 @@ extern "C" int32_t sipa_quantize_store_block_rows(const void* x, int32_t x_dtype
 }
 
 extern "C" int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dtype, int64_t x_stride_t,
-                                     int64_t x_stride_h, const int64_t* rows, int32_t n, int32_t H, int32_t D,
+                                     int64_t x_stride_h, int64_t x2_stride_t, int64_t x2_stride_h,
+                                     const int64_t* rows, int32_t n, int32_t H, int32_t D,
                                      const int64_t* blocks, const int64_t* offsets, void* pool, void* pool2,
                                      int32_t pool_dtype, int64_t p_stride_h, int64_t p_stride_n, int64_t p_stride_b,
                                      void* stream) {
@@ -215,7 +218,7 @@ extern "C" int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dt
              pool_dtype);
   SIPA_CHECK(x && blocks && offsets && pool, SIPA_EINVAL, "NULL pointer");
   SIPA_CHECK((x2 == nullptr) == (pool2 == nullptr), SIPA_EINVAL, "x2 and pool2 go together");
-  StoreArgs a{x, x2, x_stride_t, x_stride_h, rows, blocks, offsets, pool, pool2,
+  StoreArgs a{x, x2, x_stride_t, x_stride_h, x2_stride_t, x2_stride_h, rows, blocks, offsets, pool, pool2,
               p_stride_h, p_stride_n, p_stride_b, n, H, D, x_dtype, pool_dtype};
   const int64_t total = (int64_t)n * H * D;
   const unsigned wgs = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);

@@ -66,7 +66,8 @@ SIGNATURES = {
                                          i64, vp]),
     "sipa_quantize_store_block_rows": (i32, [vp, i32, i64, i64, vp, vp, i32, i32, i32, i32, vp, i64, i64, vp, i64,
                                              i64, vp]),
-    "sipa_store_tokens": (i32, [vp, vp, i32, i64, i64, vp, i32, i32, i32, vp, vp, vp, vp, i32, i64, i64, i64, vp]),
+    "sipa_store_tokens": (i32, [vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, i32, vp, vp, vp, vp, i32, i64, i64,
+                                i64, vp]),
 }
 
 _lib = None

@@ -81,20 +81,22 @@ def store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, p
                  rows: torch.Tensor | None = None, x2: torch.Tensor | None = None,
                  pool2: torch.Tensor | None = None) -> None:
     """pool[:, blocks[i], offsets[i]] = x[rows[i] if rows is not None else i] (x [T, H, D], pool [H, N, B, D]),
-    converted to the pool's dtype with round-to-nearest-even; (x2, pool2) in the same launch. One launch."""
+    converted to the pool's dtype with round-to-nearest-even; (x2, pool2) in the same launch (x2 may have other
+    strides than x, as K and V views of a fused projection do). One launch."""
     n = blocks.numel()
     if n == 0:
         return
     _, H, D = x.shape
     assert x.stride(-1) == 1 and pool.stride(-1) == 1
     if x2 is not None:
-        assert x2.shape == x.shape and x2.stride() == x.stride() and x2.dtype == x.dtype
+        assert x2.shape == x.shape and x2.stride(-1) == 1 and x2.dtype == x.dtype
         assert pool2 is not None and pool2.stride() == pool.stride() and pool2.dtype == pool.dtype
     _hip.require_gpu(x, blocks, offsets, pool)
     blocks, offsets = _i64(blocks), _i64(offsets)
     rows = None if rows is None else _i64(rows)
     rc = _hip.lib().sipa_store_tokens(
-        x.data_ptr(), _hip.ptr(x2), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), _hip.ptr(rows), n, H, D,
+        x.data_ptr(), _hip.ptr(x2), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1),
+        x.stride(0) if x2 is None else x2.stride(0), x.stride(1) if x2 is None else x2.stride(1), _hip.ptr(rows), n, H, D,
         blocks.data_ptr(), offsets.data_ptr(), pool.data_ptr(), _hip.ptr(pool2), _hip.dtype_code(pool.dtype),
         pool.stride(0), pool.stride(1), pool.stride(2), _hip.stream_of(x))
     _hip.check(rc, "store_tokens")

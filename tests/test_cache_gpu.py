@@ -103,3 +103,30 @@ def test_paged_cache_mixed_batches(dtype, D):
 def test_quant_cache_mixed_batches(fmt, dtype, D):
     run_mixed(lambda m: QuantPagedKVCache(CFG[D], 256, 16, "cuda", dtype, "triton", fmt, m, n_stage=16),
               dtype, D, seed=7 + D)
+
+
+def test_model_mixed_batch_kernel_vs_gather():
+    """A tiny Qwen2-shaped model (engine/model.py) drives the cache as the reference's model does (fused QKV
+    views as K and V, per-layer write then attend): one prefill chunk and two decode rows in one packed forward;
+    the HIP backend's logits equal the gather backend's to fp32 summation order (reference
+    tests/test_paged.py:186-205)."""
+    from engine.model import Qwen2Model
+
+    tiny = ModelConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_layers=2, num_q_heads=4,
+                       num_kv_heads=2, head_dim=16)
+    model = Qwen2Model(tiny, "cuda", torch.float32, seed=1, max_positions=128, std=0.2)
+    outs = {}
+    for backend in ("gather", "triton"):
+        m = fragmented_manager(32, 4, torch.Generator().manual_seed(2))
+        cache = PagedKVCache(tiny, 32, 4, "cuda", torch.float32, attn_backend=backend)
+        for s, n in ((1, 9), (2, 30)):
+            m.allocate(s, n)
+            meta = build_metadata(m, [(s, 0, n)], "cuda")
+            model.forward(torch.arange(n, device="cuda") % 97, meta.positions, cache, meta)
+        m.allocate(0, 13)
+        m.append_slot(1)
+        m.append_slot(2)
+        meta = build_metadata(m, [(1, 9, 1), (0, 0, 13), (2, 30, 1)], "cuda")
+        ids = torch.tensor([5] + list(range(20, 33)) + [7], device="cuda")
+        outs[backend] = model.forward(ids, meta.positions, cache, meta, last_only=False)
+    torch.testing.assert_close(outs["triton"], outs["gather"], rtol=1e-5, atol=1e-5)

@@ -78,8 +78,8 @@ def test_store_entry_points_reject_bad_arguments():
                                           1, None) == _hip.OK  # T = 0
     assert lib.sipa_quantize_store_blocks(4096, _hip.I8, 1, 1, 1, 4096, 4096, 1, 2, 16, 64, 4096, 1, 1, 4096, 1, 1,
                                           None) == _hip.EUNSUPPORTED
-    assert lib.sipa_store_tokens(4096, 4096, _hip.BF16, 1, 1, None, 3, 2, 64, 4096, 4096, 4096, None, _hip.BF16, 1,
-                                 1, 1, None) == _hip.EINVAL  # x2 without pool2
+    assert lib.sipa_store_tokens(4096, 4096, _hip.BF16, 1, 1, 1, 1, None, 3, 2, 64, 4096, 4096, 4096, None,
+                                 _hip.BF16, 1, 1, 1, None) == _hip.EINVAL  # x2 without pool2
 
 
 def test_split_policy_host_side():

@@ -127,6 +127,15 @@ def test_store_tokens_is_exact(dtype):
     store_tokens(x, blocks, offsets, pk, x2=y, pool2=pv)
     assert torch.equal(pk[:, blocks, offsets], x.transpose(0, 1))
     assert torch.equal(pv[:, blocks, offsets], y.transpose(0, 1))
+    # K and V as views of one fused projection output with different row strides (as the model passes them)
+    fused = torch.randn(40, 19, 64, generator=g).to("cuda", dtype)
+    k_view, v_view = fused[:, 14:16], fused[:, 17:19]
+    assert k_view.stride() != x.stride()
+    store_tokens(x, blocks, offsets, pk, x2=v_view, pool2=pv)
+    assert torch.equal(pk[:, blocks, offsets], x.transpose(0, 1))
+    assert torch.equal(pv[:, blocks, offsets], v_view.transpose(0, 1))
+    store_tokens(k_view, blocks, offsets, pk, x2=v_view, pool2=pv)
+    assert torch.equal(pk[:, blocks, offsets], k_view.transpose(0, 1))
     stage = torch.zeros(2, 4, 16, 64, dtype=torch.bfloat16, device="cuda")
     rows = torch.tensor([7, 3, 9], device="cuda")
     store_tokens(x, torch.tensor([2, 2, 0], device="cuda"), torch.tensor([5, 6, 15], device="cuda"), stage,
