@@ -13,6 +13,8 @@ from __future__ import annotations
 
 from typing import Callable
 
+import numpy as np
+
 
 class OutOfBlocks(RuntimeError):
     """Not enough free blocks for the request; nothing was changed."""
@@ -29,6 +31,9 @@ class BlockManager:
         self._ref = [0] * num_blocks
         self._tables: dict[int, list[int]] = {}
         self._lengths: dict[int, int] = {}
+        # int32 mirror of every table (capacity doubles as it grows), so per-forward metadata is built with array
+        # copies instead of Python list work: _arrays[seq][:len(table)] == table.
+        self._arrays: dict[int, np.ndarray] = {}
         self._free_listeners: list[Callable[[list[int]], None]] = []
 
     # ---- queries -------------------------------------------------------------------------------------------------
@@ -69,6 +74,22 @@ class BlockManager:
         """Live sequences."""
         return list(self._tables)
 
+    def table_array(self, seq_id: int) -> np.ndarray:
+        """The sequence's blocks in token order as a read-only int32 array view (valid until its next change)."""
+        v = self._arrays[seq_id][:len(self._tables[seq_id])]
+        v.flags.writeable = False
+        return v
+
+    def _mirror_extend(self, seq_id: int, blocks: list[int]) -> None:
+        arr = self._arrays.get(seq_id)
+        n = len(self._tables[seq_id])  # table length after the extension
+        if arr is None or arr.shape[0] < n:
+            grown = np.empty(max(16, 2 * n), dtype=np.int32)
+            if arr is not None:
+                grown[:n - len(blocks)] = arr[:n - len(blocks)]
+            arr = self._arrays[seq_id] = grown
+        arr[n - len(blocks):n] = blocks
+
     def slots(self, seq_id: int, start: int, end: int) -> list[int]:
         """Slots of positions [start, end) of the sequence."""
         n = self._lengths[seq_id]
@@ -103,6 +124,7 @@ class BlockManager:
             raise OutOfBlocks(f"{need} blocks needed, {len(self._free)} free")
         self._tables[seq_id] = self._pop_blocks(need)
         self._lengths[seq_id] = n_tokens
+        self._mirror_extend(seq_id, self._tables[seq_id])
         return self.slots(seq_id, 0, n_tokens)
 
     def append_slots(self, seq_id: int, n: int = 1) -> list[int]:
@@ -110,7 +132,10 @@ class BlockManager:
         need = self.new_blocks_needed(seq_id, n)
         if need > len(self._free):
             raise OutOfBlocks(f"sequence {seq_id}: {need} blocks needed, {len(self._free)} free")
-        self._tables[seq_id].extend(self._pop_blocks(need))
+        new = self._pop_blocks(need)
+        self._tables[seq_id].extend(new)
+        if new:
+            self._mirror_extend(seq_id, new)
         start = self._lengths[seq_id]
         self._lengths[seq_id] = start + n
         return self.slots(seq_id, start, start + n)
@@ -123,6 +148,7 @@ class BlockManager:
         """Release seq_id; a block returns to the stack when its reference count reaches 0."""
         table = self._tables.pop(seq_id)
         del self._lengths[seq_id]
+        self._arrays.pop(seq_id, None)
         released = []
         for b in table[::-1]:  # last block first, so the stack hands the blocks out again in table order
             self._ref[b] -= 1
@@ -143,6 +169,7 @@ class BlockManager:
         owners = [0] * self.num_blocks
         for seq_id, table in self._tables.items():
             assert len(table) == self.blocks_for(self._lengths[seq_id]), f"sequence {seq_id}: table size wrong"
+            assert self._arrays[seq_id][:len(table)].tolist() == table, f"sequence {seq_id}: array mirror differs"
             for b in table:
                 owners[b] += 1
         for b, n in enumerate(owners):

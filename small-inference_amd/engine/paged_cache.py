@@ -16,8 +16,10 @@ On a GPU pool, write() scatters K and V with one HIP store launch; a CPU pool us
 
 from __future__ import annotations
 
+from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from .attention import attention
@@ -26,6 +28,35 @@ from .config import ModelConfig
 
 BACKENDS = ("gather", "hip", "triton")
 KERNEL_BACKENDS = ("hip", "triton")
+
+
+class PerSequence(Sequence):
+    """A per-sequence list whose entries are made on first access and kept: the kernel path of a forward reads
+    none of them, the gather path only its own sequences'. Indexes, iterates and compares like a list."""
+
+    def __init__(self, n: int, make: Callable[[int], object]):
+        self._n, self._make = n, make
+        self._made: dict[int, object] = {}
+
+    def __len__(self) -> int:
+        return self._n
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return [self[j] for j in range(*i.indices(self._n))]
+        if i < 0:
+            i += self._n
+        if not 0 <= i < self._n:
+            raise IndexError(i)
+        if i not in self._made:
+            self._made[i] = self._make(i)
+        return self._made[i]
+
+    def __eq__(self, other) -> bool:
+        return list(self) == list(other)
+
+    def __repr__(self) -> str:
+        return repr(list(self))
 
 
 @dataclass
@@ -40,8 +71,8 @@ class PagedMetadata:
     slot_mapping: torch.Tensor  # [T] int64 slot of each new token
     slot_blocks: torch.Tensor  # [T] slot // block_size
     slot_offsets: torch.Tensor  # [T] slot % block_size
-    block_ids: list[torch.Tensor]  # per sequence: its first ceil(context_len / B) blocks, int64 on the device
-    block_ids_cpu: list[list[int]]  # the same on the CPU
+    block_ids: Sequence  # per sequence: its first ceil(context_len / B) blocks, int64 on the device (made on access)
+    block_ids_cpu: Sequence  # the same as lists on the CPU (made on access)
     block_tables: torch.Tensor  # [num_seqs, max_blocks] int32, padded with -1 (the kernel-facing form)
     context_lens_t: torch.Tensor  # [num_seqs] int32 on the device
     last_token_indices: torch.Tensor  # [num_seqs] row of each sequence's last new token
@@ -55,11 +86,18 @@ class PagedMetadata:
 def build_metadata(manager: BlockManager, batch: list[tuple[int, int, int]],
                    device: str | torch.device) -> PagedMetadata:
     """Metadata for a forward over batch = [(seq_id, start, n), ...]: n new tokens per sequence at positions
-    start .. start + n - 1, whose slots the manager already holds. Afterwards each context is start + n tokens."""
+    start .. start + n - 1, whose slots the manager already holds. Afterwards each context is start + n tokens.
+
+    Same contents as the reference's (engine/paged_cache.py:55-90). The tables come from the manager's int32
+    mirrors with array copies, and the device arrays travel in two host-to-device copies (one int64, one int32),
+    so a batch of 512 long sequences costs about a millisecond of host time instead of tens."""
     B = manager.block_size
+    S = len(batch)
+    if S == 0:
+        raise ValueError("a forward needs at least one sequence")
+    starts, lens, tables = [0], [], []
     positions: list[int] = []
     slot_list: list[int] = []
-    starts, lens, tables = [0], [], []
     for seq_id, start, n in batch:
         if n < 1:
             raise ValueError(f"sequence {seq_id}: a forward needs at least one new token")
@@ -67,30 +105,47 @@ def build_metadata(manager: BlockManager, batch: list[tuple[int, int, int]],
         held = manager.seq_len(seq_id)
         if held < ctx:
             raise ValueError(f"sequence {seq_id} holds {held} tokens, forward needs {ctx}")
-        positions.extend(range(start, ctx))
-        slot_list.extend(manager.slots(seq_id, start, ctx))
+        if start < 0:
+            raise ValueError(f"sequence {seq_id}: negative start {start}")
+        table = manager.table_array(seq_id)[:(ctx + B - 1) // B]
+        if n == 1:  # a decode row: one slot, no array work
+            positions.append(start)
+            slot_list.append(int(table[start // B]) * B + start % B)
+        else:
+            p = np.arange(start, ctx, dtype=np.int64)
+            positions.extend(p.tolist())
+            slot_list.extend((table[p // B].astype(np.int64) * B + p % B).tolist())
         starts.append(starts[-1] + n)
         lens.append(ctx)
-        tables.append(manager.block_table(seq_id)[:manager.blocks_for(ctx)])
-    width = max(len(t) for t in tables)
-
-    def dev64(xs):
-        return torch.tensor(xs, dtype=torch.int64, device=device)
-
+        tables.append(table)
+    T = len(positions)
+    width = max(t.shape[0] for t in tables)
+    # One int64 upload: positions, slots, slot blocks, slot offsets, last-token rows.
+    slots = np.asarray(slot_list, dtype=np.int64)
+    i64 = np.concatenate([np.asarray(positions, dtype=np.int64), slots, slots // B, slots % B,
+                          np.asarray(starts[1:], dtype=np.int64) - 1])
+    # One int32 upload: the -1 padded block tables, then the context lengths.
+    i32 = np.full(S * width + S, -1, dtype=np.int32)
+    bt = i32[:S * width].reshape(S, width)
+    for i, t in enumerate(tables):
+        bt[i, :t.shape[0]] = t
+    i32[S * width:] = lens
+    d64 = torch.from_numpy(i64).to(device)
+    d32 = torch.from_numpy(i32).to(device)
     return PagedMetadata(
-        num_tokens=len(positions),
+        num_tokens=T,
         query_starts=starts,
         context_lens=lens,
-        positions=dev64(positions),
+        positions=d64[:T],
         slots_cpu=slot_list,
-        slot_mapping=dev64(slot_list),
-        slot_blocks=dev64([s // B for s in slot_list]),
-        slot_offsets=dev64([s % B for s in slot_list]),
-        block_ids=[dev64(t) for t in tables],
-        block_ids_cpu=tables,
-        block_tables=torch.tensor([t + [-1] * (width - len(t)) for t in tables], dtype=torch.int32, device=device),
-        context_lens_t=torch.tensor(lens, dtype=torch.int32, device=device),
-        last_token_indices=dev64([e - 1 for e in starts[1:]]),
+        slot_mapping=d64[T:2 * T],
+        slot_blocks=d64[2 * T:3 * T],
+        slot_offsets=d64[3 * T:4 * T],
+        block_ids=PerSequence(S, lambda i: torch.from_numpy(tables[i].astype(np.int64)).to(device)),
+        block_ids_cpu=PerSequence(S, lambda i: tables[i].tolist()),
+        block_tables=d32[:S * width].view(S, width),
+        context_lens_t=d32[S * width:],
+        last_token_indices=d64[4 * T:],
     )
 
 

@@ -116,9 +116,10 @@ class QuantPagedKVCache(PagedKVCache):
         self._direct = (dev64(direct), dev64(direct_rows)) if direct else None
         for b in done:  # free now: nothing reassigns a slot before the next forward's begin()
             self._free_stage.append(self._stage_of.pop(b))
-        # Per sequence: the staging slot of its partial last block, -1 if the last block is full.
-        tails = [self._stage_of[meta.block_ids_cpu[i][-1]] if ctx % B else -1
-                 for i, ctx in enumerate(meta.context_lens)]
+        # Per sequence: the staging slot of its partial last block, -1 if the last block is full (the last block
+        # is the one holding the sequence's last new token).
+        last_slots = [meta.slots_cpu[e - 1] for e in meta.query_starts[1:]]
+        tails = [self._stage_of[last_slots[i] // B] if ctx % B else -1 for i, ctx in enumerate(meta.context_lens)]
         self._tails = torch.tensor(tails, dtype=torch.int32, device=dev)
         if self._decode is not None and len(self._decode_seqs) != meta.num_seqs:
             self._tails_dec = self._tails[torch.tensor(self._decode_seqs, device=dev)]

@@ -324,3 +324,32 @@ def test_torch_quantizer_bounds():
     e_tok = relative_error(x, dequantize(qt, st[:, None]))
     e_ch = relative_error(x, dequantize(qc, sc[None, :]))
     assert e_ch < e_tok / 3
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_metadata_matches_oracle_on_random_batches(seed):
+    """build_metadata (array mirrors, packed uploads, rows made on access) equals the oracle's restatement of the
+    reference's metadata on random mixes of decode rows and multi-token chunks over a fragmented pool."""
+    from oracle import paged_ref
+
+    rng = random.Random(seed)
+    B = rng.choice([4, 16])
+    m = fragmented(4096, B, seed)
+    batch, tables = [], {}
+    for s in range(rng.randint(1, 40)):
+        start = rng.randint(0, 300)
+        n = rng.choice([1, 1, 1, rng.randint(1, 70)])
+        m.allocate(s, start + n)
+        batch.append((s, start, n))
+        tables[s] = m.block_table(s)
+    meta = build_metadata(m, batch, "cpu")
+    ref = paged_ref.metadata(tables, batch, B)
+    for key in ("query_starts", "context_lens", "positions", "slot_mapping", "slot_blocks", "slot_offsets",
+                "block_tables", "last_token_indices"):
+        got = getattr(meta, key)
+        got = got.tolist() if isinstance(got, torch.Tensor) else got
+        assert got == ref[key], key
+    assert meta.slots_cpu == ref["slot_mapping"] and meta.num_tokens == ref["query_starts"][-1]
+    want = [tables[s][:-(-(start + n) // B)] for s, start, n in batch]
+    assert [b.tolist() for b in meta.block_ids] == want and meta.block_ids_cpu == want
+    assert meta.context_lens_t.dtype == meta.block_tables.dtype == torch.int32
