@@ -398,6 +398,13 @@ def details(steps: int, warmup: int) -> dict:
         torch.cuda.empty_cache()
     out.update(store_bench(steps))
     out["stream_read_ceiling"] = stream_ceiling(steps)
+    torch.cuda.empty_cache()
+    for fmt in ("bf16", "int8"):
+        try:
+            out[f"c5_decode_step_{fmt}"] = decode_step_bench(fmt=fmt)
+        except (RuntimeError, torch.OutOfMemoryError) as e:  # a box with less free HBM than the pool needs
+            out[f"c5_decode_step_{fmt}"] = {"error": str(e)[:200]}
+        torch.cuda.empty_cache()
     return out
 
 

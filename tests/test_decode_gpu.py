@@ -130,3 +130,37 @@ def test_work_list_block_sizes():
     """Work lists with 8- and 32-token blocks (VALU kernel): pieces start on 64-token boundaries."""
     for B in (8, 32):
         run(RAGGED + [3000], "0.5B", B, torch.float32, None, work_list="on")
+
+
+def test_decode_plan_replays_in_a_hip_graph():
+    """A layer loop of decode launches (split merge fused, workspace allocated and zeroed before capture, no
+    allocation or memset inside) captured in a HIP graph: every replay, with eager work and synchronizations in
+    between, equals the eager result bit for bit."""
+    from engine.hip_decode import DecodePlan
+
+    Hq, Hkv, D = HEADS["0.5B"]
+    layers = 3
+    q, k, v, bt, ctx, tables = make_case(RAGGED, Hq, Hkv, D, 16, torch.bfloat16, seed=7)
+    ks = [torch.randn_like(k) for _ in range(layers)]
+    vs = [torch.randn_like(v) for _ in range(layers)]
+    outs = [torch.empty_like(q) for _ in range(layers)]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        plan = DecodePlan(q, ks[0], vs[0], bt, ctx, D ** -0.5, max(RAGGED), num_splits=4)
+        for i in range(layers):
+            plan(k_cache=ks[i], v_cache=vs[i], out=outs[i])
+        stream.synchronize()
+        eager = [o.clone() for o in outs]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(layers):
+                plan(k_cache=ks[i], v_cache=vs[i], out=outs[i])
+        for rep in range(4):
+            for o in outs:
+                o.zero_()
+            graph.replay()
+            stream.synchronize()
+            for o, e in zip(outs, eager):
+                assert torch.equal(o, e), f"replay {rep}"
+            plan(k_cache=ks[0], v_cache=vs[0], out=torch.empty_like(q))  # eager work between replays
+            stream.synchronize()
