@@ -125,7 +125,8 @@ int32_t sipa_device_cu_count(int32_t device);
  */
 int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count);
 /* sipa_decode with num_splits <= 0 applies it with cu_count = the device's CUs for bf16/fp32 pools and twice
- * that for INT8 pools, whose kernels run two workgroups per CU. */
+ * that for INT8 pools, whose kernels run two workgroups per CU. INT8 pools also use at least
+ * ceil(max_context / 4096) splits whatever num_splits asks (size the workspace for that count). */
 
 /* Tokens per split for a call with num_splits splits: ceil(max_context / num_splits) rounded up to a multiple
  * of 64 tokens, at most 32768. Calls launch ceil(max_context / chunk) splits, which may be fewer than asked. */
@@ -140,15 +141,16 @@ int32_t sipa_decode(const sipa_decode_params* p, void* stream);
 /*
  * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,
  * split)): every (sequence, KV head) pair is cut into ceil(ctx / piece) splits of near-equal length, piece about
- * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, 256 .. 32768), and the items are
- * ordered longest first, so the longest work starts first and consecutive workgroups spread over the XCDs.
+ * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, 256 .. max_piece; max_piece <= 0
+ * means 32768, and INT8 pools need max_piece <= 4096), and the items are ordered longest first, so the longest
+ * work starts first and consecutive workgroups spread over the XCDs.
  * context_lens_host [num_seqs] (each >= 1) are the lengths the decode call will read. Writes at most capacity
  * items (8 int32 each) to items_out and the largest split count of a pair to *max_splits; returns the number of
  * items, or a negative SIPA_E* code (items_out may be NULL to ask for the count).
  */
 int32_t sipa_build_work_list(const int32_t* context_lens_host, int32_t num_seqs, int32_t num_kv_heads,
-                             int32_t cu_count, int32_t items_per_cu, int32_t* items_out, int32_t capacity,
-                             int32_t* max_splits);
+                             int32_t cu_count, int32_t items_per_cu, int32_t max_piece, int32_t* items_out,
+                             int32_t capacity, int32_t* max_splits);
 
 /*
  * Per-token INT8 quantize-and-store (reference engine/triton_quant.py:24-39,61-71 and the quantizer

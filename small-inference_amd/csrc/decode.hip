@@ -540,20 +540,24 @@ extern "C" int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits) {
   return split_chunk_host(max_context, num_splits);
 }
 
-// wgs_per_cu: workgroups of the chosen kernel that run on one CU at once (the INT8 kernels fit two).
-static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int wgs_per_cu, int* chunk) {
+// wgs_per_cu: workgroups of the chosen kernel that run on one CU at once (the INT8 kernels fit two); int8: the
+// INT8 kernels' splits are at most kMaxInt8Split tokens (more splits than requested if need be).
+static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int wgs_per_cu, bool int8, int* chunk) {
   int splits = requested;
   if (splits <= 0) splits = choose_splits_host(S, Hkv, max_ctx, wgs_per_cu * sipa_device_cu_count(-1));
+  if (int8) splits = std::max(splits, ceil_div(max_ctx, kMaxInt8Split));
   *chunk = split_chunk_host(max_ctx, splits);
   return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
 }
 
 extern "C" int32_t sipa_build_work_list(const int32_t* ctx, int32_t S, int32_t Hkv, int32_t cu_count,
-                                        int32_t items_per_cu, int32_t* items, int32_t capacity,
+                                        int32_t items_per_cu, int32_t max_piece, int32_t* items, int32_t capacity,
                                         int32_t* max_splits) {
   SIPA_CHECK(ctx != nullptr && S >= 0 && Hkv > 0, SIPA_EINVAL, "work list: bad arguments");
   if (cu_count <= 0) cu_count = 256;
   if (items_per_cu <= 0) items_per_cu = 2;
+  const int64_t cap = max_piece > 0 ? std::min<int64_t>(max_piece, kMaxSplitBlocks * 16) : kMaxSplitBlocks * 16;
+  SIPA_CHECK(cap >= kMinChunk, SIPA_EINVAL, "max_piece %d < %d", max_piece, kMinChunk);
   int64_t total = 0;
   for (int s = 0; s < S; ++s) {
     SIPA_CHECK(ctx[s] >= 1, SIPA_EINVAL, "context length %d of sequence %d < 1", ctx[s], s);
@@ -562,7 +566,7 @@ extern "C" int32_t sipa_build_work_list(const int32_t* ctx, int32_t S, int32_t H
   total *= Hkv;
   int64_t piece = (total + (int64_t)cu_count * items_per_cu - 1) / ((int64_t)cu_count * items_per_cu);
   piece = std::min<int64_t>(std::max<int64_t>((piece + kChunkAlign - 1) / kChunkAlign * kChunkAlign, kMinChunk),
-                            kMaxSplitBlocks * 16);
+                            cap / kChunkAlign * kChunkAlign);
   struct Item {
     int32_t s, h, sp, n, start, end;
   };
@@ -645,7 +649,8 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
     SIPA_CHECK(p->num_splits >= 1, SIPA_EINVAL, "with a work list, num_splits must be its largest split count");
     splits = p->num_splits;
   } else {
-    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, mode == SIPA_KV_PLAIN ? 1 : 2, &chunk);
+    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, mode == SIPA_KV_PLAIN ? 1 : 2,
+                            mode != SIPA_KV_PLAIN, &chunk);
   }
   SIPA_CHECK((int64_t)(Hq / Hkv) * splits * D * 4 < INT32_MAX, SIPA_EUNSUPPORTED,
              "%d splits: a KV head's partial rows exceed 2 GiB", splits);

@@ -45,10 +45,14 @@ template <int D>
 struct Int8Tile {
   u32x4 k[2][D / 64];   // K codes: lane (r, q4) holds token r's channels (D/4) q4 .. (D/4)(q4+1)
   u32x4 v[2][D / 64];   // V codes as 16-byte row chunks
-  uint2 ks[2];          // mode 1: K scales of tokens 4 q4 .. 4 q4 + 3 (fp16)
-  uint2 vs[2];          // V scales of the same tokens (fp16)
   uint32_t kc[2];       // mode 2: one 32-bit word (2 fp16 channel scales) of the block's D scales per lane
 };
+
+// Per-token scales (K in mode 1, V in every mode) of a whole split live in LDS, loaded in the prologue with one
+// 16-byte load per half block row: a tile then issues only its eight 16-byte code loads. (Per-tile 8-byte scale
+// loads made a third of the load instructions for 1.5% of the bytes, and load issue, not bytes, limited the
+// kernel.) Each block's 16 fp16 scales are 8 words.
+constexpr int kScaleBlocks = kMaxInt8Split / 16;
 
 // MODE 1: per-token K scales; 2: per-(block, channel) K scales; 3: mode 2 with one channel scale per (head,
 // channel) for every block (a zero block stride), folded into the query once.
@@ -63,6 +67,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   constexpr int QW = D / 4;    // channels per lane group
   __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
   __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
+  constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
+  __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
 
@@ -73,8 +79,9 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
+  const int wend = min(w.end, start + kMaxInt8Split);  // the host never makes longer splits; LDS holds no more
   int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(a, s, start, w.end, ids);
+  const int nb_spec = fetch_split_ids(a, s, start, wend, ids);
   // The query group in bf16, channel order of the int8 K layout: k-step j of lane (r, q4) (zero for r >= G).
   const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
   auto load_qb = [&](int j) {
@@ -104,7 +111,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   }
   const int ctx = a.ctx[s];
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
-  const int end = max(start, min(w.end, ctx));
+  const int end = max(start, min(wend, ctx));
   const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
   const int tail = (MODE >= 2) ? a.tail[s] : -1;       // staging slot of the partial last block, -1 if none
@@ -121,6 +128,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;
   auto tile_t0 = [&](int k) { return start + 32 * (wave + kWaves * k); };
 
+  const int nblk = (end - start + 15) >> 4;  // blocks of this split, <= kScaleBlocks
   auto load_tile = [&](int k, Int8Tile<D>& tl) {
     const int t0 = tile_t0(k);
     const int bi = (t0 - start) >> 4;
@@ -135,11 +143,14 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       for (int j = 0; j < KL; ++j) tl.k[mt][j] = __builtin_nontemporal_load((const u32x4*)(kb + r * D + QW * q4 + 16 * j));
 #pragma unroll
       for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
-      tl.vs[mt] = *(const uint2*)(vsh + blk * a.vs_sn + 4 * q4);
-      if (MODE == 1) tl.ks[mt] = *(const uint2*)(ksh + blk * a.ks_sn + 4 * q4);
       if (MODE == 2)  // lane L holds channels 2L, 2L + 1 (lanes past D / 2 repeat the first half)
         tl.kc[mt] = *(const uint32_t*)(ksh + blk * a.ks_sn + 2 * (lane % (D / 2)));
     }
+  };
+  // Token scales of tokens 4 q4 .. 4 q4 + 3 of the tile's block mt (a second block past the end reads the last).
+  auto token_scales = [&](int arr, int t0, int mt) {
+    const int bl = min(((t0 - start) >> 4) + mt, nblk - 1);
+    return *(const uint2*)(tsc + (arr * kScaleBlocks + bl) * 8 + 2 * q4);
   };
 
   float m_run = kNegInf, l_run = 0.f;
@@ -211,7 +222,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
         }
       }
       if (MODE == 1) {
-        const uint2 kw = tl.ks[mt];
+        const uint2 kw = token_scales(1, t0, mt);
         sc[mt][0] *= h2f(kw.x);
         sc[mt][1] *= h2f(kw.x >> 16);
         sc[mt][2] *= h2f(kw.y);
@@ -240,12 +251,13 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     }
     f16x8 pop;
     float psum = 0.f;
+    const uint2 vsc[2] = {token_scales(0, t0, 0), token_scales(0, t0, 1)};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int mt = i >> 2, e = i & 3;
       const float p = fast_exp2(fmaf(sc[mt][e], a.scale_log2, -m_run));
       psum += p;
-      const uint32_t vsw = (e < 2) ? tl.vs[mt].x : tl.vs[mt].y;
+      const uint32_t vsw = (e < 2) ? vsc[mt].x : vsc[mt].y;
       pop[i] = (_Float16)(p * h2f(vsw >> (16 * (e & 1))));
     }
     l_run += psum;
@@ -259,10 +271,36 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     wave_sync();
   };
 
+  // The split's token scales: one 16-byte load per half block row and array, issued before the first tiles'
+  // loads so that waiting for them does not wait for the tiles.
+  constexpr int kScaleLoads = (2 * kScaleBlocks + kThreads - 1) / kThreads;
+  u32x4 sreg[kScaleArrays][kScaleLoads];
+#pragma unroll
+  for (int arr = 0; arr < kScaleArrays; ++arr) {
+    const uint16_t* base = arr ? ksh : vsh;
+    const int64_t sn = arr ? a.ks_sn : a.vs_sn;
+#pragma unroll
+    for (int i = 0; i < kScaleLoads; ++i) {
+      const int c = threadIdx.x + kThreads * i;  // half block row c % 2 of block c / 2
+      const int64_t bid = nblk > 0 ? bids[min(c >> 1, nblk - 1)] : 0;  // an empty split reads block 0, unused
+      sreg[arr][i] = *(const u32x4*)(base + bid * sn + 8 * (c & 1));
+    }
+  }
   Int8Tile<D> ring[NB];
-  if (mine >= 2 * NB) {
+  const bool piped = mine >= 2 * NB;
+  if (piped) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) load_tile(j, ring[j]);
+  }
+#pragma unroll
+  for (int arr = 0; arr < kScaleArrays; ++arr)
+#pragma unroll
+    for (int i = 0; i < kScaleLoads; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      if (c < 2 * nblk) *(u32x4*)(tsc + (arr * kScaleBlocks + (c >> 1)) * 8 + 4 * (c & 1)) = sreg[arr][i];
+    }
+  __syncthreads();  // token scales staged
+  if (piped) {
     int k0 = 0;
     for (; k0 + 2 * NB <= mine; k0 += NB) {
 #pragma unroll

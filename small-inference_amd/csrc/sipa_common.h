@@ -20,6 +20,7 @@ constexpr int kMaxGroup = 16;      // query heads per KV head the kernels accept
 constexpr int kChunkAlign = 64;    // split chunks are multiples of 64 tokens (the reference's TILE)
 constexpr int kMinChunk = 256;     // smallest split the CU-count policy makes
 constexpr int kMaxChunk = 2048;    // largest split the policy makes when the grid is already full
+constexpr int kMaxInt8Split = 4096;  // longest split of the INT8 MFMA kernels (their token scales are staged in LDS)
 
 // ---- element conversions -------------------------------------------------------------------------------------
 

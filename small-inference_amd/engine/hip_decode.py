@@ -66,20 +66,24 @@ def choose_splits(num_seqs: int, num_kv_heads: int, max_context: int, cu_count: 
     return int(_hip.lib().sipa_choose_splits(num_seqs, num_kv_heads, max_context, cu))
 
 
+INT8_MAX_SPLIT = 4096  # the INT8 kernels stage a split's token scales in LDS: splits of at most this many tokens
+
+
 def build_work_list(context_lens: list[int], num_kv_heads: int, cu_count: int | None = None,
-                    items_per_cu: int = 2) -> tuple[np.ndarray, int]:
+                    items_per_cu: int = 2, max_piece: int = 0) -> tuple[np.ndarray, int]:
     """Work list for a ragged batch from host-side context lengths: ([n, 8] int32 items, largest split count of
     a pair). Each (sequence, KV head) pair is cut into near-equal pieces of about sum(ctx) * Hkv /
-    (cu_count * items_per_cu) tokens; items are ordered longest first."""
+    (cu_count * items_per_cu) tokens (at most max_piece; 0: 32768); items are ordered longest first."""
     cu = device_cu_count() if cu_count is None else cu_count
     ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
     lib, maxs = _hip.lib(), ctypes.c_int32(0)
-    n = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, None, 0, None)
+    n = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, max_piece, None, 0,
+                                 None)
     if n < 0:
         _hip.check(n, "build_work_list")
     items = np.zeros((n, 8), dtype=np.int32)
-    rc = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, items.ctypes.data, n,
-                                  ctypes.byref(maxs))
+    rc = lib.sipa_build_work_list(ctx.ctypes.data, len(ctx), num_kv_heads, cu, items_per_cu, max_piece,
+                                  items.ctypes.data, n, ctypes.byref(maxs))
     if rc < 0:
         _hip.check(rc, "build_work_list")
     return items, int(maxs.value)
@@ -151,7 +155,8 @@ class DecodePlan:
         if use_list:
             if len(host_context_lens) != S or max(host_context_lens, default=0) > max_context:
                 raise ValueError("host_context_lens must hold S lengths, none above max_context")
-            items, max_splits = build_work_list(host_context_lens, Hkv, device_cu_count(q.device))
+            items, max_splits = build_work_list(host_context_lens, Hkv, device_cu_count(q.device),
+                                                max_piece=0 if quant is None else INT8_MAX_SPLIT)
             self.items = torch.from_numpy(items).to(q.device)
             self._keep.append(self.items)
             self.requested = self.splits = max_splits
@@ -160,6 +165,8 @@ class DecodePlan:
             # The INT8 kernels run two workgroups per CU: size their grid for twice the CUs.
             wgs_per_cu = 1 if quant is None else 2
             self.requested = num_splits or choose_splits(S, Hkv, max_context, wgs_per_cu * device_cu_count(q.device))
+            if quant is not None:  # the library splits INT8 work into pieces of at most INT8_MAX_SPLIT tokens
+                self.requested = max(self.requested, math.ceil(max_context / INT8_MAX_SPLIT))
             self.splits, self.chunk = split_plan(max_context, self.requested)
 
         p = self.params = _hip.DecodeParams()

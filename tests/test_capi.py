@@ -99,14 +99,14 @@ def test_split_policy_host_side():
     assert lib.sipa_decode_workspace_bytes(32, 14, 2, 64, 1) == 0
 
 
-def work_list(lengths, Hkv, cu=256, per_cu=2):
+def work_list(lengths, Hkv, cu=256, per_cu=2, max_piece=0):
     lib = _hip.lib()
     ctx = (ctypes.c_int32 * len(lengths))(*lengths)
-    n = lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, None, 0, None)
+    n = lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, max_piece, None, 0, None)
     assert n > 0
     items = (ctypes.c_int32 * (8 * n))()
     maxs = ctypes.c_int32(0)
-    assert lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, items, n, ctypes.byref(maxs)) == n
+    assert lib.sipa_build_work_list(ctx, len(lengths), Hkv, cu, per_cu, max_piece, items, n, ctypes.byref(maxs)) == n
     return [tuple(items[8 * i:8 * i + 8]) for i in range(n)], maxs.value
 
 
@@ -144,7 +144,10 @@ def test_work_list_piece_size_and_errors():
     assert len(items) == 4 and maxs == 1
     lib = _hip.lib()
     bad = (ctypes.c_int32 * 2)(5, 0)
-    assert lib.sipa_build_work_list(bad, 2, 2, 256, 2, None, 0, None) == _hip.EINVAL
+    assert lib.sipa_build_work_list(bad, 2, 2, 256, 2, 0, None, 0, None) == _hip.EINVAL
     ok = (ctypes.c_int32 * 2)(5000, 7)
     small = (ctypes.c_int32 * 8)()
-    assert lib.sipa_build_work_list(ok, 2, 2, 256, 2, small, 1, None) == _hip.EINVAL
+    assert lib.sipa_build_work_list(ok, 2, 2, 256, 2, 0, small, 1, None) == _hip.EINVAL
+    assert lib.sipa_build_work_list(ok, 2, 2, 256, 2, 100, None, 0, None) == _hip.EINVAL  # max_piece < 256
+    items, maxs = work_list([40000, 300], 2, cu=4, per_cu=1, max_piece=4096)  # huge total: pieces capped
+    assert max(e - b for *_, b, e, _, _ in items) <= 4096 and maxs == 10
