@@ -330,6 +330,62 @@ def store_bench(steps: int) -> dict:
     return res
 
 
+def prefill_bench(steps: int, warmup: int) -> dict:
+    """Multi-token rows (prefill) with 0.5B shapes: the HIP paged prefill kernel against the reference's gather
+    path (per sequence: gather K/V out of the pool, engine/attention.py's bmm-softmax-bmm in bf16) on the same
+    inputs. Cases: 4 fresh 2048-token prompts, and one 512-token chunk at 8K context. Reports µs per call, the
+    causal attention TFLOP/s (4 D Hq flops per visible (query, key) pair) and the max-abs difference between the
+    two paths."""
+    from engine.attention import attention
+    from engine.hip_prefill import paged_prefill_attention
+
+    Hq, Hkv, D, B, N = 14, 2, 64, 16, 32768
+    res = {}
+    for name, ctx, qlen in (("prefill_4x2048_fresh", [2048] * 4, [2048] * 4), ("prefill_512_at_8k", [8192], [512])):
+        g = torch.Generator(device="cuda").manual_seed(3)
+        k = torch.randn(Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
+        v = torch.randn(Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
+        T = sum(qlen)
+        q = torch.randn(T, Hq, D, device="cuda", dtype=torch.bfloat16, generator=g)
+        tables = lifo_tables(N, ctx, B, 3)
+        bt = padded(tables, ctx, B)
+        starts = [sum(qlen[:i]) for i in range(len(qlen))]
+        i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device="cuda")  # noqa: E731
+        c, st, ln = i32(ctx), i32(starts), i32(qlen)
+        out = torch.empty_like(q)
+        scale = D ** -0.5
+
+        def kern(i):
+            paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out)
+
+        blocks = [torch.tensor(t[:-(-n // B)], device="cuda") for t, n in zip(tables, ctx)]
+        kpos = torch.arange(max(ctx), device="cuda")
+
+        def gather_path(i):
+            outs = []
+            for s in range(len(ctx)):
+                kk = k[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
+                vv = v[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
+                qpos = torch.arange(ctx[s] - qlen[s], ctx[s], device="cuda")
+                outs.append(attention(q[starts[s]:starts[s] + qlen[s]], kk, vv, qpos, kpos[:ctx[s]], scale))
+            return torch.cat(outs)
+
+        ms, kus = time_calls(kern, steps, warmup, True)
+        gms, _ = time_calls(gather_path, max(3, steps // 10), 2, False)
+        diff = (out.float().view(T, -1) - gather_path(0).float()).abs().max().item()
+        pairs = sum(sum(n - m + r + 1 for r in range(m)) for n, m in zip(ctx, qlen))
+        flops = 4 * D * Hq * pairs
+        res[name] = {"us_per_call": round(ms * 1e3, 2), "kernel_us": round(kus, 2),
+                     "tflop_s": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "frac_of_bf16_mfma_peak": round(flops / (ms * 1e-3) / 2.5e15, 4),
+                     "gather_path_us": round(gms * 1e3, 1), "speedup_vs_gather": round(gms / ms, 2),
+                     "max_abs_vs_gather_path": round(diff, 5), "tokens": T, "context": ctx}
+        del k, v
+        torch.cuda.empty_cache()
+    log(f"[bench] prefill: {json.dumps(res)}")
+    return res
+
+
 def stream_ceiling(steps: int) -> dict:
     """Read-only streaming ceiling of this GPU from the probe library (1 GiB buffers, 4 rotating)."""
     lib = ctypes.CDLL(str(ROOT / "small-inference_amd" / "build" / "libsmallinf_probe.so"))
@@ -397,6 +453,7 @@ def details(steps: int, warmup: int) -> dict:
         del wl
         torch.cuda.empty_cache()
     out.update(store_bench(steps))
+    out.update(prefill_bench(steps, warmup))
     out["stream_read_ceiling"] = stream_ceiling(steps)
     torch.cuda.empty_cache()
     for fmt in ("bf16", "int8"):
@@ -528,6 +585,8 @@ def main() -> int:
     ap.add_argument("--no-details", dest="details", action="store_false")
     ap.add_argument("--no-cpu", dest="cpu", action="store_false", default=True)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
+    ap.add_argument("--prefill", action="store_true", help="only run the paged prefill kernel against the "
+                    "gather path")
     ap.add_argument("--c5", action="store_true", help="only run config C5 (decode steps of a random-init 0.5B "
                     "model at batch 512 through the paged cache) and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -548,6 +607,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.prefill:
+        print(json.dumps(prefill_bench(args.steps, args.warmup)), flush=True)
+        return 0
     if args.c5:
         res = {}
         for fmt in ("bf16", "int8"):

@@ -139,6 +139,39 @@ int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32
 int32_t sipa_decode(const sipa_decode_params* p, void* stream);
 
 /*
+ * Paged attention for multi-token rows (prefill chunks): replaces the reference's gather path for rows with
+ * several new tokens (reference engine/paged_cache.py:149-155,174-175 with engine/attention.py:6-28). For each
+ * sequence s, rows query_starts[s] .. query_starts[s] + query_lens[s] - 1 of q are its new tokens at positions
+ * context_lens[s] - query_lens[s] .. context_lens[s] - 1 (their K/V already written to the pool); each attends
+ * causally to positions 0 .. its own, query head g to KV head g / (Hq / Hkv), softmax in fp32 with the
+ * probabilities rounded to bf16 for P.V, written to the same rows of out. bf16 q, pool and out; 16-token blocks;
+ * head_dim 64 or 128; group Hq / Hkv <= 8; max_context <= 32768. Context lengths are clamped to max_context and
+ * block ids to [0, num_blocks); q and out rows must be 16-byte aligned.
+ */
+typedef struct sipa_prefill_params {
+  int32_t struct_size;   /* sizeof(sipa_prefill_params) */
+  int32_t num_seqs;
+  int32_t num_tokens;    /* T: rows of q and out (rows past T are neither read nor written) */
+  int32_t num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context;
+  int32_t max_query_len; /* max over s of query_lens[s] (sizes the grid) */
+  float scale;
+  const void* q;         /* [T, Hq, D] bf16, last dim contiguous */
+  int64_t q_stride_t, q_stride_h;
+  const void* k_cache;   /* [Hkv, N, B, D] bf16 */
+  const void* v_cache;
+  int64_t kv_stride_h, kv_stride_n;
+  const int32_t* block_tables; /* [S, >= ceil(max_context / B)] */
+  int64_t bt_stride_s;
+  const int32_t* context_lens; /* [S] tokens in the cache, this forward's included */
+  const int32_t* query_starts; /* [S] first row of each sequence's new tokens */
+  const int32_t* query_lens;   /* [S] new tokens of each sequence (>= 1) */
+  void* out;                   /* [T, Hq, D] bf16 */
+  int64_t out_stride_t, out_stride_h;
+} sipa_prefill_params;
+
+int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
+
+/*
  * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,
  * split)): every (sequence, KV head) pair is cut into ceil(ctx / piece) splits of near-equal length, piece about
  * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, 256 .. max_piece; max_piece <= 0

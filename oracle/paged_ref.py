@@ -91,6 +91,30 @@ def decode(q, k_pool, v_pool, tables, lengths, scale, dtype=np.float64) -> np.nd
     return out
 
 
+def prefill(q, k_pool, v_pool, tables, context_lens, query_starts, query_lens, scale, dtype=np.float64):
+    """Causal attention of multi-token rows over the paged context (the reference's gather path for prefill
+    chunks, engine/paged_cache.py:149-155 with engine/attention.py:6-28): sequence s's new tokens are rows
+    query_starts[s] .. + query_lens[s] - 1 of q [T, Hq, D], at positions ctx - n .. ctx - 1 (ctx =
+    context_lens[s], n = query_lens[s]); the token at position p sees keys 0 .. p. Returns [T, Hq, D] in dtype
+    (rows of no sequence are zero)."""
+    T, Hq, D = q.shape
+    out = np.zeros((T, Hq, D), dtype=dtype)
+    for s, (ctx, q0, n) in enumerate(zip(context_lens, query_starts, query_lens)):
+        k = gather(k_pool, tables[s], ctx).astype(dtype)
+        v = gather(v_pool, tables[s], ctx).astype(dtype)
+        Hkv = k.shape[0]
+        g = Hq // Hkv
+        qs = q[q0:q0 + n].astype(dtype).reshape(n, Hkv, g, D).transpose(1, 2, 0, 3)  # [Hkv, g, n, D]
+        sc = np.matmul(qs, k.transpose(0, 2, 1)[:, None]) * dtype(scale)              # [Hkv, g, n, ctx]
+        pos = np.arange(ctx - n, ctx)[:, None]
+        sc = np.where(np.arange(ctx)[None, :] <= pos, sc, -np.inf)
+        sc = sc - sc.max(axis=-1, keepdims=True)
+        p = np.exp(sc)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[q0:q0 + n] = np.matmul(p, v[:, None]).transpose(2, 0, 1, 3).reshape(n, Hq, D)
+    return out
+
+
 # ---- INT8 dequantize-then-attend ---------------------------------------------------------------------------------
 
 def dequant_tokens(q_pool: np.ndarray, s_pool: np.ndarray) -> np.ndarray:

@@ -1,0 +1,282 @@
+// Paged attention for multi-token rows (prefill chunks) on the matrix cores (gfx950).
+//
+// Reference: the reference serves these rows with its gather path (engine/paged_cache.py:149-155,174-175):
+// every sequence's K/V are copied out of the pool and engine/attention.py:6-28 computes causal GQA attention
+// (query at position p sees keys 0 .. p, query head g uses KV head g / G, softmax in fp32, probabilities rounded
+// to the model dtype before P.V). This kernel computes the same rows in place from the pool.
+//
+// Work unit: (sequence s, KV head h, tile j of 16 consecutive new tokens). The unit's keys are positions
+// [0, P0 + ntok) of the sequence, P0 the position of the tile's first token. The four waves stream the same
+// 32-key tiles, which the workgroup loads cooperatively into double-buffered LDS (one HBM read per unit), and
+// each wave owns two query heads of the GQA group (heads w and w + 4), so no cross-wave merge is needed.
+// Per tile and head, with the decode kernels' layouts (decode.hip) and the query tokens in place of the heads:
+//   S^T[16 keys x 16 tokens] = K[16 x 32 d] . Q^T[32 d x 16 tokens]     v_mfma_f32_16x16x32_bf16
+//   causal mask: key position > token position -> -inf; online softmax per token (exp2 domain, lazy rescale)
+//   O^T[16 d x 16 tokens] += V^T . P^T   (V^T by transposing LDS reads, P^T from the S^T registers)
+#include "decode_common.h"
+
+namespace sipa {
+
+struct PrefillArgs {
+  const void* q;
+  int64_t q_st, q_sh;
+  const void* k;
+  const void* v;
+  int64_t kv_sh, kv_sn;
+  const int32_t* bt;
+  int64_t bt_ss;
+  const int32_t* ctx;     // [S] context lengths after this forward's writes
+  const int32_t* qstart;  // [S] first row of each sequence's new tokens in q / out
+  const int32_t* qlen;    // [S] new tokens per sequence
+  void* out;
+  int64_t o_st, o_sh;
+  int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / 16)
+  int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
+  float scale_log2;
+};
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPrefillHeadsPerWave = 2;  // group heads per wave: G <= 2 * kWaves
+
+template <int D>
+struct PrefillSmem {
+  static constexpr int kPitch = D + 8;       // bf16 per LDS row of a 32-key tile
+  static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
+};
+
+template <int D>
+__global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
+  constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
+  constexpr int CPK = D / 8;                // 16-byte chunks per key row
+  constexpr int LPT = 32 * CPK / kThreads;  // chunks per thread per K (or V) tile
+  static_assert(LPT * kThreads == 32 * CPK, "tile chunks must divide over the workgroup");
+  __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
+  __shared__ int bids[kMaxSplitBlocks];
+
+  const int L = blockIdx.x;
+  const int j = L % a.qtiles;
+  const int pair = L / a.qtiles;
+  const int s = pair % a.S, h = pair / a.S;
+  const int n = a.qlen[s];
+  if (16 * j >= n) return;
+  const int row0 = a.qstart[s] + 16 * j;
+  const int ctx = min(a.ctx[s], a.max_ctx);
+  const int ntok = min(min(16, n - 16 * j), a.T - row0);  // rows past T are not touched
+  if (ntok <= 0 || row0 < 0) return;
+  const int P0 = ctx - n + 16 * j;                       // position of the tile's first token
+  // keys [0, kv_end) are visible to some token (at most the block ids one workgroup stages)
+  const int kv_end = min(max(1, min(ctx, P0 + ntok)), kMaxSplitBlocks * 16);
+  const int nblk = min((kv_end + 15) >> 4, kMaxSplitBlocks);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const int G = a.G;
+
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
+  for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[i], 0), a.nb - 1);
+
+  // B operands: tokens r of heads g = wave + 4 hi (zero for padding tokens and heads past the group).
+  bf16x8 qop[kPrefillHeadsPerWave][KS];
+#pragma unroll
+  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+    const int g = wave + kWaves * hi;
+    const bool valid = g < G && r < ntok;
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(row0 + min(r, ntok - 1)) * a.q_st +
+                           (int64_t)(h * G + min(g, G - 1)) * a.q_sh;
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj) {
+      u32x4 u = *(const u32x4*)(qrow + 32 * jj + 8 * q4);
+      if (!valid) u = u32x4{0, 0, 0, 0};
+      qop[hi][jj] = __builtin_bit_cast(bf16x8, u);
+    }
+  }
+  float m_run[kPrefillHeadsPerWave], l_run[kPrefillHeadsPerWave];
+  f32x4 acc[kPrefillHeadsPerWave][DT];
+#pragma unroll
+  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+    m_run[hi] = kNegInf;
+    l_run[hi] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[hi][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();  // block ids staged
+
+  const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
+  const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
+  const int ntiles = (kv_end + 31) >> 5;
+  // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
+  // 8 (c % CPK) ..; keys past kv_end re-read the last visible key (finite values that the mask zeroes).
+  u32x4 kreg[LPT], vreg[LPT];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int pos = min(32 * t + c / CPK, kv_end - 1);
+      const int64_t off = (int64_t)bids[pos >> 4] * a.kv_sn + (pos & 15) * D + 8 * (c % CPK);
+      kreg[i] = __builtin_nontemporal_load((const u32x4*)(kh + off));
+      vreg[i] = __builtin_nontemporal_load((const u32x4*)(vh + off));
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int e = (c / CPK) * P + 8 * (c % CPK);
+      *(u32x4*)(&sm[buf][0][e]) = kreg[i];
+      *(u32x4*)(&sm[buf][1][e]) = vreg[i];
+    }
+  };
+  const int tr_off = tr16_offset(r, q4, P);
+  constexpr float kRescaleSlack = 8.f;  // p <= 2^8 against the lazily raised max (as in the decode kernel)
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) gload(t + 1);
+    const int t0 = 32 * t;
+    const bool masked = t0 + 31 > P0 || t0 + 32 > kv_end;  // some key of the tile is hidden from some token
+    const uint16_t* ks = sm[buf][0];
+    const uint16_t* vs = sm[buf][1];
+#pragma unroll
+    for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+      if (wave + kWaves * hi >= G) continue;  // wave-uniform
+      f32x4 sc[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < KS; ++jj) {
+          const bf16x8 kop = *(const bf16x8*)(ks + (16 * mt + r) * P + 32 * jj + 8 * q4);
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[hi][jj], sc[mt], 0, 0, 0);
+        }
+      }
+      if (masked) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kp = t0 + 16 * mt + 4 * q4 + i;  // key position of accumulator row (mt, q4, i)
+            if (kp > P0 + r || kp >= kv_end) sc[mt][i] = kNegInf;
+          }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx *= a.scale_log2;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[hi] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[hi], mx);
+        const float alpha = fast_exp2(m_run[hi] - m_new);  // 0 while m_run is -inf
+        l_run[hi] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[hi][dt] *= alpha;
+        m_run[hi] = m_new;
+      }
+      bf16x8 pop;
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_run[hi]));
+        psum += p;
+        pop[i] = (__bf16)p;
+      }
+      l_run[hi] += psum;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 vop = read_v_operand<bf16x8>(vs, tr_off, P, 16 * dt);
+        acc[hi][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[hi][dt], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) sstore(buf ^ 1);  // that buffer was last read in tile t - 1, before the last barrier
+    __syncthreads();
+  }
+
+  // Token r's output for each head: acc / l, with l summed over the four lanes that share the token.
+#pragma unroll
+  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+    const int g = wave + kWaves * hi;
+    float l = l_run[hi];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (g >= G || r >= ntok) continue;
+    const float inv = 1.f / l;
+    uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + r) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint32_t lo = f32_to_bf16_bits(acc[hi][dt][0] * inv) |
+                          ((uint32_t)f32_to_bf16_bits(acc[hi][dt][1] * inv) << 16);
+      const uint32_t hi2 = f32_to_bf16_bits(acc[hi][dt][2] * inv) |
+                           ((uint32_t)f32_to_bf16_bits(acc[hi][dt][3] * inv) << 16);
+      *(u32x2*)(orow + 16 * dt + 4 * q4) = u32x2{lo, hi2};
+    }
+  }
+}
+
+}  // namespace sipa
+
+using namespace sipa;
+
+static bool aligned16p(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
+  SIPA_CHECK(p != nullptr && p->struct_size == (int32_t)sizeof(sipa_prefill_params), SIPA_EINVAL,
+             "struct_size does not match this library's sipa_prefill_params (%d bytes)",
+             (int)sizeof(sipa_prefill_params));
+  const int S = p->num_seqs, Hq = p->num_q_heads, Hkv = p->num_kv_heads, D = p->head_dim;
+  if (S == 0 || p->max_query_len == 0) return SIPA_OK;
+  SIPA_CHECK(S > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, SIPA_EINVAL, "bad sequence or head counts");
+  const int G = Hq / Hkv;
+  SIPA_CHECK(G <= kPrefillHeadsPerWave * kWaves, SIPA_EUNSUPPORTED, "GQA group %d > %d", G,
+             kPrefillHeadsPerWave * kWaves);
+  SIPA_CHECK(D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {64, 128}", D);
+  SIPA_CHECK(p->block_size == 16, SIPA_EUNSUPPORTED, "block_size %d != 16", p->block_size);
+  SIPA_CHECK(p->max_context > 0 && p->max_context <= kMaxSplitBlocks * 16, SIPA_EUNSUPPORTED,
+             "max_context %d outside [1, %d]", p->max_context, kMaxSplitBlocks * 16);
+  SIPA_CHECK(p->max_query_len > 0, SIPA_EINVAL, "max_query_len %d", p->max_query_len);
+  SIPA_CHECK(p->q && p->k_cache && p->v_cache && p->block_tables && p->context_lens && p->query_starts &&
+                 p->query_lens && p->out, SIPA_EINVAL, "NULL pointer");
+  SIPA_CHECK(aligned16p(p->q) && p->q_stride_t % 8 == 0 && p->q_stride_h % 8 == 0, SIPA_EINVAL,
+             "q rows must be 16-byte aligned");
+  SIPA_CHECK(aligned16p(p->out) && p->out_stride_t % 8 == 0 && p->out_stride_h % 8 == 0, SIPA_EINVAL,
+             "out rows must be 16-byte aligned");
+  SIPA_CHECK(p->num_tokens > 0 && p->num_blocks > 0, SIPA_EINVAL, "num_tokens %d, num_blocks %d",
+             p->num_tokens, p->num_blocks);
+  SIPA_CHECK(aligned16p(p->k_cache) && aligned16p(p->v_cache) && p->kv_stride_h % 8 == 0 &&
+                 p->kv_stride_n % 8 == 0, SIPA_EINVAL, "K/V pools must be 16-byte aligned");
+  const int qtiles = (p->max_query_len + 15) / 16;
+  const int64_t wgs = (int64_t)S * Hkv * qtiles;
+  SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
+  PrefillArgs a;
+  a.q = p->q;
+  a.q_st = p->q_stride_t;
+  a.q_sh = p->q_stride_h;
+  a.k = p->k_cache;
+  a.v = p->v_cache;
+  a.kv_sh = p->kv_stride_h;
+  a.kv_sn = p->kv_stride_n;
+  a.bt = p->block_tables;
+  a.bt_ss = p->bt_stride_s;
+  a.ctx = p->context_lens;
+  a.qstart = p->query_starts;
+  a.qlen = p->query_lens;
+  a.out = p->out;
+  a.o_st = p->out_stride_t;
+  a.o_sh = p->out_stride_h;
+  a.S = S;
+  a.G = G;
+  a.qtiles = qtiles;
+  a.T = p->num_tokens;
+  a.nb = p->num_blocks;
+  a.max_ctx = p->max_context;
+  a.scale_log2 = p->scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 64)
+    hipLaunchKernelGGL(prefill_mfma_bf16<64>, dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(prefill_mfma_bf16<128>, dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
+  return SIPA_OK;
+}

@@ -50,6 +50,19 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
+class PrefillParams(ctypes.Structure):
+    """Mirror of struct sipa_prefill_params."""
+    _fields_ = [
+        ("struct_size", i32), ("num_seqs", i32), ("num_tokens", i32), ("num_q_heads", i32), ("num_kv_heads", i32),
+        ("head_dim", i32), ("block_size", i32), ("num_blocks", i32), ("max_context", i32), ("max_query_len", i32),
+        ("scale", f32),
+        ("q", vp), ("q_stride_t", i64), ("q_stride_h", i64),
+        ("k_cache", vp), ("v_cache", vp), ("kv_stride_h", i64), ("kv_stride_n", i64),
+        ("block_tables", vp), ("bt_stride_s", i64), ("context_lens", vp), ("query_starts", vp), ("query_lens", vp),
+        ("out", vp), ("out_stride_t", i64), ("out_stride_h", i64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol the header declares
 SIGNATURES = {
     "sipa_abi_version": (i32, []),
@@ -60,6 +73,7 @@ SIGNATURES = {
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp]),
+    "sipa_prefill": (i32, [_c.POINTER(PrefillParams), vp]),
     "sipa_quantize_store_tokens": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, i64, i64,
                                          vp]),
     "sipa_quantize_store_blocks": (i32, [vp, i32, i64, i64, i64, vp, vp, i32, i32, i32, i32, vp, i64, i64, vp, i64,

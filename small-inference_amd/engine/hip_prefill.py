@@ -1,0 +1,62 @@
+"""Paged attention for multi-token rows (prefill chunks) through libsmallinf_hip.so: the rows the reference
+serves with its gather path (engine/paged_cache.py:149-155,174-175 with engine/attention.py:6-28), computed in
+place from the block pool by one launch for all sequences of a forward.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _hip
+
+
+def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
+                      max_context: int) -> bool:
+    """Whether the prefill kernel covers this shape (bf16 q and pool, 16-token blocks, head_dim 64/128, GQA group
+    <= 8, contexts <= 32768); callers use the gather path otherwise."""
+    return (q_dtype == torch.bfloat16 and pool_dtype == torch.bfloat16 and block_size == 16 and
+            head_dim in (64, 128) and group <= 8 and 0 < max_context <= 32768)
+
+
+def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                            context_lens: torch.Tensor, query_starts: torch.Tensor, query_lens: torch.Tensor,
+                            scale: float, max_context: int, max_query_len: int,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal attention of every sequence's new tokens over its paged context.
+
+    q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16, one layer
+    of the pool with this forward's K/V already written; block_tables [S, >= ceil(max_context / 16)] int32;
+    context_lens [S] int32 (after the writes); query_starts, query_lens [S] int32: sequence s's new tokens are rows
+    query_starts[s] .. + query_lens[s] - 1 of q at positions context_lens[s] - query_lens[s] ..; max_context and
+    max_query_len are the host-known maxima. Writes those rows of out ([T, Hq, D], q's dtype; other rows are left
+    as they are) and returns out.
+    """
+    S = block_tables.shape[0]
+    T, Hq, D = q.shape
+    Hkv, N, B, _ = k_cache.shape
+    if out is None:
+        out = torch.empty_like(q)
+    for t in (block_tables, context_lens, query_starts, query_lens):
+        if t.dtype != torch.int32 or not t.is_contiguous() and t.dim() == 1:
+            raise ValueError("block tables, context lengths and query rows must be int32")
+    if q.stride(-1) != 1 or out.stride(-1) != 1 or out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("q and out must be [T, Hq, D] of one dtype with a contiguous last dim")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or block_tables.stride(-1) != 1:
+        raise ValueError("pools and block tables must be contiguous")
+    _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens, query_starts, query_lens, out)
+    p = _hip.PrefillParams()
+    p.struct_size = ctypes.sizeof(_hip.PrefillParams)
+    p.num_seqs, p.num_tokens, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = S, T, Hq, Hkv, D, B
+    p.num_blocks, p.max_context, p.max_query_len, p.scale = N, max_context, max_query_len, float(scale)
+    p.q, p.q_stride_t, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
+    p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
+    p.context_lens, p.query_starts, p.query_lens = context_lens.data_ptr(), query_starts.data_ptr(), query_lens.data_ptr()
+    p.out, p.out_stride_t, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise ValueError("the prefill kernel needs bf16 q and pools")
+    _hip.check(_hip.lib().sipa_prefill(ctypes.byref(p), _hip.stream_of(q)), "paged_prefill_attention")
+    return out

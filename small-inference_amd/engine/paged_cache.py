@@ -161,6 +161,7 @@ class PagedKVCache:
         self._allocate((cfg.num_layers, cfg.num_kv_heads, num_blocks, block_size, cfg.head_dim), device, dtype)
         self.meta: PagedMetadata | None = None
         self._decode = None
+        self._prefill_launch = None
         self._plan = None
         self._plan_scale = None
         self._arange = torch.empty(0, dtype=torch.int64, device=device)
@@ -185,6 +186,7 @@ class PagedKVCache:
             raise ValueError("a paged forward needs metadata for exactly its tokens")
         self.meta = meta
         self._decode = None
+        self._prefill_launch = None
         self._plan = None  # decode launch parameters, built by the first attend() of the forward
         if self.attn_backend not in KERNEL_BACKENDS:
             return
@@ -193,6 +195,20 @@ class PagedKVCache:
         per_seq = [meta.query_starts[i + 1] - meta.query_starts[i] for i in range(meta.num_seqs)]
         dec = [i for i, n in enumerate(per_seq) if n == 1]
         self._prefill = [i for i, n in enumerate(per_seq) if n > 1]
+        if self._prefill and self._prefill_kernel_ok(max(meta.context_lens[i] for i in self._prefill)):
+            # Multi-token rows run the paged prefill kernel in place of gather-then-attend: one launch per layer
+            # for all of them, with this subset of the metadata built once per forward.
+            pf = self._prefill
+            host = [meta.query_starts[i] for i in pf] + [per_seq[i] for i in pf]
+            rows = torch.tensor(host, dtype=torch.int32).to(self.device, non_blocking=True)
+            if len(pf) == meta.num_seqs:
+                bt, ctx = meta.block_tables, meta.context_lens_t
+            else:
+                idx = torch.tensor(pf, device=meta.positions.device)
+                bt, ctx = meta.block_tables[idx], meta.context_lens_t[idx]
+            self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):],
+                                    max(meta.context_lens[i] for i in pf), max(per_seq[i] for i in pf))
+            self._prefill = []
         if dec:
             # Once per forward, shared by every layer: the decode rows and their slice of the metadata.
             if len(dec) == meta.num_seqs:
@@ -235,16 +251,40 @@ class PagedKVCache:
         k, v = self.gather(layer, i)
         return attention(q[a:b], k, v, positions[a:b], self._key_positions(m.context_lens[i]), scale)
 
+    # The paged prefill kernel reads the model-dtype pool; caches with other pool formats leave multi-token rows
+    # on the gather path.
+    _prefill_pool_kernel = True
+
+    def _prefill_kernel_ok(self, max_context: int) -> bool:
+        """Whether this forward's multi-token rows can run the paged prefill kernel."""
+        from .hip_prefill import prefill_supported
+
+        cfg = self.cfg
+        return (self._prefill_pool_kernel and
+                prefill_supported(self.dtype, self.k.dtype, self.block_size, cfg.head_dim,
+                                  cfg.num_q_heads // cfg.num_kv_heads, max_context))
+
+    def _attend_prefill(self, layer: int, q: torch.Tensor, scale: float, out: torch.Tensor) -> None:
+        """Multi-token rows of the forward, written into their rows of out [T, Hq, d] by the prefill kernel."""
+        from .hip_prefill import paged_prefill_attention
+
+        bt, ctx, qs, ql, max_ctx, max_q = self._prefill_launch
+        paged_prefill_attention(q, self.k[layer], self.v[layer], bt, ctx, qs, ql, scale, max_ctx, max_q, out=out)
+
     def attend(self, layer: int, q: torch.Tensor, positions: torch.Tensor, scale: float) -> torch.Tensor:
         """Attention of every sequence in the forward over its own context. Returns [T, Hq * d]."""
         m = self.meta
+        T, Hq, d = q.shape
         if self._decode is None:
+            if self._prefill_launch is not None:  # only multi-token rows, all on the prefill kernel
+                out = torch.empty(T, Hq, d, device=q.device, dtype=q.dtype)
+                self._attend_prefill(layer, q, scale, out)
+                return out.view(T, Hq * d)
             outs = [self._attend_gather(layer, i, q, positions, scale) for i in range(m.num_seqs)]
             return outs[0] if len(outs) == 1 else torch.cat(outs)
         from .hip_decode import DecodePlan
 
         rows, bt, ctx, lens = self._decode
-        T, Hq, d = q.shape
         q_dec = q if rows is None else q[rows]
         quant = self._kernel_quant(layer)
         if self._plan is None or self._plan_scale != scale:  # first layer of the forward: validate once
@@ -259,6 +299,8 @@ class PagedKVCache:
             return dec.view(T, Hq * d)
         out = torch.empty(T, Hq * d, device=q.device, dtype=q.dtype)
         out[rows] = dec.view(-1, Hq * d)
+        if self._prefill_launch is not None:
+            self._attend_prefill(layer, q, scale, out.view(T, Hq, d))
         for i in self._prefill:
             out[m.query_starts[i]:m.query_starts[i + 1]] = self._attend_gather(layer, i, q, positions, scale)
         return out

@@ -44,6 +44,7 @@ def blocks_for_budget(cfg: ModelConfig, fmt: str, budget_bytes: int, block_size:
 
 
 class QuantPagedKVCache(PagedKVCache):
+    _prefill_pool_kernel = False  # INT8 pools: multi-token rows attend over the dequantized gather
     def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int, device: str | torch.device,
                  dtype: torch.dtype, attn_backend: str = "gather", fmt: str = "int8",
                  manager: BlockManager | None = None, n_stage: int = 128):

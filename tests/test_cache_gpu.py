@@ -4,8 +4,10 @@ decode rows and prefill chunks, as engine/model.py:145-146 drives it (reference 
 
 Checked against the oracle: each row's softmax attention over the cache contents gathered back to fp32 (for the
 INT8 caches, the dequantized contents), causal within a chunk. Tolerances: fp32 caches 1e-5; bf16 decode rows
-(the HIP kernel) 8e-3 max-abs; bf16 prefill rows 3e-2, since they run the reference's gather path, which computes
-scores and probabilities in the model dtype (engine/attention.py).
+(the HIP decode kernel) 8e-3 max-abs; bf16 prefill rows of the model-dtype cache (the HIP prefill kernel) 8e-3
+max-abs where |out| < 2 and 2^-7 |out| above, whose bf16 rounding alone reaches 2^-8 |out|; bf16 prefill rows of
+the INT8 caches 3e-2, since they run the reference's gather path, which computes scores and probabilities in the
+model dtype (engine/attention.py).
 """
 
 import numpy as np
@@ -60,16 +62,40 @@ def reference(cache, meta, q, layer):
     return np.stack(rows).reshape(len(rows), cfg.num_q_heads * d)
 
 
+def check_rows(cache, meta, q, out, layer, dtype, what):
+    ref = reference(cache, meta, q, layer)
+    got = out.float().cpu().numpy()
+    err = np.abs(got - ref)
+    chunk = {r for a, b in zip(meta.query_starts, meta.query_starts[1:]) if b - a > 1 for r in range(a, b)}
+    dec = np.array([r not in chunk for r in range(meta.num_tokens)])
+    if dtype == torch.float32:
+        assert err.max() <= 1e-5, f"{what}: {err.max():.3e}"
+        return
+    if dec.any():
+        assert err[dec].max() <= 8e-3, f"{what}: decode rows {err[dec].max():.3e}"
+    if not (~dec).any():
+        return
+    if isinstance(cache, QuantPagedKVCache):  # gather path in the model dtype
+        assert err[~dec].max() <= 3e-2, f"{what}: chunk rows {err[~dec].max():.3e}"
+        return
+    big = np.abs(ref[~dec]) >= 2
+    e = err[~dec]
+    assert e[~big].max(initial=0.0) <= 8e-3, f"{what}: chunk rows {e[~big].max(initial=0.0):.3e}"
+    assert (e[big] / np.abs(ref[~dec][big])).max(initial=0.0) <= 2 ** -7, f"{what}: chunk rows, |out| >= 2"
+
+
 def run_mixed(make_cache, dtype, D, seed):
     gen = torch.Generator().manual_seed(seed)
     m = fragmented_manager(256, 16, gen)
     cache = make_cache(m)
     print(f"case {type(cache).__name__} {getattr(cache, 'fmt', 'model')} {dtype} D={D} seed={seed}", flush=True)
-    for layer in range(2):
+    for layer in range(2):  # prompts only
         for s, n in ((1, 70), (2, 300), (3, 16)):
             if s not in m.seq_ids():
                 m.allocate(s, n)
-        forward(m, cache, [(1, 0, 70), (2, 0, 300), (3, 0, 16)], layer, gen, dtype)
+        meta, q, out = forward(m, cache, [(1, 0, 70), (2, 0, 300), (3, 0, 16)], layer, gen, dtype)
+        torch.cuda.synchronize()
+        check_rows(cache, meta, q, out, layer, dtype, f"prompts layer {layer}")
     for step in range(3):  # decode steps mixed with a prefill chunk of a new sequence
         for s in (1, 2, 3):
             m.append_slot(s)
@@ -81,14 +107,7 @@ def run_mixed(make_cache, dtype, D, seed):
         for layer in range(2):
             meta, q, out = forward(m, cache, batch, layer, gen, dtype)
             torch.cuda.synchronize()
-            ref = reference(cache, meta, q, layer)
-            err = np.abs(out.float().cpu().numpy() - ref).max(axis=1)
-            chunk = {r for a, b in zip(meta.query_starts, meta.query_starts[1:]) if b - a > 1 for r in range(a, b)}
-            dec = np.array([r not in chunk for r in range(meta.num_tokens)])
-            tol_dec, tol_chunk = (1e-5, 1e-5) if dtype == torch.float32 else (8e-3, 3e-2)
-            assert err[dec].max() <= tol_dec, f"step {step} layer {layer}: decode rows {err[dec].max():.3e}"
-            if (~dec).any():
-                assert err[~dec].max() <= tol_chunk, f"step {step} layer {layer}: chunk {err[~dec].max():.3e}"
+            check_rows(cache, meta, q, out, layer, dtype, f"step {step} layer {layer}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])

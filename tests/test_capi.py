@@ -151,3 +151,44 @@ def test_work_list_piece_size_and_errors():
     assert lib.sipa_build_work_list(ok, 2, 2, 256, 2, 100, None, 0, None) == _hip.EINVAL  # max_piece < 256
     items, maxs = work_list([40000, 300], 2, cu=4, per_cu=1, max_piece=4096)  # huge total: pieces capped
     assert max(e - b for *_, b, e, _, _ in items) <= 4096 and maxs == 10
+
+
+def prefill_params(**over):
+    p = _hip.PrefillParams()
+    p.struct_size = ctypes.sizeof(_hip.PrefillParams)
+    p.num_seqs, p.num_tokens, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = 2, 40, 14, 2, 64, 16
+    p.num_blocks, p.max_context, p.max_query_len, p.scale = 8, 64, 32, 0.125
+    p.q_stride_t, p.q_stride_h, p.out_stride_t, p.out_stride_h = 14 * 64, 64, 14 * 64, 64
+    p.kv_stride_h, p.kv_stride_n, p.bt_stride_s = 8 * 16 * 64, 16 * 64, 4
+    for ptr in ("q", "k_cache", "v_cache", "block_tables", "context_lens", "query_starts", "query_lens", "out"):
+        setattr(p, ptr, 4096)
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"struct_size": 8}, _hip.EINVAL),
+    ({"num_q_heads": 13}, _hip.EINVAL),
+    ({"num_q_heads": 18}, _hip.EUNSUPPORTED),           # group 9 > 8
+    ({"head_dim": 96}, _hip.EUNSUPPORTED),
+    ({"block_size": 32}, _hip.EUNSUPPORTED),
+    ({"max_context": 32784}, _hip.EUNSUPPORTED),
+    ({"num_tokens": 0}, _hip.EINVAL),
+    ({"query_lens": None}, _hip.EINVAL),
+    ({"q": 4100}, _hip.EINVAL),                         # unaligned rows
+    ({"out_stride_h": 66}, _hip.EINVAL),
+    ({"kv_stride_n": 1020}, _hip.EINVAL),
+])
+def test_prefill_rejects_bad_arguments_before_launch(over, code):
+    lib = _hip.lib()
+    rc = lib.sipa_prefill(ctypes.byref(prefill_params(**over)), None)
+    assert rc == code, lib.sipa_last_error()
+    assert lib.sipa_last_error()
+
+
+def test_prefill_layout_and_empty_calls():
+    """The binding's struct size is the library's (a mismatch is rejected), and empty batches launch nothing."""
+    lib = _hip.lib()
+    assert lib.sipa_prefill(ctypes.byref(prefill_params(num_seqs=0)), None) == _hip.OK
+    assert lib.sipa_prefill(ctypes.byref(prefill_params(max_query_len=0)), None) == _hip.OK

@@ -196,6 +196,56 @@ def test_gather_and_decode_follow_the_block_table():
                                paged_ref.attend_one(q[0], seq_k, seq_k, 0.5))
 
 
+def scatter_sequences(rng, lengths, Hkv, D, B, N):
+    """Random pool [Hkv, N, B, D] holding sequences of these lengths through shuffled block tables; returns the
+    pool, the tables and the contiguous [Hkv, n, D] sequences."""
+    pool = rng.standard_normal((Hkv, N, B, D))
+    free = list(rng.permutation(N))
+    tables, seqs = [], []
+    for n in lengths:
+        t = [int(free.pop()) for _ in range(-(-n // B))]
+        x = rng.standard_normal((Hkv, n, D))
+        for p in range(n):
+            pool[:, t[p // B], p % B] = x[:, p]
+        tables.append(t)
+        seqs.append(x)
+    return pool, tables, seqs
+
+
+def test_prefill_fresh_sequence_matches_sdpa_causal():
+    """A sequence's first chunk (context == new tokens) is torch's causal scaled_dot_product_attention."""
+    rng = np.random.default_rng(13)
+    Hq, Hkv, D, B, n = 6, 2, 16, 4, 23
+    kp, tables, ks = scatter_sequences(rng, [n], Hkv, D, B, 12)
+    vp, _, _ = scatter_sequences(np.random.default_rng(13), [n], Hkv, D, B, 12)  # same tables, other values
+    vs = paged_ref.gather(vp, tables[0], n)
+    q = rng.standard_normal((n, Hq, D))
+    got = paged_ref.prefill(q, kp, vp, tables, [n], [0], [n], 0.3)
+    qt = torch.from_numpy(q).permute(1, 0, 2)                                         # [Hq, n, D]
+    kk = torch.from_numpy(ks[0]).repeat_interleave(Hq // Hkv, 0)
+    vv = torch.from_numpy(vs).repeat_interleave(Hq // Hkv, 0)
+    want = torch.nn.functional.scaled_dot_product_attention(qt, kk, vv, is_causal=True, scale=0.3)
+    np.testing.assert_allclose(got, want.permute(1, 0, 2).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_chunk_rows_are_decode_rows():
+    """Mid-context chunks of a packed batch: row r of sequence s (position ctx - n + r) equals one-token attention
+    over keys 0 .. its position; rows of no sequence stay zero."""
+    rng = np.random.default_rng(14)
+    Hq, Hkv, D, B = 8, 2, 8, 4
+    ctx, qlen = [9, 30, 5], [4, 17, 1]
+    pool, tables, seqs = scatter_sequences(rng, ctx, Hkv, D, B, 20)
+    starts = [0, 6, 23]                      # rows 4, 5 and 24.. belong to no sequence
+    q = rng.standard_normal((26, Hq, D))
+    got = paged_ref.prefill(q, pool, pool, tables, ctx, starts, qlen, 0.25)
+    for s in range(3):
+        for r in range(qlen[s]):
+            n = ctx[s] - qlen[s] + r + 1
+            want = paged_ref.attend_one(q[starts[s] + r], seqs[s][:, :n], seqs[s][:, :n], 0.25)
+            np.testing.assert_allclose(got[starts[s] + r], want, rtol=1e-12, atol=1e-12)
+    assert not got[[4, 5, 24, 25]].any()
+
+
 def test_kchannel_gather_reads_tail_from_staging():
     rng = np.random.default_rng(12)
     H, N, B, D, n = 2, 6, 4, 8, 10  # 2 full blocks + 2 staged tokens

@@ -1,0 +1,142 @@
+"""Parity of the HIP paged prefill kernel (multi-token rows attending causally over the paged context) with the
+CPU oracle, on the shapes the reference serves: fresh prompts and mid-context chunks, ragged chunk lengths around
+the 16-token tile and 32-key tile boundaries, shuffled block tables, GQA groups 1 .. 8, head_dim 64 and 128.
+
+Tolerances, written here: against the fp32 oracle, max-abs 8e-3 where |out| < 2 (the decode kernels' bound) and
+2^-7 |out| where |out| >= 2, since short contexts give outputs of a few units whose bf16 rounding alone reaches
+2^-8 |out| (the reference's own path rounds scores, probabilities and outputs to bf16 too,
+engine/attention.py:22-27); rtol/atol 1e-2 against fp64 beside it; a torch fp32 reference on the GPU for the
+long-context case.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import as_np32, fragmented_manager
+from engine.hip_prefill import paged_prefill_attention
+from oracle import paged_ref
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"0.5B": (14, 2, 64), "1.5B": (12, 2, 128), "g4": (32, 8, 128), "g8": (16, 2, 64), "g1": (4, 4, 64)}
+SENTINEL = 7.0
+
+
+def make_prefill(ctx, qlen, Hq, Hkv, D, seed=0, gap=0, device="cuda"):
+    """Pools over a fragmented manager, -1 padded tables, q rows packed with `gap` unused rows between sequences.
+    Returns q, k, v, bt, ctx, starts, lens (device int32) and the tables, row starts and T."""
+    B = 16
+    g = torch.Generator().manual_seed(seed)
+    need = sum(-(-n // B) for n in ctx)
+    m = fragmented_manager(max(2 * need, 1), B, g)
+    for i, n in enumerate(ctx):
+        m.allocate(i, n)
+    tables = [m.block_table(i) for i in range(len(ctx))]
+    starts, T = [], 0
+    for n in qlen:
+        starts.append(T)
+        T += n + gap
+    k = torch.randn(Hkv, m.num_blocks, B, D, generator=g).to(device, torch.bfloat16)
+    v = torch.randn(Hkv, m.num_blocks, B, D, generator=g).to(device, torch.bfloat16)
+    q = torch.randn(T, Hq, D, generator=g).to(device, torch.bfloat16)
+
+    def i32(x):
+        return torch.tensor(x, dtype=torch.int32, device=device)
+
+    bt = torch.from_numpy(paged_ref.padded_tables(tables, ctx, B)).to(device)
+    return q, k, v, bt, i32(ctx), i32(starts), i32(qlen), tables, starts, T
+
+
+def assert_bf16_close(got, ref, what=""):
+    """max-abs 8e-3 where |ref| < 2, relative 2^-7 where |ref| >= 2."""
+    big = np.abs(ref) >= 2
+    err = np.abs(got - ref)
+    small_err = err[~big].max(initial=0.0)
+    assert small_err <= 8e-3, f"{what} max-abs {small_err:.3e} vs fp32 reference (|out| < 2)"
+    rel = (err[big] / np.abs(ref[big])).max(initial=0.0)
+    assert rel <= 2 ** -7, f"{what} max relative {rel:.3e} vs fp32 reference (|out| >= 2)"
+
+
+def check(ctx, qlen, shape, seed=0, gap=0):
+    Hq, Hkv, D = SHAPES[shape]
+    print(f"case ctx={ctx[:6]} qlen={qlen[:6]} shape={shape} seed={seed} gap={gap}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed, gap)
+    scale = D ** -0.5
+    out = torch.full_like(q, SENTINEL)
+    paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out)
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
+    ref32, ref64 = paged_ref.prefill(*args, dtype=np.float32), paged_ref.prefill(*args, dtype=np.float64)
+    rows = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, qlen)])
+    other = np.setdiff1d(np.arange(T), rows)
+    assert_bf16_close(got[rows], ref32[rows])
+    np.testing.assert_allclose(got[rows], ref64[rows], rtol=1e-2, atol=1e-2)
+    assert (got[other] == SENTINEL).all(), "rows of no sequence were written"
+    return out
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_fresh_prompts(shape):
+    """First chunks (context == new tokens) of ragged lengths around the tile boundaries."""
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 64, 100]
+    check(lens, lens, shape)
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g8"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_mid_context_chunks(shape, seed):
+    """Chunks after a cached prefix (chunked prefill): prefix lengths on and off block and tile boundaries."""
+    ctx = [300, 1000, 33, 16, 48, 517, 129]
+    qlen = [64, 7, 33, 1, 32, 500, 16]
+    check(ctx, qlen, shape, seed, gap=3)
+
+
+def test_single_token_rows_equal_decode():
+    """One-token chunks are decode rows: the prefill kernel agrees with the oracle's decode at every length."""
+    lens = [1, 15, 16, 17, 33, 100, 1000]
+    check(lens, [1] * len(lens), "0.5B")
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+def test_long_context_chunk_against_torch(shape):
+    """A 512-token chunk at 8K context (and a 2K prompt) against torch fp32 attention on the GPU, row blocks at a
+    time; repeated launches give identical bits."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [8192, 2048], [512, 2048]
+    print(f"case long ctx={ctx} qlen={qlen} shape={shape}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=5)
+    scale = D ** -0.5
+    out = paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen))
+    again = paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen))
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    G = Hq // Hkv
+    for s in range(2):
+        idx = torch.tensor(tables[s][:-(-ctx[s] // 16)], device="cuda", dtype=torch.int64)
+        kk = k.index_select(1, idx).reshape(Hkv, -1, D)[:, :ctx[s]].float().repeat_interleave(G, 0)
+        vv = v.index_select(1, idx).reshape(Hkv, -1, D)[:, :ctx[s]].float().repeat_interleave(G, 0)
+        for r0 in range(0, qlen[s], 256):
+            r1 = min(r0 + 256, qlen[s])
+            qq = q[starts[s] + r0:starts[s] + r1].float().permute(1, 0, 2)                 # [Hq, rows, D]
+            sc = torch.matmul(qq, kk.transpose(1, 2).contiguous()) * scale
+            pos = torch.arange(ctx[s] - qlen[s] + r0, ctx[s] - qlen[s] + r1, device="cuda")[:, None]
+            sc = sc.masked_fill(torch.arange(ctx[s], device="cuda")[None, :] > pos, float("-inf"))
+            want = torch.matmul(torch.softmax(sc, -1), vv).permute(1, 0, 2)
+            assert_bf16_close(out[starts[s] + r0:starts[s] + r1].double().cpu().numpy(),
+                              want.double().cpu().numpy(), f"seq {s} rows {r0}..{r1}")
+
+
+def test_strided_q_view():
+    """q as a view into a fused QKV projection (row stride past Hq * D) and a head-strided out."""
+    Hq, Hkv, D = SHAPES["0.5B"]
+    ctx, qlen = [70, 40], [70, 24]
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=3)
+    fused = torch.zeros(T, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device="cuda")
+    fused[:, :Hq * D] = q.reshape(T, -1)
+    qv = fused[:, :Hq * D].view(T, Hq, D)
+    out = paged_prefill_attention(qv, k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen))
+    ref = paged_prefill_attention(q.contiguous(), k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
