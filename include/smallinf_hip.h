@@ -96,8 +96,10 @@ typedef struct sipa_decode_params {
   int64_t st_stride_h, st_stride_n, st_stride_b;
   const int32_t* tail_slots;
   /* Split partials and merge counters; at least sipa_decode_workspace_bytes() bytes, 256-byte aligned. The
-     counter words must be zero before the first call that uses the buffer; every completed call leaves them
-     zero again. Calls that share one workspace must be ordered (one stream). May be NULL when 1 split runs. */
+     first 256 KiB hold the merge counters (at most 65536 (sequence, KV head) pairs per split call), which must be
+     zero before the first call that uses the buffer; every completed call leaves them zero again and no call
+     writes partials there, so one buffer serves decode and prefill calls of any size. Calls that share one
+     workspace must be ordered (one stream). May be NULL when 1 split runs. */
   void* workspace;
   int64_t workspace_bytes;
   /* Optional work list (fields read only when struct_size covers them): num_items > 0 launches one workgroup
@@ -167,9 +169,24 @@ typedef struct sipa_prefill_params {
   const int32_t* query_lens;   /* [S] new tokens of each sequence (>= 1) */
   void* out;                   /* [T, Hq, D] bf16 */
   int64_t out_stride_t, out_stride_h;
+  /* Key splits per 16-token query tile (<= 0: sipa_prefill_splits with units = S x Hkv x query tiles) and the
+     workspace they need when more than one split runs: sipa_prefill_workspace_bytes() bytes, laid out and reused
+     as sipa_decode_params.workspace (the same buffer may serve both); at most 65536 KV heads x query tiles. */
+  int32_t num_splits;
+  void* workspace;
+  int64_t workspace_bytes;
 } sipa_prefill_params;
 
 int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
+
+/* Key splits for a prefill call (no counterpart in the reference, whose gather path has no grid): about two
+ * workgroups per CU over num_kv_heads x query_tiles units (query_tiles = sum over sequences of
+ * ceil(query_len / 16)), at least 256 keys per split, at most 32 splits; cu_count <= 0 asks the current device. */
+int32_t sipa_prefill_splits(int32_t num_kv_heads, int64_t query_tiles, int32_t max_context, int32_t cu_count);
+
+/* Workspace bytes sipa_prefill needs for these sizes and num_splits (0 when one split runs). */
+int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t max_query_len, int32_t max_context, int32_t num_splits);
 
 /*
  * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,

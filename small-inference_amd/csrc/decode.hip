@@ -434,7 +434,7 @@ struct WorkspaceLayout {
 static WorkspaceLayout workspace_layout(int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t splits) {
   WorkspaceLayout w;
   w.counters = 0;
-  w.pm = align256(S * Hkv * 4);
+  w.pm = kCounterBytes;
   w.pl = w.pm + align256(S * Hq * splits * 4);
   w.part = w.pl + align256(S * Hq * splits * 4);
   w.total = w.part + align256(S * Hq * splits * D * 4);
@@ -696,6 +696,9 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.scale_log2 = p->scale * 1.4426950408889634f;
 
   if (splits > 1) {
+    SIPA_CHECK((int64_t)S * Hkv <= kMaxCounters, SIPA_EINVAL,
+               "%lld (sequence, KV head) pairs exceed the %d merge counters of a split launch", (long long)S * Hkv,
+               kMaxCounters);
     const WorkspaceLayout w = workspace_layout(S, Hq, Hkv, D, splits);
     SIPA_CHECK(p->workspace != nullptr && p->workspace_bytes >= w.total, SIPA_EWORKSPACE,
                "workspace of %lld bytes needed for %d splits (got %lld)", (long long)w.total, splits,

@@ -6,13 +6,18 @@
 // to the model dtype before P.V). This kernel computes the same rows in place from the pool.
 //
 // Work unit: (sequence s, KV head h, tile j of 16 consecutive new tokens). The unit's keys are positions
-// [0, P0 + ntok) of the sequence, P0 the position of the tile's first token. The four waves stream the same
-// 32-key tiles, which the workgroup loads cooperatively into double-buffered LDS (one HBM read per unit), and
-// each wave owns two query heads of the GQA group (heads w and w + 4), so no cross-wave merge is needed.
+// [0, P0 + ntok) of the sequence, P0 the position of the tile's first token; they are cut into splits of `chunk`
+// keys, one workgroup each, so that a short chunk over a long context still fills the chip. The four waves of a
+// workgroup stream the same 32-key tiles, which the workgroup loads cooperatively into double-buffered LDS (one
+// HBM read per split), and each wave owns two query heads of the GQA group (heads w and w + 4), so no cross-wave
+// merge is needed. A unit with one split writes its rows; otherwise every split writes its softmax state
+// (m, l, unnormalised O) and the last split workgroup of the unit to finish merges them, as the decode kernels do.
 // Per tile and head, with the decode kernels' layouts (decode.hip) and the query tokens in place of the heads:
 //   S^T[16 keys x 16 tokens] = K[16 x 32 d] . Q^T[32 d x 16 tokens]     v_mfma_f32_16x16x32_bf16
 //   causal mask: key position > token position -> -inf; online softmax per token (exp2 domain, lazy rescale)
 //   O^T[16 d x 16 tokens] += V^T . P^T   (V^T by transposing LDS reads, P^T from the S^T registers)
+#include <algorithm>
+
 #include "decode_common.h"
 
 namespace sipa {
@@ -32,12 +37,53 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
   int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / 16)
   int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
+  int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 32)
   float scale_log2;
+  int* counters;           // [units] split arrivals, zero between launches
+  float* pm;               // [units][nsplit][8 heads][16 tokens] running max (exp2 domain)
+  float* pl;               // same shape: softmax denominators
+  float* part;             // [units][nsplit][8 heads][16 tokens][D] unnormalised outputs
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPrefillHeadsPerWave = 2;  // group heads per wave: G <= 2 * kWaves
+constexpr int kPrefillSlots = kPrefillHeadsPerWave * kWaves * 16;  // (head, token) rows of a unit's split state
+constexpr int kPrefillMaxSplits = 32;
+
+// Merge one round of up to KB splits j0 .. of one (head, token) row: every load issued before the first is used;
+// entries past nvalid re-read the last split and get weight 0. Split 0 always holds the row's first key, so M is
+// finite from the first round on.
+template <int KB>
+__device__ __forceinline__ void prefill_merge_round(const PrefillArgs& a, __amdgpu_buffer_rsrc_t rows,
+                                                    int64_t mrow, int off, int split_bytes, int j0, int nvalid,
+                                                    float& M, float& den, f32x4& num) {
+  float mj[KB], lj[KB];
+  f32x4 pj[KB];
+#pragma unroll
+  for (int u = 0; u < KB; ++u) {
+    const int j = min(j0 + u, nvalid - 1);
+    mj[u] = load_coherent(a.pm + mrow + (int64_t)j * kPrefillSlots);
+    lj[u] = load_coherent(a.pl + mrow + (int64_t)j * kPrefillSlots);
+    pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, off + j * split_bytes, 0, kAuxSc1);
+  }
+#pragma unroll
+  for (int u = 0; u < KB; ++u)
+    if (j0 + u >= nvalid) mj[u] = kNegInf;
+  float mb = M;
+#pragma unroll
+  for (int u = 0; u < KB; ++u) mb = fmaxf(mb, mj[u]);
+  const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf, mb finite)
+  den *= rescale;
+  num *= rescale;
+#pragma unroll
+  for (int u = 0; u < KB; ++u) {
+    const float w = fast_exp2(mj[u] - mb);  // 0 for padding entries and for splits the token sees nothing of
+    den += w * lj[u];
+    num += w * pj[u];
+  }
+  M = mb;
+}
 
 template <int D>
 struct PrefillSmem {
@@ -54,9 +100,15 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
 
+  __shared__ int last_flag;
+
+  // Splits fastest: consecutive workgroups (which the dispatcher deals round-robin to the 8 XCDs) take the
+  // splits of one unit, so each XCD's L2 serves one key range to every query tile of a sequence.
   const int L = blockIdx.x;
-  const int j = L % a.qtiles;
-  const int pair = L / a.qtiles;
+  const int sp = L % a.nsplit;
+  const int u = L / a.nsplit;
+  const int j = u % a.qtiles;
+  const int pair = u / a.qtiles;
   const int s = pair % a.S, h = pair / a.S;
   const int n = a.qlen[s];
   if (16 * j >= n) return;
@@ -65,14 +117,18 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const int ntok = min(min(16, n - 16 * j), a.T - row0);  // rows past T are not touched
   if (ntok <= 0 || row0 < 0) return;
   const int P0 = ctx - n + 16 * j;                       // position of the tile's first token
-  // keys [0, kv_end) are visible to some token (at most the block ids one workgroup stages)
-  const int kv_end = min(max(1, min(ctx, P0 + ntok)), kMaxSplitBlocks * 16);
-  const int nblk = min((kv_end + 15) >> 4, kMaxSplitBlocks);
+  // keys [0, kv_vis) are visible to some token of the tile; this split takes [k_lo, kv_end)
+  const int kv_vis = max(1, min(ctx, P0 + ntok));
+  const int nvalid = (kv_vis + a.chunk - 1) / a.chunk;
+  const int k_lo = sp * a.chunk;
+  if (k_lo >= kv_vis) return;
+  const int kv_end = min(k_lo + a.chunk, kv_vis);
+  const int nblk = min((kv_end - k_lo + 15) >> 4, kMaxSplitBlocks);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
   const int G = a.G;
 
-  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
+  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
   for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[i], 0), a.nb - 1);
 
   // B operands: tokens r of heads g = wave + 4 hi (zero for padding tokens and heads past the group).
@@ -85,9 +141,9 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
                            (int64_t)(h * G + min(g, G - 1)) * a.q_sh;
 #pragma unroll
     for (int jj = 0; jj < KS; ++jj) {
-      u32x4 u = *(const u32x4*)(qrow + 32 * jj + 8 * q4);
-      if (!valid) u = u32x4{0, 0, 0, 0};
-      qop[hi][jj] = __builtin_bit_cast(bf16x8, u);
+      u32x4 qv = *(const u32x4*)(qrow + 32 * jj + 8 * q4);
+      if (!valid) qv = u32x4{0, 0, 0, 0};
+      qop[hi][jj] = __builtin_bit_cast(bf16x8, qv);
     }
   }
   float m_run[kPrefillHeadsPerWave], l_run[kPrefillHeadsPerWave];
@@ -103,16 +159,16 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 
   const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
   const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
-  const int ntiles = (kv_end + 31) >> 5;
+  const int ntiles = (kv_end - k_lo + 31) >> 5;
   // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
-  // 8 (c % CPK) ..; keys past kv_end re-read the last visible key (finite values that the mask zeroes).
+  // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes).
   u32x4 kreg[LPT], vreg[LPT];
   auto gload = [&](int t) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i;
-      const int pos = min(32 * t + c / CPK, kv_end - 1);
-      const int64_t off = (int64_t)bids[pos >> 4] * a.kv_sn + (pos & 15) * D + 8 * (c % CPK);
+      const int rel = min(32 * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
+      const int64_t off = (int64_t)bids[rel >> 4] * a.kv_sn + (rel & 15) * D + 8 * (c % CPK);
       kreg[i] = __builtin_nontemporal_load((const u32x4*)(kh + off));
       vreg[i] = __builtin_nontemporal_load((const u32x4*)(vh + off));
     }
@@ -135,7 +191,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) gload(t + 1);
-    const int t0 = 32 * t;
+    const int t0 = k_lo + 32 * t;
     const bool masked = t0 + 31 > P0 || t0 + 32 > kv_end;  // some key of the tile is hidden from some token
     const uint16_t* ks = sm[buf][0];
     const uint16_t* vs = sm[buf][1];
@@ -166,19 +222,22 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       mx *= a.scale_log2;
+      // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
+      // below are taken as 0 then, so that -inf - -inf never forms.
       if (__builtin_amdgcn_ballot_w64(mx > m_run[hi] + kRescaleSlack)) {
         const float m_new = fmaxf(m_run[hi], mx);
-        const float alpha = fast_exp2(m_run[hi] - m_new);  // 0 while m_run is -inf
+        const float alpha = fast_exp2(m_run[hi] - (m_new == kNegInf ? 0.f : m_new));  // 0 while m_run is -inf
         l_run[hi] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[hi][dt] *= alpha;
         m_run[hi] = m_new;
       }
+      const float m_off = m_run[hi] == kNegInf ? 0.f : m_run[hi];
       bf16x8 pop;
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_run[hi]));
+        const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_off));
         psum += p;
         pop[i] = (__bf16)p;
       }
@@ -193,13 +252,74 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     __syncthreads();
   }
 
-  // Token r's output for each head: acc / l, with l summed over the four lanes that share the token.
+  float lsum[kPrefillHeadsPerWave];  // token r's denominators, summed over the four lanes that share the token
 #pragma unroll
   for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-    const int g = wave + kWaves * hi;
     float l = l_run[hi];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    lsum[hi] = l;
+  }
+  if (nvalid > 1) {
+    // This split's state for (head g, token r): m, l at slot 16 g + r, O at channels 16 dt + 4 q4 .. of that row.
+    const int64_t base = ((int64_t)u * a.nsplit + sp) * kPrefillSlots;
+    const int split_bytes = kPrefillSlots * D * 4;
+    const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+        a.part + (int64_t)u * a.nsplit * kPrefillSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
+#pragma unroll
+    for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+      const int g = wave + kWaves * hi;
+      if (g >= G || r >= ntok) continue;
+      const int slot = 16 * g + r;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[hi][dt], rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 4,
+                                               0, kAuxSc1);
+      if (q4 == 0) {
+        store_coherent(a.pm + base + slot, m_run[hi]);
+        store_coherent(a.pl + base + slot, lsum[hi]);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = __hip_atomic_fetch_add(a.counters + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = (prev == nvalid - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    // The last split to arrive: one thread per (head, token, channel quad) merges every split's state.
+    constexpr int Q = D / 4;
+    for (int idx = threadIdx.x; idx < G * ntok * Q; idx += kThreads) {
+      const int g = idx / (ntok * Q), rem = idx % (ntok * Q);
+      const int rr = rem / Q, c = rem % Q;
+      const int slot = 16 * g + rr;
+      const int64_t mrow = (int64_t)u * a.nsplit * kPrefillSlots + slot;
+      const int off = (slot * D + 4 * c) * 4;
+      float M = kNegInf, den = 0.f;
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      if (nvalid <= 4) {
+        prefill_merge_round<4>(a, rows, mrow, off, split_bytes, 0, nvalid, M, den, num);
+      } else {
+        for (int j0 = 0; j0 < nvalid; j0 += 8)
+          prefill_merge_round<8>(a, rows, mrow, off, split_bytes, j0, nvalid, M, den, num);
+      }
+      const f32x4 o = num / den;
+      uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + rr) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
+      const uint32_t lo = f32_to_bf16_bits(o[0]) | ((uint32_t)f32_to_bf16_bits(o[1]) << 16);
+      const uint32_t hi2 = f32_to_bf16_bits(o[2]) | ((uint32_t)f32_to_bf16_bits(o[3]) << 16);
+      *(u32x2*)(orow + 4 * c) = u32x2{lo, hi2};
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // One split: token r's output for each head is acc / l.
+#pragma unroll
+  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
+    const int g = wave + kWaves * hi;
+    const float l = lsum[hi];
     if (g >= G || r >= ntok) continue;
     const float inv = 1.f / l;
     uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + r) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
@@ -219,6 +339,56 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 using namespace sipa;
 
 static bool aligned16p(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Keys per split for a requested split count: ceil(max_context / splits) rounded up to a multiple of 32 (the key
+// tile), at least 256; the launch then has ceil(max_context / chunk) splits.
+static int prefill_chunk(int max_context, int splits) {
+  splits = std::max(1, std::min(splits, kPrefillMaxSplits));
+  const int c = (max_context + splits - 1) / splits;
+  return std::max(256, (c + 31) / 32 * 32);
+}
+
+// Split count policy: about two workgroups per CU over all query tiles (units = KV heads x query tiles of
+// 16 tokens), no split under 256 keys, at most 32.
+static int prefill_splits_host(int64_t units, int max_context, int cu_count) {
+  if (units <= 0 || max_context <= 0) return 1;
+  const int64_t target = 2LL * std::max(cu_count, 1);
+  const int want = (int)std::min<int64_t>((target + units - 1) / units, kPrefillMaxSplits);
+  const int chunk = prefill_chunk(max_context, want);
+  return (max_context + chunk - 1) / chunk;
+}
+
+struct PrefillLayout {
+  int64_t counters, pm, pl, part, total;  // byte offsets into the workspace
+};
+
+static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  PrefillLayout l;
+  const int64_t rows = units * nsplit * kPrefillSlots;
+  l.counters = 0;
+  l.pm = kCounterBytes;
+  l.pl = l.pm + up(rows * 4);
+  l.part = l.pl + up(rows * 4);
+  l.total = l.part + up(rows * D * 4);
+  return l;
+}
+
+extern "C" int32_t sipa_prefill_splits(int32_t num_kv_heads, int64_t query_tiles, int32_t max_context,
+                                       int32_t cu_count) {
+  if (cu_count <= 0) cu_count = sipa_device_cu_count(-1);
+  return prefill_splits_host((int64_t)num_kv_heads * query_tiles, max_context, cu_count);
+}
+
+extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t head_dim,
+                                                int32_t max_query_len, int32_t max_context, int32_t num_splits) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || max_query_len <= 0 || max_context <= 0) return 0;
+  const int chunk = prefill_chunk(max_context, num_splits);
+  const int nsplit = (max_context + chunk - 1) / chunk;
+  if (nsplit <= 1) return 0;
+  const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + 15) / 16);
+  return prefill_layout(units, nsplit, head_dim).total;
+}
 
 extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   SIPA_CHECK(p != nullptr && p->struct_size == (int32_t)sizeof(sipa_prefill_params), SIPA_EINVAL,
@@ -246,8 +416,24 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   SIPA_CHECK(aligned16p(p->k_cache) && aligned16p(p->v_cache) && p->kv_stride_h % 8 == 0 &&
                  p->kv_stride_n % 8 == 0, SIPA_EINVAL, "K/V pools must be 16-byte aligned");
   const int qtiles = (p->max_query_len + 15) / 16;
-  const int64_t wgs = (int64_t)S * Hkv * qtiles;
+  const int64_t units = (int64_t)S * Hkv * qtiles;
+  int splits = p->num_splits;
+  if (splits <= 0) splits = prefill_splits_host(units, p->max_context, sipa_device_cu_count(-1));
+  const int chunk = prefill_chunk(p->max_context, splits);
+  const int nsplit = (p->max_context + chunk - 1) / chunk;
+  const int64_t wgs = units * nsplit;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
+  PrefillLayout lay{};
+  if (nsplit > 1) {
+    SIPA_CHECK(units <= kMaxCounters, SIPA_EINVAL,
+               "%lld query tiles x KV heads exceed the %d merge counters of a split launch; use one split",
+               (long long)units, kMaxCounters);
+    lay = prefill_layout(units, nsplit, D);
+    SIPA_CHECK(p->workspace != nullptr && ((uintptr_t)p->workspace & 255) == 0 && p->workspace_bytes >= lay.total,
+               SIPA_EWORKSPACE, "%d key splits need a 256-byte aligned workspace of %lld bytes (have %lld)", nsplit,
+               (long long)lay.total, (long long)p->workspace_bytes);
+    SIPA_CHECK((int64_t)nsplit * kPrefillSlots * D * 4 <= 0x7fffffff, SIPA_EINVAL, "split state too large");
+  }
   PrefillArgs a;
   a.q = p->q;
   a.q_st = p->q_stride_t;
@@ -271,6 +457,13 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.nb = p->num_blocks;
   a.max_ctx = p->max_context;
   a.scale_log2 = p->scale * 1.4426950408889634f;
+  a.nsplit = nsplit;
+  a.chunk = chunk;
+  char* ws = (char*)p->workspace;
+  a.counters = nsplit > 1 ? (int*)(ws + lay.counters) : nullptr;
+  a.pm = nsplit > 1 ? (float*)(ws + lay.pm) : nullptr;
+  a.pl = nsplit > 1 ? (float*)(ws + lay.pl) : nullptr;
+  a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (D == 64)
     hipLaunchKernelGGL(prefill_mfma_bf16<64>, dim3((unsigned)wgs), dim3(kThreads), 0, st, a);

@@ -20,6 +20,11 @@ constexpr int kMaxGroup = 16;      // query heads per KV head the kernels accept
 constexpr int kChunkAlign = 64;    // split chunks are multiples of 64 tokens (the reference's TILE)
 constexpr int kMinChunk = 256;     // smallest split the CU-count policy makes
 constexpr int kMaxChunk = 2048;    // largest split the policy makes when the grid is already full
+// Split workspaces (decode and prefill) keep their merge counters in a fixed region at the start, which no call
+// writes partials into: every call leaves the counters it used at zero, so one zero-filled workspace serves calls
+// of any size, decode and prefill alike, in any order on one stream.
+constexpr int64_t kCounterBytes = 1 << 18;
+constexpr int kMaxCounters = (int)(kCounterBytes / 4);
 constexpr int kMaxInt8Split = 4096;  // longest split of the INT8 MFMA kernels (their token scales are staged in LDS)
 
 // ---- element conversions -------------------------------------------------------------------------------------

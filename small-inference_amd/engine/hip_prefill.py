@@ -10,6 +10,7 @@ import ctypes
 import torch
 
 from . import _hip
+from .hip_decode import _workspace  # one split workspace per (device, stream) serves decode and prefill
 
 
 def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
@@ -20,10 +21,17 @@ def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size:
             head_dim in (64, 128) and group <= 8 and 0 < max_context <= 32768)
 
 
+def prefill_splits(num_kv_heads: int, query_lens: list[int], max_context: int, cu_count: int = 0) -> int:
+    """Key splits per query tile for a call whose sequences have these new-token counts (library policy)."""
+    tiles = sum(-(-n // 16) for n in query_lens)
+    return _hip.lib().sipa_prefill_splits(num_kv_heads, tiles, max_context, cu_count)
+
+
 def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                             context_lens: torch.Tensor, query_starts: torch.Tensor, query_lens: torch.Tensor,
                             scale: float, max_context: int, max_query_len: int,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None, *, num_splits: int | None = None,
+                            host_query_lens: list[int] | None = None) -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16, one layer
@@ -31,7 +39,8 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     context_lens [S] int32 (after the writes); query_starts, query_lens [S] int32: sequence s's new tokens are rows
     query_starts[s] .. + query_lens[s] - 1 of q at positions context_lens[s] - query_lens[s] ..; max_context and
     max_query_len are the host-known maxima. Writes those rows of out ([T, Hq, D], q's dtype; other rows are left
-    as they are) and returns out.
+    as they are) and returns out. Each 16-token query tile's keys are cut into num_splits splits (default: the
+    library's policy over host_query_lens when given, else over S x ceil(max_query_len / 16) tiles).
     """
     S = block_tables.shape[0]
     T, Hq, D = q.shape
@@ -58,5 +67,15 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     p.out, p.out_stride_t, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
         raise ValueError("the prefill kernel needs bf16 q and pools")
-    _hip.check(_hip.lib().sipa_prefill(ctypes.byref(p), _hip.stream_of(q)), "paged_prefill_attention")
+    lib = _hip.lib()
+    if num_splits is None:
+        lens = host_query_lens if host_query_lens is not None else [max_query_len] * S
+        num_splits = prefill_splits(Hkv, lens, max_context)
+    p.num_splits = num_splits
+    stream = _hip.stream_of(q)
+    nbytes = lib.sipa_prefill_workspace_bytes(S, Hkv, D, max_query_len, max_context, num_splits)
+    if nbytes > 0:
+        ws = _workspace(q.device, stream, nbytes)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    _hip.check(lib.sipa_prefill(ctypes.byref(p), stream), "paged_prefill_attention")
     return out

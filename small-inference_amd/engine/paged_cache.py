@@ -206,8 +206,12 @@ class PagedKVCache:
             else:
                 idx = torch.tensor(pf, device=meta.positions.device)
                 bt, ctx = meta.block_tables[idx], meta.context_lens_t[idx]
-            self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):],
-                                    max(meta.context_lens[i] for i in pf), max(per_seq[i] for i in pf))
+            from .hip_prefill import prefill_splits
+
+            max_ctx = max(meta.context_lens[i] for i in pf)
+            splits = prefill_splits(self.cfg.num_kv_heads, [per_seq[i] for i in pf], max_ctx)
+            self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):], max_ctx, max(per_seq[i] for i in pf),
+                                    splits)
             self._prefill = []
         if dec:
             # Once per forward, shared by every layer: the decode rows and their slice of the metadata.
@@ -268,8 +272,9 @@ class PagedKVCache:
         """Multi-token rows of the forward, written into their rows of out [T, Hq, d] by the prefill kernel."""
         from .hip_prefill import paged_prefill_attention
 
-        bt, ctx, qs, ql, max_ctx, max_q = self._prefill_launch
-        paged_prefill_attention(q, self.k[layer], self.v[layer], bt, ctx, qs, ql, scale, max_ctx, max_q, out=out)
+        bt, ctx, qs, ql, max_ctx, max_q, splits = self._prefill_launch
+        paged_prefill_attention(q, self.k[layer], self.v[layer], bt, ctx, qs, ql, scale, max_ctx, max_q, out=out,
+                                num_splits=splits)
 
     def attend(self, layer: int, q: torch.Tensor, positions: torch.Tensor, scale: float) -> torch.Tensor:
         """Attention of every sequence in the forward over its own context. Returns [T, Hq * d]."""

@@ -164,3 +164,10 @@ def test_decode_plan_replays_in_a_hip_graph():
                 assert torch.equal(o, e), f"replay {rep}"
             plan(k_cache=ks[0], v_cache=vs[0], out=torch.empty_like(q))  # eager work between replays
             stream.synchronize()
+
+
+def test_workspace_reuse_with_more_pairs():
+    """Split calls on one workspace with a growing number of (sequence, KV head) pairs: 2 sequences then 300,
+    both split 4 ways; the second call's merge counters must not overlap the first call's partials."""
+    run([3000, 2000], "0.5B", 16, torch.bfloat16, 4)
+    run([600] * 300, "0.5B", 16, torch.bfloat16, 4, seed=1)

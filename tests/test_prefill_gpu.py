@@ -58,13 +58,14 @@ def assert_bf16_close(got, ref, what=""):
     assert rel <= 2 ** -7, f"{what} max relative {rel:.3e} vs fp32 reference (|out| >= 2)"
 
 
-def check(ctx, qlen, shape, seed=0, gap=0):
+def check(ctx, qlen, shape, seed=0, gap=0, splits=None):
     Hq, Hkv, D = SHAPES[shape]
-    print(f"case ctx={ctx[:6]} qlen={qlen[:6]} shape={shape} seed={seed} gap={gap}", flush=True)
+    print(f"case ctx={ctx[:6]} qlen={qlen[:6]} shape={shape} seed={seed} gap={gap} splits={splits}", flush=True)
     q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed, gap)
     scale = D ** -0.5
     out = torch.full_like(q, SENTINEL)
-    paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out)
+    paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out, num_splits=splits,
+                            host_query_lens=qlen)
     torch.cuda.synchronize()
     got = out.double().cpu().numpy()
     args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
@@ -86,11 +87,20 @@ def test_fresh_prompts(shape):
 
 @pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g8"])
 @pytest.mark.parametrize("seed", [0, 1])
-def test_mid_context_chunks(shape, seed):
-    """Chunks after a cached prefix (chunked prefill): prefix lengths on and off block and tile boundaries."""
-    ctx = [300, 1000, 33, 16, 48, 517, 129]
-    qlen = [64, 7, 33, 1, 32, 500, 16]
-    check(ctx, qlen, shape, seed, gap=3)
+@pytest.mark.parametrize("splits", [1, 4, None], ids=["one_split", "split256", "auto"])
+def test_mid_context_chunks(shape, seed, splits):
+    """Chunks after a cached prefix (chunked prefill): prefix lengths on and off block and tile boundaries; key
+    splits of 256 keys put split starts inside query tiles (tokens that see none of a split's keys)."""
+    ctx = [300, 1000, 33, 16, 48, 517, 129, 280]
+    qlen = [64, 7, 33, 1, 32, 500, 16, 30]
+    check(ctx, qlen, shape, seed, gap=3, splits=splits)
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+@pytest.mark.parametrize("splits", [2, 7, 32])
+def test_split_counts(shape, splits):
+    """A long chunk over a longer prefix at several split counts (32: more splits than 256-key chunks allow)."""
+    check([3000, 700], [700, 300], shape, seed=splits, splits=splits)
 
 
 def test_single_token_rows_equal_decode():
@@ -128,6 +138,33 @@ def test_long_context_chunk_against_torch(shape):
                               want.double().cpu().numpy(), f"seq {s} rows {r0}..{r1}")
 
 
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+def test_chunk_at_8k_splits_against_torch(shape):
+    """The reference scheduler's default step (one 512-token chunk) at 8K context runs split (the policy gives
+    8 splits of 1024 keys on 256 CUs): torch fp32 on the GPU agrees, and launches with the workspace reused (split
+    counts 8, 3, 8) give the same bits each time the split count repeats."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [8192], [512]
+    print(f"case chunk at 8k shape={shape}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=6)
+    scale = D ** -0.5
+    run = lambda n: paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=n)  # noqa: E731
+    a, b, a2 = run(8), run(3), run(8)
+    torch.cuda.synchronize()
+    assert torch.equal(a, a2)
+    G = Hq // Hkv
+    idx = torch.tensor(tables[0], device="cuda", dtype=torch.int64)
+    kk = k.index_select(1, idx).reshape(Hkv, -1, D)[:, :8192].float().repeat_interleave(G, 0)
+    vv = v.index_select(1, idx).reshape(Hkv, -1, D)[:, :8192].float().repeat_interleave(G, 0)
+    qq = q.float().permute(1, 0, 2)
+    sc = torch.matmul(qq, kk.transpose(1, 2).contiguous()) * scale
+    pos = torch.arange(8192 - 512, 8192, device="cuda")[:, None]
+    sc = sc.masked_fill(torch.arange(8192, device="cuda")[None, :] > pos, float("-inf"))
+    want = torch.matmul(torch.softmax(sc, -1), vv).permute(1, 0, 2).double().cpu().numpy()
+    for got in (a, b):
+        assert_bf16_close(got.double().cpu().numpy(), want, "chunk at 8k")
+
+
 def test_strided_q_view():
     """q as a view into a fused QKV projection (row stride past Hq * D) and a head-strided out."""
     Hq, Hkv, D = SHAPES["0.5B"]
@@ -140,3 +177,25 @@ def test_strided_q_view():
     ref = paged_prefill_attention(q.contiguous(), k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen))
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_workspace_shared_with_decode_in_any_order():
+    """Decode and prefill split calls of growing sizes share one workspace: the merge counters live in a region no
+    call writes partials into, so a call with more (sequence, head) pairs than the last never reads old partials
+    as counters. Prefill (16 splits, 8 units) -> decode (200 sequences, 4 splits) -> prefill (150 units) ->
+    the first prefill again, bit-identical."""
+    from cases import make_case, oracle_decode
+    from engine.hip_decode import paged_decode_attention
+
+    first = check([4096], [64], "0.5B", seed=11)
+    Hq, Hkv, D = SHAPES["0.5B"]
+    lengths = [1000] * 200
+    q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=12)
+    print("case decode 200 x 1000 splits=4 after a prefill split call", flush=True)
+    out = paged_decode_attention(q, k, v, bt, ctx, D ** -0.5, 1000, num_splits=4, work_list="off")
+    torch.cuda.synchronize()
+    ref = oracle_decode(q, k, v, tables, lengths, D ** -0.5, np.float32)
+    assert np.abs(out.double().cpu().numpy() - ref).max() <= 8e-3
+    check([3000] * 3, [400] * 3, "0.5B", seed=13)
+    again = check([4096], [64], "0.5B", seed=11)
+    assert torch.equal(first, again)
