@@ -180,13 +180,17 @@ typedef struct sipa_prefill_params {
 int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
 
 /* Key splits for a prefill call (no counterpart in the reference, whose gather path has no grid): about two
- * workgroups per CU over num_kv_heads x query_tiles units (query_tiles = sum over sequences of
- * ceil(query_len / 16)), at least 256 keys per split, at most 32 splits; cu_count <= 0 asks the current device. */
-int32_t sipa_prefill_splits(int32_t num_kv_heads, int64_t query_tiles, int32_t max_context, int32_t cu_count);
+ * workgroups per CU over the call's units, at least 256 keys per split, at most 32 splits. A unit is a KV head
+ * and 16 tt new tokens of one sequence, tt = 8 / G 16-token subtiles for a group of G = Hq / Hkv query heads
+ * (1 for G > 4); query_tiles = sum over sequences of ceil(query_len / 16). cu_count <= 0 asks the current
+ * device. */
+int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int64_t query_tiles, int32_t max_context,
+                            int32_t cu_count);
 
 /* Workspace bytes sipa_prefill needs for these sizes and num_splits (0 when one split runs). */
-int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t head_dim,
-                                     int32_t max_query_len, int32_t max_context, int32_t num_splits);
+int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t max_query_len, int32_t max_context,
+                                     int32_t num_splits);
 
 /*
  * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,

@@ -28,6 +28,9 @@ ARCH = "gfx950"
 # torch's libamdhip64 is loaded first and shares the SONAME libamdhip64.so.7 with ROCm's.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}", "-mcode-object-version=5",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA accumulators in VGPRs: the default AGPR form makes the compiler copy every accumulator between
+         # AGPRs and VGPRs around the softmax rescale of each key tile.
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas"]
 
 

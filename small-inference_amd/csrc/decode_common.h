@@ -18,6 +18,24 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes of an MFMA accumulator column) with gfx950's row-swap
+// permutes: permlane16_swap(x, x) yields the even and the odd 16-lane row of each row pair, permlane32_swap(x, x)
+// the low and the high half-wave, so each step is one permute and one VALU op, with no LDS round trip. Every lane
+// combines the same two operands in the same order, so all four lanes get the same bits.
+__device__ __forceinline__ float max_over_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float sum_over_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -302,8 +320,7 @@ __device__ __forceinline__ void mfma_epilogue(const DecodeArgs& a, int s, int h,
   constexpr int P = MfmaSmem<D>::kMergePitch;
   constexpr int J = D / 64;  // channel quads per thread
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
+  l_run = sum_over_rows(l_run);
   __syncthreads();  // every wave is done with its LDS tiles: the LDS becomes the merge buffer
   float2* ml = (float2*)smem;                       // [kWaves][16] (m, l)
   float* accs = (float*)(ml + kWaves * kMaxGroup);  // [kWaves][16][P]

@@ -35,20 +35,26 @@ struct PrefillArgs {
   const int32_t* qlen;    // [S] new tokens per sequence
   void* out;
   int64_t o_st, o_sh;
-  int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / 16)
+  int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / (16 tt))
+  int32_t tt;              // 16-token subtiles per unit: G * tt <= 8 column tiles
   int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
   int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 32)
   float scale_log2;
   int* counters;           // [units] split arrivals, zero between launches
-  float* pm;               // [units][nsplit][8 heads][16 tokens] running max (exp2 domain)
+  float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
   float* pl;               // same shape: softmax denominators
-  float* part;             // [units][nsplit][8 heads][16 tokens][D] unnormalised outputs
+  float* part;             // [units][nsplit][8 columns][16 tokens][D] unnormalised outputs
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kPrefillHeadsPerWave = 2;  // group heads per wave: G <= 2 * kWaves
-constexpr int kPrefillSlots = kPrefillHeadsPerWave * kWaves * 16;  // (head, token) rows of a unit's split state
+constexpr int kPrefillColsPerWave = 2;                              // column tiles (head, 16 tokens) per wave
+constexpr int kPrefillCols = kPrefillColsPerWave * kWaves;           // column tiles per unit: G * tt <= 8
+constexpr int kPrefillSlots = kPrefillCols * 16;                     // (column, token) rows of a split state
+
+// 16-token subtiles per unit for a GQA group of G heads: as many as fit the 8 column tiles (G = 7: 1, G = 4: 2,
+// G = 1: 8), so that every group size keeps the four waves busy.
+static inline int prefill_subtiles(int G) { return G >= 8 ? 1 : 8 / G; }
 constexpr int kPrefillMaxSplits = 32;
 
 // Merge one round of up to KB splits j0 .. of one (head, token) row: every load issued before the first is used;
@@ -96,10 +102,10 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
   constexpr int CPK = D / 8;                // 16-byte chunks per key row
   constexpr int LPT = 32 * CPK / kThreads;  // chunks per thread per K (or V) tile
+  constexpr int CW = kPrefillColsPerWave;
   static_assert(LPT * kThreads == 32 * CPK, "tile chunks must divide over the workgroup");
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
-
   __shared__ int last_flag;
 
   // Splits fastest: consecutive workgroups (which the dispatcher deals round-robin to the 8 XCDs) take the
@@ -110,14 +116,15 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const int j = u % a.qtiles;
   const int pair = u / a.qtiles;
   const int s = pair % a.S, h = pair / a.S;
+  const int G = a.G, TT = a.tt, NT = 16 * a.tt;  // query heads, token subtiles, tokens per unit
   const int n = a.qlen[s];
-  if (16 * j >= n) return;
-  const int row0 = a.qstart[s] + 16 * j;
+  if (NT * j >= n) return;
+  const int row0 = a.qstart[s] + NT * j;
   const int ctx = min(a.ctx[s], a.max_ctx);
-  const int ntok = min(min(16, n - 16 * j), a.T - row0);  // rows past T are not touched
+  const int ntok = min(min(NT, n - NT * j), a.T - row0);  // rows past T are not touched
   if (ntok <= 0 || row0 < 0) return;
-  const int P0 = ctx - n + 16 * j;                       // position of the tile's first token
-  // keys [0, kv_vis) are visible to some token of the tile; this split takes [k_lo, kv_end)
+  const int P0 = ctx - n + NT * j;  // position of the unit's first token
+  // keys [0, kv_vis) are visible to some token of the unit; this split takes [k_lo, kv_end)
   const int kv_vis = max(1, min(ctx, P0 + ntok));
   const int nvalid = (kv_vis + a.chunk - 1) / a.chunk;
   const int k_lo = sp * a.chunk;
@@ -126,34 +133,39 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const int nblk = min((kv_end - k_lo + 15) >> 4, kMaxSplitBlocks);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
-  const int G = a.G;
 
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
   for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[i], 0), a.nb - 1);
 
-  // B operands: tokens r of heads g = wave + 4 hi (zero for padding tokens and heads past the group).
-  bf16x8 qop[kPrefillHeadsPerWave][KS];
+  // Column tiles c = wave + 4 ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15 with
+  // tt = c / G (G * TT <= 8). A column tile's B operand holds token r of head g (zero past the unit's tokens).
+  int cg[CW], ctok[CW];
+  bool cvalid[CW];  // wave-uniform
+  bf16x8 qop[CW][KS];
 #pragma unroll
-  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-    const int g = wave + kWaves * hi;
-    const bool valid = g < G && r < ntok;
-    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(row0 + min(r, ntok - 1)) * a.q_st +
-                           (int64_t)(h * G + min(g, G - 1)) * a.q_sh;
+  for (int ci = 0; ci < CW; ++ci) {
+    const int c = wave + kWaves * ci;
+    cg[ci] = c % G;
+    ctok[ci] = 16 * (c / G);
+    cvalid[ci] = c / G < TT && ctok[ci] < ntok;
+    const bool valid = cvalid[ci] && ctok[ci] + r < ntok;
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(row0 + min(ctok[ci] + r, ntok - 1)) * a.q_st +
+                           (int64_t)(h * G + cg[ci]) * a.q_sh;
 #pragma unroll
     for (int jj = 0; jj < KS; ++jj) {
       u32x4 qv = *(const u32x4*)(qrow + 32 * jj + 8 * q4);
       if (!valid) qv = u32x4{0, 0, 0, 0};
-      qop[hi][jj] = __builtin_bit_cast(bf16x8, qv);
+      qop[ci][jj] = __builtin_bit_cast(bf16x8, qv);
     }
   }
-  float m_run[kPrefillHeadsPerWave], l_run[kPrefillHeadsPerWave];
-  f32x4 acc[kPrefillHeadsPerWave][DT];
+  float m_run[CW], l_run[CW];
+  f32x4 acc[CW][DT];
 #pragma unroll
-  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-    m_run[hi] = kNegInf;
-    l_run[hi] = 0.f;
+  for (int ci = 0; ci < CW; ++ci) {
+    m_run[ci] = kNegInf;
+    l_run[ci] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[hi][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) acc[ci][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();  // block ids staged
 
@@ -195,89 +207,89 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     const bool masked = t0 + 31 > P0 || t0 + 32 > kv_end;  // some key of the tile is hidden from some token
     const uint16_t* ks = sm[buf][0];
     const uint16_t* vs = sm[buf][1];
+    // The K operands of the tile serve both column tiles of the wave.
+    bf16x8 kop[2][KS];
 #pragma unroll
-    for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-      if (wave + kWaves * hi >= G) continue;  // wave-uniform
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj) kop[mt][jj] = *(const bf16x8*)(ks + (16 * mt + r) * P + 32 * jj + 8 * q4);
+    bf16x8 pop[CW];
+#pragma unroll
+    for (int ci = 0; ci < CW; ++ci) {
+      if (!cvalid[ci]) continue;  // wave-uniform
       f32x4 sc[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jj = 0; jj < KS; ++jj) {
-          const bf16x8 kop = *(const bf16x8*)(ks + (16 * mt + r) * P + 32 * jj + 8 * q4);
-          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[hi][jj], sc[mt], 0, 0, 0);
-        }
+        for (int jj = 0; jj < KS; ++jj)
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[mt][jj], qop[ci][jj], sc[mt], 0, 0, 0);
       }
       if (masked) {
+        const int tok_pos = P0 + ctok[ci] + r;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = t0 + 16 * mt + 4 * q4 + i;  // key position of accumulator row (mt, q4, i)
-            if (kp > P0 + r || kp >= kv_end) sc[mt][i] = kNegInf;
+            if (kp > tok_pos || kp >= kv_end) sc[mt][i] = kNegInf;
           }
       }
       float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                        fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      mx *= a.scale_log2;
+      mx = max_over_rows(mx) * a.scale_log2;
       // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
       // below are taken as 0 then, so that -inf - -inf never forms.
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[hi] + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run[hi], mx);
-        const float alpha = fast_exp2(m_run[hi] - (m_new == kNegInf ? 0.f : m_new));  // 0 while m_run is -inf
-        l_run[hi] *= alpha;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[ci] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[ci], mx);
+        const float alpha = fast_exp2(m_run[ci] - (m_new == kNegInf ? 0.f : m_new));  // 0 while m_run is -inf
+        l_run[ci] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[hi][dt] *= alpha;
-        m_run[hi] = m_new;
+        for (int dt = 0; dt < DT; ++dt) acc[ci][dt] *= alpha;
+        m_run[ci] = m_new;
       }
-      const float m_off = m_run[hi] == kNegInf ? 0.f : m_run[hi];
-      bf16x8 pop;
+      const float m_off = m_run[ci] == kNegInf ? 0.f : m_run[ci];
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_off));
         psum += p;
-        pop[i] = (__bf16)p;
+        pop[ci][i] = (__bf16)p;
       }
-      l_run[hi] += psum;
+      l_run[ci] += psum;
+    }
+    // V^T operands, each shared by both column tiles.
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 vop = read_v_operand<bf16x8>(vs, tr_off, P, 16 * dt);
-        acc[hi][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[hi][dt], 0, 0, 0);
-      }
+    for (int dt = 0; dt < DT; ++dt) {
+      const bf16x8 vop = read_v_operand<bf16x8>(vs, tr_off, P, 16 * dt);
+#pragma unroll
+      for (int ci = 0; ci < CW; ++ci)
+        if (cvalid[ci]) acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci], acc[ci][dt], 0, 0, 0);
     }
     if (t + 1 < ntiles) sstore(buf ^ 1);  // that buffer was last read in tile t - 1, before the last barrier
     __syncthreads();
   }
 
-  float lsum[kPrefillHeadsPerWave];  // token r's denominators, summed over the four lanes that share the token
+  float lsum[CW];  // token r's denominators, summed over the four lanes that share the token
 #pragma unroll
-  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-    float l = l_run[hi];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    lsum[hi] = l;
-  }
+  for (int ci = 0; ci < CW; ++ci) lsum[ci] = sum_over_rows(l_run[ci]);
   if (nvalid > 1) {
-    // This split's state for (head g, token r): m, l at slot 16 g + r, O at channels 16 dt + 4 q4 .. of that row.
+    // This split's state for column c, token r: m, l at slot 16 c + r, O at channels 16 dt + 4 q4 .. of that row.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kPrefillSlots;
     const int split_bytes = kPrefillSlots * D * 4;
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
         a.part + (int64_t)u * a.nsplit * kPrefillSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
 #pragma unroll
-    for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-      const int g = wave + kWaves * hi;
-      if (g >= G || r >= ntok) continue;
-      const int slot = 16 * g + r;
+    for (int ci = 0; ci < CW; ++ci) {
+      if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
+      const int slot = 16 * (wave + kWaves * ci) + r;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        __builtin_amdgcn_raw_buffer_store_b128(acc[hi][dt], rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 4,
+        __builtin_amdgcn_raw_buffer_store_b128(acc[ci][dt], rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 4,
                                                0, kAuxSc1);
       if (q4 == 0) {
-        store_coherent(a.pm + base + slot, m_run[hi]);
-        store_coherent(a.pl + base + slot, lsum[hi]);
+        store_coherent(a.pm + base + slot, m_run[ci]);
+        store_coherent(a.pl + base + slot, lsum[ci]);
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -288,14 +300,15 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     }
     __syncthreads();
     if (!last_flag) return;
-    // The last split to arrive: one thread per (head, token, channel quad) merges every split's state.
+    // The last split to arrive: one thread per (column, token, channel quad) merges every split's state.
     constexpr int Q = D / 4;
-    for (int idx = threadIdx.x; idx < G * ntok * Q; idx += kThreads) {
-      const int g = idx / (ntok * Q), rem = idx % (ntok * Q);
-      const int rr = rem / Q, c = rem % Q;
-      const int slot = 16 * g + rr;
+    for (int idx = threadIdx.x; idx < kPrefillSlots * Q; idx += kThreads) {
+      const int slot = idx / Q, cq = idx % Q;
+      const int c = slot >> 4, rr = slot & 15;
+      const int g = c % G, tok = 16 * (c / G) + rr;
+      if (c / G >= TT || tok >= ntok) continue;
       const int64_t mrow = (int64_t)u * a.nsplit * kPrefillSlots + slot;
-      const int off = (slot * D + 4 * c) * 4;
+      const int off = (slot * D + 4 * cq) * 4;
       float M = kNegInf, den = 0.f;
       f32x4 num = {0.f, 0.f, 0.f, 0.f};
       if (nvalid <= 4) {
@@ -305,30 +318,28 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
           prefill_merge_round<8>(a, rows, mrow, off, split_bytes, j0, nvalid, M, den, num);
       }
       const f32x4 o = num / den;
-      uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + rr) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
+      uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
       const uint32_t lo = f32_to_bf16_bits(o[0]) | ((uint32_t)f32_to_bf16_bits(o[1]) << 16);
       const uint32_t hi2 = f32_to_bf16_bits(o[2]) | ((uint32_t)f32_to_bf16_bits(o[3]) << 16);
-      *(u32x2*)(orow + 4 * c) = u32x2{lo, hi2};
+      *(u32x2*)(orow + 4 * cq) = u32x2{lo, hi2};
     }
     if (threadIdx.x == 0)
       __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
-  // One split: token r's output for each head is acc / l.
+  // One split: token r's output for each column tile is acc / l.
 #pragma unroll
-  for (int hi = 0; hi < kPrefillHeadsPerWave; ++hi) {
-    const int g = wave + kWaves * hi;
-    const float l = lsum[hi];
-    if (g >= G || r >= ntok) continue;
-    const float inv = 1.f / l;
-    uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + r) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
+  for (int ci = 0; ci < CW; ++ci) {
+    if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
+    const float inv = 1.f / lsum[ci];
+    uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + ctok[ci] + r) * a.o_st + (int64_t)(h * G + cg[ci]) * a.o_sh;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t lo = f32_to_bf16_bits(acc[hi][dt][0] * inv) |
-                          ((uint32_t)f32_to_bf16_bits(acc[hi][dt][1] * inv) << 16);
-      const uint32_t hi2 = f32_to_bf16_bits(acc[hi][dt][2] * inv) |
-                           ((uint32_t)f32_to_bf16_bits(acc[hi][dt][3] * inv) << 16);
+      const uint32_t lo = f32_to_bf16_bits(acc[ci][dt][0] * inv) |
+                          ((uint32_t)f32_to_bf16_bits(acc[ci][dt][1] * inv) << 16);
+      const uint32_t hi2 = f32_to_bf16_bits(acc[ci][dt][2] * inv) |
+                           ((uint32_t)f32_to_bf16_bits(acc[ci][dt][3] * inv) << 16);
       *(u32x2*)(orow + 16 * dt + 4 * q4) = u32x2{lo, hi2};
     }
   }
@@ -348,7 +359,7 @@ static int prefill_chunk(int max_context, int splits) {
   return std::max(256, (c + 31) / 32 * 32);
 }
 
-// Split count policy: about two workgroups per CU over all query tiles (units = KV heads x query tiles of
+// Split count policy: about two workgroups per CU over all units (units = KV heads x query tiles of
 // 16 tokens), no split under 256 keys, at most 32.
 static int prefill_splits_host(int64_t units, int max_context, int cu_count) {
   if (units <= 0 || max_context <= 0) return 1;
@@ -374,19 +385,24 @@ static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
   return l;
 }
 
-extern "C" int32_t sipa_prefill_splits(int32_t num_kv_heads, int64_t query_tiles, int32_t max_context,
-                                       int32_t cu_count) {
+extern "C" int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int64_t query_tiles,
+                                       int32_t max_context, int32_t cu_count) {
+  if (num_kv_heads <= 0 || num_q_heads < num_kv_heads) return 1;
   if (cu_count <= 0) cu_count = sipa_device_cu_count(-1);
-  return prefill_splits_host((int64_t)num_kv_heads * query_tiles, max_context, cu_count);
+  const int tt = prefill_subtiles(num_q_heads / num_kv_heads);
+  return prefill_splits_host((int64_t)num_kv_heads * ((query_tiles + tt - 1) / tt), max_context, cu_count);
 }
 
-extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t head_dim,
-                                                int32_t max_query_len, int32_t max_context, int32_t num_splits) {
-  if (num_seqs <= 0 || num_kv_heads <= 0 || max_query_len <= 0 || max_context <= 0) return 0;
+extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                                                int32_t head_dim, int32_t max_query_len, int32_t max_context,
+                                                int32_t num_splits) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads < num_kv_heads || max_query_len <= 0 || max_context <= 0)
+    return 0;
   const int chunk = prefill_chunk(max_context, num_splits);
   const int nsplit = (max_context + chunk - 1) / chunk;
   if (nsplit <= 1) return 0;
-  const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + 15) / 16);
+  const int nt = 16 * prefill_subtiles(num_q_heads / num_kv_heads);
+  const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + nt - 1) / nt);
   return prefill_layout(units, nsplit, head_dim).total;
 }
 
@@ -398,8 +414,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   if (S == 0 || p->max_query_len == 0) return SIPA_OK;
   SIPA_CHECK(S > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, SIPA_EINVAL, "bad sequence or head counts");
   const int G = Hq / Hkv;
-  SIPA_CHECK(G <= kPrefillHeadsPerWave * kWaves, SIPA_EUNSUPPORTED, "GQA group %d > %d", G,
-             kPrefillHeadsPerWave * kWaves);
+  SIPA_CHECK(G <= kPrefillCols, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kPrefillCols);
   SIPA_CHECK(D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {64, 128}", D);
   SIPA_CHECK(p->block_size == 16, SIPA_EUNSUPPORTED, "block_size %d != 16", p->block_size);
   SIPA_CHECK(p->max_context > 0 && p->max_context <= kMaxSplitBlocks * 16, SIPA_EUNSUPPORTED,
@@ -415,7 +430,8 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
              p->num_tokens, p->num_blocks);
   SIPA_CHECK(aligned16p(p->k_cache) && aligned16p(p->v_cache) && p->kv_stride_h % 8 == 0 &&
                  p->kv_stride_n % 8 == 0, SIPA_EINVAL, "K/V pools must be 16-byte aligned");
-  const int qtiles = (p->max_query_len + 15) / 16;
+  const int tt = prefill_subtiles(G);
+  const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
   const int64_t units = (int64_t)S * Hkv * qtiles;
   int splits = p->num_splits;
   if (splits <= 0) splits = prefill_splits_host(units, p->max_context, sipa_device_cu_count(-1));
@@ -453,6 +469,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.S = S;
   a.G = G;
   a.qtiles = qtiles;
+  a.tt = tt;
   a.T = p->num_tokens;
   a.nb = p->num_blocks;
   a.max_ctx = p->max_context;

@@ -21,10 +21,11 @@ def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size:
             head_dim in (64, 128) and group <= 8 and 0 < max_context <= 32768)
 
 
-def prefill_splits(num_kv_heads: int, query_lens: list[int], max_context: int, cu_count: int = 0) -> int:
+def prefill_splits(num_q_heads: int, num_kv_heads: int, query_lens: list[int], max_context: int,
+                   cu_count: int = 0) -> int:
     """Key splits per query tile for a call whose sequences have these new-token counts (library policy)."""
     tiles = sum(-(-n // 16) for n in query_lens)
-    return _hip.lib().sipa_prefill_splits(num_kv_heads, tiles, max_context, cu_count)
+    return _hip.lib().sipa_prefill_splits(num_q_heads, num_kv_heads, tiles, max_context, cu_count)
 
 
 def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -47,9 +48,14 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     Hkv, N, B, _ = k_cache.shape
     if out is None:
         out = torch.empty_like(q)
+    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise ValueError("the prefill kernel needs bf16 q and pools")
     for t in (block_tables, context_lens, query_starts, query_lens):
-        if t.dtype != torch.int32 or not t.is_contiguous() and t.dim() == 1:
+        if t.dtype != torch.int32:
             raise ValueError("block tables, context lengths and query rows must be int32")
+    for t in (context_lens, query_starts, query_lens):
+        if t.dim() != 1 or not t.is_contiguous() or t.numel() < S:
+            raise ValueError("context lengths and query rows must be contiguous [num_seqs] vectors")
     if q.stride(-1) != 1 or out.stride(-1) != 1 or out.shape != q.shape or out.dtype != q.dtype:
         raise ValueError("q and out must be [T, Hq, D] of one dtype with a contiguous last dim")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or block_tables.stride(-1) != 1:
@@ -63,17 +69,16 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
     p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
     p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
-    p.context_lens, p.query_starts, p.query_lens = context_lens.data_ptr(), query_starts.data_ptr(), query_lens.data_ptr()
+    p.context_lens, p.query_starts = context_lens.data_ptr(), query_starts.data_ptr()
+    p.query_lens = query_lens.data_ptr()
     p.out, p.out_stride_t, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
-    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise ValueError("the prefill kernel needs bf16 q and pools")
     lib = _hip.lib()
     if num_splits is None:
         lens = host_query_lens if host_query_lens is not None else [max_query_len] * S
-        num_splits = prefill_splits(Hkv, lens, max_context)
+        num_splits = prefill_splits(Hq, Hkv, lens, max_context)
     p.num_splits = num_splits
     stream = _hip.stream_of(q)
-    nbytes = lib.sipa_prefill_workspace_bytes(S, Hkv, D, max_query_len, max_context, num_splits)
+    nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)
     if nbytes > 0:
         ws = _workspace(q.device, stream, nbytes)
         p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()

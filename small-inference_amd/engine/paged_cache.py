@@ -209,7 +209,7 @@ class PagedKVCache:
             from .hip_prefill import prefill_splits
 
             max_ctx = max(meta.context_lens[i] for i in pf)
-            splits = prefill_splits(self.cfg.num_kv_heads, [per_seq[i] for i in pf], max_ctx)
+            splits = prefill_splits(self.cfg.num_q_heads, self.cfg.num_kv_heads, [per_seq[i] for i in pf], max_ctx)
             self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):], max_ctx, max(per_seq[i] for i in pf),
                                     splits)
             self._prefill = []

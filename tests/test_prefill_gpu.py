@@ -19,7 +19,9 @@ from oracle import paged_ref
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = {"0.5B": (14, 2, 64), "1.5B": (12, 2, 128), "g4": (32, 8, 128), "g8": (16, 2, 64), "g1": (4, 4, 64)}
+# (Hq, Hkv, D); groups of 1 .. 4 query heads put 2 .. 8 16-token subtiles in one unit
+SHAPES = {"0.5B": (14, 2, 64), "1.5B": (12, 2, 128), "g4": (32, 8, 128), "g8": (16, 2, 64), "g1": (4, 4, 64),
+          "g2": (8, 4, 64), "g3": (6, 2, 128)}
 SENTINEL = 7.0
 
 
@@ -85,7 +87,7 @@ def test_fresh_prompts(shape):
     check(lens, lens, shape)
 
 
-@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g8"])
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g8", "g4", "g3", "g2", "g1"])
 @pytest.mark.parametrize("seed", [0, 1])
 @pytest.mark.parametrize("splits", [1, 4, None], ids=["one_split", "split256", "auto"])
 def test_mid_context_chunks(shape, seed, splits):
