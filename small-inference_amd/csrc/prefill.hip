@@ -97,7 +97,9 @@ struct PrefillSmem {
   static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
 };
 
-template <int D>
+// NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
+// issued NPRE tiles before its LDS store.
+template <int D, int NPRE>
 __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
   constexpr int CPK = D / 8;                // 16-byte chunks per key row
@@ -173,36 +175,33 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
   const int ntiles = (kv_end - k_lo + 31) >> 5;
   // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
-  // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes).
-  u32x4 kreg[LPT], vreg[LPT];
-  auto gload = [&](int t) {
+  // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
+  // (temporal) loads: every query tile of the sequence reads the same keys, so L2 keeps serving them.
+  u32x4 kreg[NPRE][LPT], vreg[NPRE][LPT];
+  auto gload = [&](int set, int t) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i;
       const int rel = min(32 * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
       const int64_t off = (int64_t)bids[rel >> 4] * a.kv_sn + (rel & 15) * D + 8 * (c % CPK);
-      kreg[i] = __builtin_nontemporal_load((const u32x4*)(kh + off));
-      vreg[i] = __builtin_nontemporal_load((const u32x4*)(vh + off));
+      kreg[set][i] = *(const u32x4*)(kh + off);
+      vreg[set][i] = *(const u32x4*)(vh + off);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int set, int buf) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i;
       const int e = (c / CPK) * P + 8 * (c % CPK);
-      *(u32x4*)(&sm[buf][0][e]) = kreg[i];
-      *(u32x4*)(&sm[buf][1][e]) = vreg[i];
+      *(u32x4*)(&sm[buf][0][e]) = kreg[set][i];
+      *(u32x4*)(&sm[buf][1][e]) = vreg[set][i];
     }
   };
   const int tr_off = tr16_offset(r, q4, P);
   constexpr float kRescaleSlack = 8.f;  // p <= 2^8 against the lazily raised max (as in the decode kernel)
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
+  auto tile = [&](int t) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
     const int t0 = k_lo + 32 * t;
     const bool masked = t0 + 31 > P0 || t0 + 32 > kv_end;  // some key of the tile is hidden from some token
     const uint16_t* ks = sm[buf][0];
@@ -266,8 +265,27 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       for (int ci = 0; ci < CW; ++ci)
         if (cvalid[ci]) acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci], acc[ci][dt], 0, 0, 0);
     }
-    if (t + 1 < ntiles) sstore(buf ^ 1);  // that buffer was last read in tile t - 1, before the last barrier
-    __syncthreads();
+  };
+
+  // Register set k % NPRE carries tile k from its global loads to its LDS store; LDS is double-buffered (tile t
+  // in buffer t & 1). The set of tile t is free once tile t is in LDS, and is refilled with tile t + NPRE. The
+  // loads are issued unconditionally (past the last tile they re-read the split's last key), so that the wait
+  // before each LDS store is a fixed count that leaves the NPRE - 1 younger sets in flight.
+#pragma unroll
+  for (int k = 0; k < NPRE; ++k) gload(k, k);
+  sstore(0, 0);
+  __syncthreads();
+  for (int tb = 0; tb < ntiles; tb += NPRE) {
+#pragma unroll
+    for (int k = 0; k < NPRE; ++k) {
+      const int t = tb + k;
+      if (t >= ntiles) break;
+      gload(k, t + NPRE);
+      tile(t);
+      // buffer (t + 1) & 1 was last read in tile t - 1, before the last barrier
+      if (t + 1 < ntiles) sstore((k + 1) % NPRE, (t + 1) & 1);
+      __syncthreads();
+    }
   }
 
   float lsum[CW];  // token r's denominators, summed over the four lanes that share the token
@@ -483,9 +501,9 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
   if (D == 64)
-    hipLaunchKernelGGL(prefill_mfma_bf16<64>, dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<64, 3>), dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL(prefill_mfma_bf16<128>, dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<128, 2>), dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
   return SIPA_OK;
