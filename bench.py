@@ -454,6 +454,7 @@ def details(steps: int, warmup: int) -> dict:
         torch.cuda.empty_cache()
     out.update(store_bench(steps))
     out.update(prefill_bench(steps, warmup))
+    out["graph_decode_steps"] = graph_step_bench()
     out["stream_read_ceiling"] = stream_ceiling(steps)
     torch.cuda.empty_cache()
     for fmt in ("bf16", "int8"):
@@ -552,6 +553,65 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
     return r
 
 
+def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
+    """Decode steps of a random-init Qwen2.5-0.5B-shaped model (24 layers) at small batches, contexts ~ U[512, 2048],
+    bf16 pool: the ordinary eager step (build_metadata, ~300 launches from Python) against the same step replayed
+    from a HIP graph (engine/graph_runner.py: one metadata copy, one replay). Wall time per step, synchronised
+    each step as a serving loop is (it needs the sampled tokens), host work included."""
+    import random
+    import time
+
+    from engine.block_manager import BlockManager
+    from engine.config import QWEN2_5_0_5B as cfg
+    from engine.graph_runner import DecodeGraphRunner
+    from engine.model import Qwen2Model
+    from engine.paged_cache import PagedKVCache, build_metadata
+
+    res = {}
+    model = Qwen2Model(cfg, "cuda", torch.bfloat16, seed=seed, max_positions=4096)
+    N, B = 16384, 16
+    for batch in batches:
+        rng = random.Random(seed + batch)
+        m = BlockManager(N, B)
+        rng.shuffle(m._free)
+        cache = PagedKVCache(cfg, N, B, "cuda", torch.bfloat16, attn_backend="triton")
+        cache.k.normal_()
+        cache.v.normal_()
+        ctx = [rng.randint(512, 2048) for _ in range(batch)]
+        for s, n in enumerate(ctx):
+            m.allocate(s, n)
+        runner = DecodeGraphRunner(model, cache, m, max_batch=batch, max_context=4096, buckets=[batch])
+        seqs = list(range(batch))
+        ids = torch.zeros(batch, dtype=torch.long, device="cuda")
+        times = {}
+        for mode in ("eager", "graph"):
+            ts = []
+            for i in range(warmup + steps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for s in seqs:
+                    m.append_slot(s)
+                if mode == "eager":
+                    meta = build_metadata(m, [(s, m.seq_len(s) - 1, 1) for s in seqs], "cuda")
+                    logits = model.forward(ids, meta.positions, cache, meta)
+                else:
+                    logits = runner.step(seqs, ids)
+                ids = logits.argmax(-1)
+                torch.cuda.synchronize()
+                if i >= warmup:
+                    ts.append((time.perf_counter() - t0) * 1e3)
+            times[mode] = sorted(ts)[len(ts) // 2]
+        runner.close()
+        res[f"batch{batch}"] = {"eager_step_ms": round(times["eager"], 3), "graph_step_ms": round(times["graph"], 3),
+                                "speedup": round(times["eager"] / times["graph"], 2),
+                                "graph_tokens_per_s": round(batch / (times["graph"] * 1e-3)),
+                                "context_mean": round(sum(ctx) / batch)}
+        del cache, runner
+        torch.cuda.empty_cache()
+    log(f"[bench] graph decode steps: {json.dumps(res)}")
+    return res
+
+
 def calibrate_copy(mib: int) -> int:
     """A plain device copy of a known size, 10 launches: rocprof's per-dispatch FETCH_SIZE and WRITE_SIZE of this
     kernel against its exact byte count give the scale factor applied to the decode kernel's counters."""
@@ -587,6 +647,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
     ap.add_argument("--prefill", action="store_true", help="only run the paged prefill kernel against the "
                     "gather path")
+    ap.add_argument("--graph", action="store_true", help="only run small-batch decode steps, eager against HIP "
+                    "graph replay")
     ap.add_argument("--c5", action="store_true", help="only run config C5 (decode steps of a random-init 0.5B "
                     "model at batch 512 through the paged cache) and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -609,6 +671,9 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy)
     if args.prefill:
         print(json.dumps(prefill_bench(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.graph:
+        print(json.dumps(graph_step_bench()), flush=True)
         return 0
     if args.c5:
         res = {}

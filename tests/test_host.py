@@ -353,3 +353,15 @@ def test_metadata_matches_oracle_on_random_batches(seed):
     want = [tables[s][:-(-(start + n) // B)] for s, start, n in batch]
     assert [b.tolist() for b in meta.block_ids] == want and meta.block_ids_cpu == want
     assert meta.context_lens_t.dtype == meta.block_tables.dtype == torch.int32
+
+
+def test_graph_runner_needs_a_gpu_kernel_cache():
+    """Graph capture is for the HIP backend on a GPU pool: a CPU or gather cache is refused before any device
+    allocation."""
+    from engine.graph_runner import DecodeGraphRunner
+
+    cfg = ModelConfig(vocab_size=32, hidden_size=32, intermediate_size=32, num_layers=1, num_q_heads=2,
+                      num_kv_heads=1, head_dim=16)
+    cache = PagedKVCache(cfg, 8, 4, "cpu", torch.float32)
+    with pytest.raises(ValueError):
+        DecodeGraphRunner(None, cache, BlockManager(8, 4), max_batch=2, max_context=16)
