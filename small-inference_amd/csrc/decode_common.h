@@ -18,18 +18,30 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes of an MFMA accumulator column) with gfx950's row-swap
-// permutes: permlane16_swap(x, x) yields the even and the odd 16-lane row of each row pair, permlane32_swap(x, x)
-// the low and the high half-wave, so each step is one permute and one VALU op, with no LDS round trip. Every lane
-// combines the same two operands in the same order, so all four lanes get the same bits.
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes of an MFMA accumulator column).
 __device__ __forceinline__ float max_over_rows(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ __forceinline__ float sum_over_rows(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// The same reductions with gfx950's row-swap permutes: permlane16_swap(x, x) yields the even and the odd 16-lane
+// row of each row pair, permlane32_swap(x, x) the low and the high half-wave, so each step is one permute and one
+// VALU op with no LDS round trip; every lane combines the same two operands in the same order, so all four lanes
+// get the same bits. Measured: 3-6% faster in the prefill kernel, but the decode kernels ran slower with them
+// (the ragged split-grid case 52 -> 65 us), so only the prefill kernel uses these.
+__device__ __forceinline__ float max_over_rows_swap(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-__device__ __forceinline__ float sum_over_rows(float x) {
+__device__ __forceinline__ float sum_over_rows_swap(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -236,7 +236,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       }
       float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                        fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-      mx = max_over_rows(mx) * a.scale_log2;
+      mx = max_over_rows_swap(mx) * a.scale_log2;
       // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
       // below are taken as 0 then, so that -inf - -inf never forms.
       if (__builtin_amdgcn_ballot_w64(mx > m_run[ci] + kRescaleSlack)) {
@@ -290,7 +290,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 
   float lsum[CW];  // token r's denominators, summed over the four lanes that share the token
 #pragma unroll
-  for (int ci = 0; ci < CW; ++ci) lsum[ci] = sum_over_rows(l_run[ci]);
+  for (int ci = 0; ci < CW; ++ci) lsum[ci] = sum_over_rows_swap(l_run[ci]);
   if (nvalid > 1) {
     // This split's state for column c, token r: m, l at slot 16 c + r, O at channels 16 dt + 4 q4 .. of that row.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kPrefillSlots;
