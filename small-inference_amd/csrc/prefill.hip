@@ -160,12 +160,14 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       qop[ci][jj] = __builtin_bit_cast(bf16x8, qv);
     }
   }
-  float m_run[CW], l_run[CW];
+  // l_run: each column's softmax denominators as an MFMA accumulator (every row holds the column sum)
+  float m_run[CW];
+  f32x4 l_run[CW];
   f32x4 acc[CW][DT];
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) {
     m_run[ci] = kNegInf;
-    l_run[ci] = 0.f;
+    l_run[ci] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[ci][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -198,6 +200,8 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     }
   };
   const int tr_off = tr16_offset(r, q4, P);
+  const bf16x8 kOnes = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                        (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
   constexpr float kRescaleSlack = 8.f;  // p <= 2^8 against the lazily raised max (as in the decode kernel)
 
   auto tile = [&](int t) {
@@ -248,14 +252,11 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
         m_run[ci] = m_new;
       }
       const float m_off = m_run[ci] == kNegInf ? 0.f : m_run[ci];
-      float psum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_off));
-        psum += p;
-        pop[ci][i] = (__bf16)p;
-      }
-      l_run[ci] += psum;
+      for (int i = 0; i < 8; ++i) pop[ci][i] = (__bf16)fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_off));
+      // The denominators on the matrix cores: ones . P^T sums each token's bf16 probabilities (the values the
+      // P.V product uses) into every row of l_run, in place of eight VALU adds and a cross-row reduction.
+      l_run[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[ci], l_run[ci], 0, 0, 0);
     }
     // V^T operands, each shared by both column tiles.
 #pragma unroll
@@ -288,9 +289,9 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     }
   }
 
-  float lsum[CW];  // token r's denominators, summed over the four lanes that share the token
+  float lsum[CW];  // token r's denominators (every row of the l_run accumulator holds the same sum)
 #pragma unroll
-  for (int ci = 0; ci < CW; ++ci) lsum[ci] = sum_over_rows_swap(l_run[ci]);
+  for (int ci = 0; ci < CW; ++ci) lsum[ci] = l_run[ci][0];
   if (nvalid > 1) {
     // This split's state for column c, token r: m, l at slot 16 c + r, O at channels 16 dt + 4 q4 .. of that row.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kPrefillSlots;
