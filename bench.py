@@ -218,6 +218,41 @@ def cpu_baseline(wl, budget_s: float) -> dict:
     return r
 
 
+def cpu_path(wl, budget_s: float = 2.0) -> dict:
+    """The CPU oracle's fp32 gather-then-attend on a detail workload's layer 0 (the INT8 pools dequantized on the
+    CPU inside the timed call, as the reference's gather path dequantizes): median time and GB/s over the same
+    algorithmic bytes, beside the GPU figure."""
+    from oracle import paged_ref
+
+    B = wl.k.shape[3]
+    used = sorted({b for t, n in zip(wl.tables, wl.lengths) for b in t[:-(-n // B)]})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.int64, device="cuda")
+    kq, vq = wl.k[0].index_select(1, idx).cpu(), wl.v[0].index_select(1, idx).cpu()
+    tables = [[remap[b] for b in t[:-(-n // B)]] for t, n in zip(wl.tables, wl.lengths)]
+    bt = torch.tensor([t + [-1] * (max(map(len, tables)) - len(t)) for t in tables], dtype=torch.int64)
+    q = wl.q.cpu()
+    if wl.quant is None:
+        def run():
+            return paged_ref.decode_torch_cpu(q, kq, vq, bt, wl.lengths, wl.scale)
+    else:
+        qk = wl.quant[0]
+        ks, vs = qk.k_scale.index_select(1, idx).cpu(), qk.v_scale.index_select(1, idx).cpu()
+
+        def run():
+            k = kq.float() * (ks.float()[..., None] if qk.mode == 1 else ks.float()[:, :, None, :])
+            v = vq.float() * vs.float()[..., None]
+            return paged_ref.decode_torch_cpu(q, k, v, bt, wl.lengths, wl.scale)
+    times, t_end = [], time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"cpu_us_per_call": round(med * 1e6, 1), "cpu_gb_s": round(wl.bytes / med / 1e9, 3),
+            "cpu_threads": torch.get_num_threads(), "cpu_reps": len(times)}
+
+
 # ---- detail workloads ----------------------------------------------------------------------------------------------
 
 def int8_decode(name, fmt, lengths, N, Hq=12, Hkv=2, D=128, B=16, layers=4, seed=0, impl="auto",
@@ -435,6 +470,7 @@ def details(steps: int, warmup: int) -> dict:
     c1.scale = 1 / 8
     out["c1_1x1024"] = measure(c1, steps, warmup)
     out["c1_1x1024"]["max_abs_vs_oracle"] = round(check_against_oracle(c1), 5)
+    out["c1_1x1024"].update(cpu_path(c1))
     rng = np.random.default_rng(0)
     c3_lengths = np.clip(np.rint(rng.lognormal(math.log(600), 1.0, 256)), 16, 8192).astype(int).tolist()
     for key, wlist in (("c3_ragged256", "auto"), ("c3_ragged256_split_grid", "off")):
@@ -442,6 +478,8 @@ def details(steps: int, warmup: int) -> dict:
         out[key] = measure(c3, steps, warmup)
         out[key]["sum_context"] = int(sum(c3_lengths))
         out[key]["max_abs_vs_oracle_first32"] = round(check_against_oracle(c3), 5)
+        if wlist == "auto":
+            out[key].update(cpu_path(c3))
         del c3
         torch.cuda.empty_cache()
     torch.cuda.empty_cache()
@@ -450,6 +488,8 @@ def details(steps: int, warmup: int) -> dict:
                            ("int8-kchannel", True, "c4a_int8_kchannel_f32_head_channel_scales")):
         wl = int8_decode(key, fmt, c4_lengths, 32768, f32_channel_scales=f32s)
         out[key] = measure(wl, steps, warmup)
+        if not f32s:
+            out[key].update(cpu_path(wl))
         del wl
         torch.cuda.empty_cache()
     out.update(store_bench(steps))
