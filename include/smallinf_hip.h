@@ -207,6 +207,23 @@ int32_t sipa_build_work_list(const int32_t* context_lens_host, int32_t num_seqs,
                              int32_t capacity, int32_t* max_splits);
 
 /*
+ * Per-forward packed metadata on the device (the device-side form of reference engine/paged_cache.py:55-90,
+ * build_metadata, with the slot rule of engine/block_manager.py:118-123). tables [table_rows, table_stride] int32
+ * hold each live sequence's block table in one row (maintained by the caller); seq_info [3 S + 1] int32 is the
+ * forward's rows[S] (table row of each sequence), starts[S] (position of its first new token) and query_starts
+ * [S + 1] (cumulative new-token counts, query_starts[S] = num_tokens). Writes, for every token t,
+ * positions[t] = starts[s] + t - query_starts[s], slots[t] = table[row][p / B] * B + p % B, slot_blocks[t],
+ * slot_offsets[t]; for every sequence, context_lens[s] = starts[s] + its new tokens, last_rows[s] =
+ * query_starts[s + 1] - 1 and block_tables[s, :out_width] = its first ceil(context / B) table entries, then -1.
+ * Table indices are clamped to the table, so malformed rows read wrong entries, never outside it.
+ */
+int32_t sipa_paged_metadata(const int32_t* tables, int64_t table_stride, int32_t table_rows, int32_t table_width,
+                            const int32_t* seq_info, int32_t num_seqs, int32_t num_tokens, int32_t block_size,
+                            int32_t out_width, int64_t* positions, int64_t* slots, int64_t* slot_blocks,
+                            int64_t* slot_offsets, int64_t* last_rows, int32_t* block_tables,
+                            int32_t* context_lens, void* stream);
+
+/*
  * Per-token INT8 quantize-and-store (reference engine/triton_quant.py:24-39,61-71 and the quantizer
  * engine/quant.py:22-31): for every (t, h),
  *   s = fp16(max_d |x[t,h,d]| / 127);  q[d] = s > 0 ? clamp(rint(x[t,h,d] / float(s)), -127, 127) : 0

@@ -35,6 +35,7 @@ class BlockManager:
         # copies instead of Python list work: _arrays[seq][:len(table)] == table.
         self._arrays: dict[int, np.ndarray] = {}
         self._free_listeners: list[Callable[[list[int]], None]] = []
+        self._table_listeners: list[Callable[[int, int], None]] = []
 
     # ---- queries -------------------------------------------------------------------------------------------------
 
@@ -89,6 +90,8 @@ class BlockManager:
                 grown[:n - len(blocks)] = arr[:n - len(blocks)]
             arr = self._arrays[seq_id] = grown
         arr[n - len(blocks):n] = blocks
+        for fn in self._table_listeners:
+            fn(seq_id, n - len(blocks))
 
     def slots(self, seq_id: int, start: int, end: int) -> list[int]:
         """Slots of positions [start, end) of the sequence."""
@@ -103,6 +106,12 @@ class BlockManager:
     def add_free_listener(self, fn: Callable[[list[int]], None]) -> None:
         """Call fn(blocks) with the blocks each free() returns to the stack."""
         self._free_listeners.append(fn)
+
+    def add_table_listener(self, fn: Callable[[int, int], None]) -> None:
+        """Call fn(seq_id, first) when a sequence's table is created (first = 0) or gains blocks from index first
+        on, and fn(seq_id, -1) when the sequence is freed (no counterpart in the reference: device-side copies
+        of the tables follow these changes)."""
+        self._table_listeners.append(fn)
 
     def _pop_blocks(self, count: int) -> list[int]:
         taken = []
@@ -158,6 +167,8 @@ class BlockManager:
                 released.append(b)
         for fn in self._free_listeners:
             fn(released)
+        for fn in self._table_listeners:
+            fn(seq_id, -1)
 
     # ---- checking ------------------------------------------------------------------------------------------------
 

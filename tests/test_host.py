@@ -365,3 +365,43 @@ def test_graph_runner_needs_a_gpu_kernel_cache():
     cache = PagedKVCache(cfg, 8, 4, "cpu", torch.float32)
     with pytest.raises(ValueError):
         DecodeGraphRunner(None, cache, BlockManager(8, 4), max_batch=2, max_context=16)
+
+
+def test_device_tables_follow_the_manager():
+    """DeviceBlockTables (on a CPU tensor here) mirrors every live sequence's table in its row after sync(), through
+    allocations, appends across block boundaries, frees and row reuse; sequences allocated before it was made are
+    picked up; too many live sequences is an error."""
+    from engine.device_tables import DeviceBlockTables
+
+    rng = random.Random(5)
+    m = BlockManager(400, 4)
+    m.allocate(100, 9)
+    dt = DeviceBlockTables(m, "cpu", max_seqs=8, max_blocks=64)
+    live = {100}
+    for step in range(300):
+        op = rng.random()
+        if op < 0.25 and len(live) < 8:
+            s = rng.randrange(1000)
+            if s not in live and m.can_allocate(40):
+                m.allocate(s, rng.randrange(0, 40))
+                live.add(s)
+        elif op < 0.35 and live:
+            s = rng.choice(sorted(live))
+            m.free(s)
+            live.discard(s)
+        elif live:
+            s = rng.choice(sorted(live))
+            if m.can_append(s, 3) and m.seq_len(s) < 200:
+                m.append_slots(s, rng.randrange(1, 4))
+        if step % 7 == 0:
+            dt.sync()
+            for s in live:
+                t = m.block_table(s)
+                assert dt.table[dt.row(s), :len(t)].tolist() == t
+    assert len({dt.row(s) for s in live}) == len(live)
+    while len(live) < 8:
+        s = max(live) + 1
+        m.allocate(s, 1)
+        live.add(s)
+    with pytest.raises(RuntimeError):
+        m.allocate(max(live) + 1, 1)
