@@ -88,9 +88,7 @@ class DeviceBlockTables:
         flat, vals = [], []
         W = self.max_blocks
         for seq, first in self._dirty.items():
-            arr = self.manager.table_array(seq)
-            if arr.shape[0] > W:
-                raise ValueError(f"sequence {seq} holds {arr.shape[0]} blocks, device tables have {W} columns")
+            arr = self.manager.table_array(seq)[:W]  # a longer sequence keeps its first W blocks (build refuses it)
             if arr.shape[0] > first:
                 row = self._row_of[seq]
                 flat.append(np.arange(row * W + first, row * W + arr.shape[0], dtype=np.int64))
@@ -121,6 +119,10 @@ class DeviceBlockTables:
             if held[i] < ctx[i]:
                 raise ValueError(f"sequence {seqs[i]} holds {held[i]} tokens, forward needs {ctx[i]}")
             raise ValueError(f"sequence {seqs[i]}: negative start {starts[i]}")
+        if int(ctx.max()) > self.max_blocks * B:
+            i = int(np.argmax(ctx))
+            raise ValueError(f"sequence {seqs[i]}: context {ctx[i]} exceeds the device tables' "
+                             f"{self.max_blocks * B} tokens")
         self.sync()
         rows = np.fromiter((self._row_of[s] for s in seqs), dtype=np.int64, count=S)
         qs = np.zeros(S + 1, dtype=np.int64)

@@ -1,14 +1,15 @@
 """Decode steps replayed from HIP graphs: the whole forward of a batch of one-token rows (embedding, every layer's
-GEMMs, the HIP store and paged-decode launches, the LM head) captured once per batch-size bucket and replayed with
-one host-to-device copy of the step's metadata.
+GEMMs, the HIP store and paged-decode launches, the LM head) captured once per batch-size bucket and replayed after
+one small upload and one metadata launch.
 
 The reference launches every kernel of a decode step from Python (about 800 launches per step for Qwen2.5-0.5B,
 reference README.md:144,172 and docs/implementation-plan.md:126), so small-batch steps are bound by launch
 overhead. Capture needs every launch to be shape-static and every pointer fixed: the metadata lives in persistent
-device buffers (one int64 and one int32 buffer, refilled by one copy each from pinned host memory), the decode
-launches run on the split grid sized for the runner's max_context (a sequence's splits past its own context exit
-at once; no per-step work list), and rows past the live batch are padding that writes to and reads from a
-scratch block the runner reserves from the block manager.
+device buffers, derived before each replay from the device block tables by one sipa_paged_metadata launch (the
+host uploads only the step's (table row, position) pairs); the decode launches run on the split grid sized for
+the runner's max_context (a sequence's splits past its own context exit at once; no per-step work list); and
+rows past the live batch are padding that writes to and reads from a scratch block the runner reserves from the
+block manager.
 
 The cache keeps its begin / write / attend interface: the runner hands it PagedMetadata whose device fields are
 views of the persistent buffers and whose host context lengths are max_context for every row, which is what fixes
@@ -18,10 +19,14 @@ the decode grid. Pools of the model dtype and INT8 format "int8" (per-token scal
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
+from . import _hip
 from .block_manager import BlockManager
+from .device_tables import DeviceBlockTables
 from .paged_cache import PagedKVCache, PagedMetadata, PerSequence
 
 SCRATCH_SEQ = -(1 << 40)  # the runner's own sequence id in the block manager: the padding rows' block
@@ -33,10 +38,13 @@ def _not_kept(i: int):
 
 class DecodeGraphRunner:
     """Replays captured decode steps of `model` through `cache` for batches of up to max_batch sequences whose
-    contexts stay within max_context tokens."""
+    contexts stay within max_context tokens. The block tables live on the device (`device_tables`, made here for
+    up to max_seqs live sequences when not given), and each step's metadata is derived there by one
+    sipa_paged_metadata launch into the graph's persistent buffers."""
 
     def __init__(self, model, cache: PagedKVCache, manager: BlockManager, max_batch: int, max_context: int,
-                 buckets: list[int] | None = None):
+                 buckets: list[int] | None = None, device_tables: DeviceBlockTables | None = None,
+                 max_seqs: int | None = None):
         if not cache.on_gpu or cache.attn_backend not in ("hip", "triton"):
             raise ValueError("graph capture needs a GPU cache on the HIP backend")
         if getattr(cache, "fmt", "int8") != "int8":
@@ -51,22 +59,27 @@ class DecodeGraphRunner:
                                           if b < max_batch] + [max_batch])
         if self.buckets[-1] < max_batch or self.buckets[0] < 1:
             raise ValueError("buckets must cover 1 .. max_batch")
-        manager.allocate(SCRATCH_SEQ, 1)
-        self.scratch_block = int(manager.table_array(SCRATCH_SEQ)[0])
         dev = cache.device
+        if device_tables is None:
+            device_tables = DeviceBlockTables(manager, dev, max_seqs or 4 * max_batch + 1, self.width)
+        if device_tables.max_blocks < self.width:
+            raise ValueError(f"device tables of {device_tables.max_blocks} blocks cannot hold {max_context} tokens")
+        self.tables = device_tables
+        manager.allocate(SCRATCH_SEQ, 1)
         n = max_batch
-        # int64: ids, positions, slots, slot blocks, slot offsets, last-token rows; int32: tables, context lengths
-        self._h64 = torch.empty(6 * n, dtype=torch.int64, pin_memory=True)
-        self._h32 = torch.empty(n * self.width + n, dtype=torch.int32, pin_memory=True)
-        self._n64, self._n32 = self._h64.numpy(), self._h32.numpy()  # numpy views of the pinned buffers
-        self._d64 = torch.empty(6 * n, dtype=torch.int64, device=dev)
+        # persistent step buffers. int64: ids, positions, slots, slot blocks, slot offsets, last-token rows;
+        # int32: block tables [n, width], context lengths
+        self._d64 = torch.zeros(6 * n, dtype=torch.int64, device=dev)
         self._d32 = torch.empty(n * self.width + n, dtype=torch.int32, device=dev)
+        # the step's (row, start, query start) triples, uploaded in one copy from pinned memory
+        self._hinfo = torch.empty(3 * n + 1, dtype=torch.int32, pin_memory=True)
+        self._ninfo = self._hinfo.numpy()
+        self._dinfo = torch.empty(3 * n + 1, dtype=torch.int32, device=dev)
         self._copied = torch.cuda.Event()
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._pool = None
         self._stream = torch.cuda.Stream(device=dev)  # capture stream (default priority)
-        self._fill_padding(0)
-        self._upload()
+        self._prepare([], max_batch)
 
     # ---- persistent metadata ------------------------------------------------------------------------------------
 
@@ -85,50 +98,33 @@ class DecodeGraphRunner:
             positions=pos, slots_cpu=[], slot_mapping=slots, slot_blocks=blocks, slot_offsets=offs,
             block_ids=no_rows, block_ids_cpu=no_rows, block_tables=bt, context_lens_t=ctx, last_token_indices=last)
 
-    def _fill_padding(self, first: int) -> None:
-        """Rows first .. max_batch - 1: token 0 at position 0 in slot 0 of the scratch block, one key of context."""
-        n, w, h64, h32 = self.max_batch, self.width, self._n64, self._n32
-        h64[first:n] = 0
-        h64[n + first:2 * n] = 0
-        h64[2 * n + first:3 * n] = self.scratch_block * self.B
-        h64[3 * n + first:4 * n] = self.scratch_block
-        h64[4 * n + first:5 * n] = 0
-        h64[5 * n + first:6 * n] = np.arange(first, n)
-        bt = h32[:n * w].reshape(n, w)
-        bt[first:] = -1
-        bt[first:, 0] = self.scratch_block
-        h32[n * w + first:n * w + n] = 1
-
-    def _upload(self) -> None:
-        self._d64.copy_(self._h64, non_blocking=True)
-        self._d32.copy_(self._h32, non_blocking=True)
+    def _prepare(self, seq_ids: list[int], bucket: int) -> None:
+        """Write the metadata of a step over seq_ids (each sequence's newest token, its slot already appended, at
+        position len - 1) padded to `bucket` rows into the persistent buffers: rows past the batch read and write
+        position 0 of the runner's scratch sequence."""
+        b = len(seq_ids)
+        m = self.manager
+        lens = np.fromiter((m.seq_len(s) for s in seq_ids), dtype=np.int64, count=b)
+        bad = np.flatnonzero((lens < 1) | (lens > self.max_context))
+        if bad.size:
+            i = int(bad[0])
+            raise ValueError(f"sequence {seq_ids[i]}: context {lens[i]} outside 1 .. {self.max_context}")
+        self._copied.synchronize()  # the previous step's copy has left the pinned buffer
+        info = self._ninfo
+        info[:b] = np.fromiter((self.tables.row(s) for s in seq_ids), dtype=np.int64, count=b)
+        info[b:bucket] = self.tables.row(SCRATCH_SEQ)
+        info[bucket:bucket + b] = lens - 1
+        info[bucket + b:2 * bucket] = 0
+        info[2 * bucket:3 * bucket + 1] = np.arange(bucket + 1)
+        self._dinfo[:3 * bucket + 1].copy_(self._hinfo[:3 * bucket + 1], non_blocking=True)
         self._copied.record()
-
-    def _fill(self, seq_ids: list[int]) -> None:
-        """This step's rows: each sequence's newest token (its slot already appended) at position len - 1."""
-        self._copied.synchronize()  # the previous step's copy has left the pinned buffers
-        n, w, B, b = self.max_batch, self.width, self.B, len(seq_ids)
-        h64, h32 = self._n64, self._n32
-        bt = h32[:n * w].reshape(n, w)
-        lens = np.empty(b, dtype=np.int64)
-        blocks = np.empty(b, dtype=np.int64)
-        for i, s in enumerate(seq_ids):
-            ctx = self.manager.seq_len(s)
-            if not 1 <= ctx <= self.max_context:
-                raise ValueError(f"sequence {s}: context {ctx} outside 1 .. {self.max_context}")
-            table = self.manager.table_array(s)
-            nb = -(-ctx // B)
-            bt[i, :nb] = table[:nb]
-            bt[i, nb:] = -1
-            lens[i] = ctx
-            blocks[i] = table[(ctx - 1) // B]
-        p = lens - 1
-        h64[n:n + b] = p
-        h64[2 * n:2 * n + b] = blocks * B + p % B
-        h64[3 * n:3 * n + b] = blocks
-        h64[4 * n:4 * n + b] = p % B
-        h64[5 * n:5 * n + b] = np.arange(b)
-        h32[n * w:n * w + b] = lens
+        self.tables.sync()
+        ids, pos, slots, blocks, offs, last, bt, ctx = self._views(bucket)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        _hip.check(_hip.lib().sipa_paged_metadata(
+            p(self.tables.table), self.tables.table.stride(0), self.tables.max_seqs, self.tables.max_blocks,
+            p(self._dinfo), bucket, bucket, self.B, self.width, p(pos), p(slots), p(blocks), p(offs), p(last),
+            p(bt), p(ctx), _hip.stream_of(self._d64)), "graph runner metadata")
 
     # ---- capture and replay -------------------------------------------------------------------------------------
 
@@ -148,9 +144,7 @@ class DecodeGraphRunner:
         block when the persistent buffers hold padding."""
         if bucket in self._graphs:
             return
-        self._copied.synchronize()
-        self._fill_padding(0)
-        self._upload()
+        self._prepare([], bucket)
         s = self._stream
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -174,9 +168,7 @@ class DecodeGraphRunner:
         bucket = self._bucket(b)
         if graph and bucket not in self._graphs:
             self.capture(bucket)
-        self._fill(seq_ids)
-        self._fill_padding(b)
-        self._upload()
+        self._prepare(seq_ids, bucket)
         # the token ids go device to device (the previous step's argmax need not visit the host)
         self._d64[:b].copy_(input_ids.to(self._d64.device, torch.int64), non_blocking=True)
         if not graph:
