@@ -374,12 +374,21 @@ def prefill_bench(steps: int, warmup: int) -> dict:
     from engine.attention import attention
     from engine.hip_prefill import paged_prefill_attention
 
+    from engine.hip_decode import QuantKV
+    from engine.quant import quantize_per_token
+
     Hq, Hkv, D, B, N = 14, 2, 64, 16, 32768
     res = {}
-    for name, ctx, qlen in (("prefill_4x2048_fresh", [2048] * 4, [2048] * 4), ("prefill_512_at_8k", [8192], [512])):
+    for name, ctx, qlen, int8 in (("prefill_4x2048_fresh", [2048] * 4, [2048] * 4, False),
+                                  ("prefill_512_at_8k", [8192], [512], False),
+                                  ("prefill_512_at_8k_int8", [8192], [512], True)):
         g = torch.Generator(device="cuda").manual_seed(3)
         k = torch.randn(Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
         v = torch.randn(Hkv, N, B, D, device="cuda", dtype=torch.bfloat16, generator=g)
+        quant = None
+        if int8:  # per-token INT8 pools (format "int8"); the gather path dequantizes them to bf16 per call
+            (kq, ks), (vq, vs) = quantize_per_token(k), quantize_per_token(v)
+            quant = QuantKV(1, ks, vs)
         T = sum(qlen)
         q = torch.randn(T, Hq, D, device="cuda", dtype=torch.bfloat16, generator=g)
         tables = lifo_tables(N, ctx, B, 3)
@@ -391,7 +400,10 @@ def prefill_bench(steps: int, warmup: int) -> dict:
         scale = D ** -0.5
 
         def kern(i):
-            paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out)
+            if quant is None:
+                paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), out=out)
+            else:
+                paged_prefill_attention(q, kq, vq, bt, c, st, ln, scale, max(ctx), max(qlen), out=out, quant=quant)
 
         blocks = [torch.tensor(t[:-(-n // B)], device="cuda") for t, n in zip(tables, ctx)]
         kpos = torch.arange(max(ctx), device="cuda")
@@ -399,8 +411,13 @@ def prefill_bench(steps: int, warmup: int) -> dict:
         def gather_path(i):
             outs = []
             for s in range(len(ctx)):
-                kk = k[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
-                vv = v[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
+                if quant is None:
+                    kk = k[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
+                    vv = v[:, blocks[s]].view(Hkv, -1, D)[:, :ctx[s]]
+                else:  # engine/quant_cache.py gather(): dequantize the sequence's blocks to the model dtype
+                    kk = (kq[:, blocks[s]].float() * ks[:, blocks[s]].float()[..., None]).bfloat16()
+                    vv = (vq[:, blocks[s]].float() * vs[:, blocks[s]].float()[..., None]).bfloat16()
+                    kk, vv = kk.view(Hkv, -1, D)[:, :ctx[s]], vv.view(Hkv, -1, D)[:, :ctx[s]]
                 qpos = torch.arange(ctx[s] - qlen[s], ctx[s], device="cuda")
                 outs.append(attention(q[starts[s]:starts[s] + qlen[s]], kk, vv, qpos, kpos[:ctx[s]], scale))
             return torch.cat(outs)
@@ -414,7 +431,8 @@ def prefill_bench(steps: int, warmup: int) -> dict:
                      "tflop_s": round(flops / (ms * 1e-3) / 1e12, 1),
                      "frac_of_bf16_mfma_peak": round(flops / (ms * 1e-3) / 2.5e15, 4),
                      "gather_path_us": round(gms * 1e3, 1), "speedup_vs_gather": round(gms / ms, 2),
-                     "max_abs_vs_gather_path": round(diff, 5), "tokens": T, "context": ctx}
+                     "max_abs_vs_gather_path": round(diff, 5), "tokens": T, "context": ctx,
+                     "pool": "int8 per-token" if int8 else "bf16"}
         del k, v
         torch.cuda.empty_cache()
     log(f"[bench] prefill: {json.dumps(res)}")

@@ -146,8 +146,8 @@ int32_t sipa_decode(const sipa_decode_params* p, void* stream);
  * sequence s, rows query_starts[s] .. query_starts[s] + query_lens[s] - 1 of q are its new tokens at positions
  * context_lens[s] - query_lens[s] .. context_lens[s] - 1 (their K/V already written to the pool); each attends
  * causally to positions 0 .. its own, query head g to KV head g / (Hq / Hkv), softmax in fp32 with the
- * probabilities rounded to bf16 for P.V, written to the same rows of out. bf16 q, pool and out; 16-token blocks;
- * head_dim 64 or 128; group Hq / Hkv <= 8; max_context <= 32768. Context lengths are clamped to max_context and
+ * probabilities rounded to bf16 for P.V, written to the same rows of out. bf16 q and out, bf16 or INT8 pools;
+ * 16-token blocks; head_dim 64 or 128; group Hq / Hkv <= 8; max_context <= 32768. Context lengths are clamped to max_context and
  * block ids to [0, num_blocks); q and out rows must be 16-byte aligned.
  */
 typedef struct sipa_prefill_params {
@@ -169,6 +169,19 @@ typedef struct sipa_prefill_params {
   const int32_t* query_lens;   /* [S] new tokens of each sequence (>= 1) */
   void* out;                   /* [T, Hq, D] bf16 */
   int64_t out_stride_t, out_stride_h;
+  /* SIPA_KV_PLAIN: bf16 pools. SIPA_KV_INT8_TOKEN / SIPA_KV_INT8_KCHAN: int8 pools with scales and (format B)
+     staging laid out as in sipa_decode_params; K/V are dequantized as the reference's gather path does,
+     q * s in fp32 rounded to bf16, with format B's keys past the last full block taken from the staging slot. */
+  int32_t kv_mode;
+  const void* k_scale;
+  int32_t k_scale_dtype;
+  int64_t ks_stride_h, ks_stride_n;
+  const void* v_scale;
+  int32_t v_scale_dtype;
+  int64_t vs_stride_h, vs_stride_n;
+  const void* stage;
+  int64_t st_stride_h, st_stride_n, st_stride_b;
+  const int32_t* tail_slots;   /* [S] staging slot of each sequence's partial last block, -1 if none */
   /* Key splits per 16-token query tile (<= 0: sipa_prefill_splits with units = S x Hkv x query tiles) and the
      workspace they need when more than one split runs: sipa_prefill_workspace_bytes() bytes, laid out and reused
      as sipa_decode_params.workspace (the same buffer may serve both); at most 65536 KV heads x query tiles. */

@@ -39,6 +39,14 @@ struct PrefillArgs {
   int32_t tt;              // 16-token subtiles per unit: G * tt <= 8 column tiles
   int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
   int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 32)
+  // INT8 pools (kernel MODE 1, 2): scales and format B's staging, as in sipa_prefill_params
+  const void* ks;
+  const void* vs;
+  bool ks_f32, vs_f32;
+  int64_t ks_sh, ks_sn, vs_sh, vs_sn;
+  const uint16_t* stage;
+  int64_t st_sh, st_sn, st_sb;
+  const int32_t* tails;
   float scale_log2;
   int* counters;           // [units] split arrivals, zero between launches
   float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
@@ -97,9 +105,55 @@ struct PrefillSmem {
   static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
 };
 
+// A cooperative-load chunk (8 channels of one key) as it arrives from memory, per pool format: MODE 0 bf16 K/V;
+// MODE 1 int8 codes with per-token K and V scales; MODE 2 int8 codes with the block's 8 K channel scales, the
+// token's V scale, and the bf16 staged K of the sequence's partial last block (used when `staged`). Scales are
+// kept as raw fp16 or fp32 bits until the LDS store, so that their loads are waited for only there.
+template <int MODE>
+struct KvRaw;
+template <>
+struct KvRaw<0> {
+  u32x4 k, v;
+};
+template <>
+struct KvRaw<1> {
+  u32x2 k, v;
+  uint32_t ks, vs;
+};
+template <>
+struct KvRaw<2> {
+  u32x2 k, v;
+  uint32_t ks[8], vs;
+  u32x4 st;
+  bool staged;
+};
+
+__device__ __forceinline__ uint32_t scale_bits(const void* base, bool f32, int64_t i) {
+  return f32 ? ((const uint32_t*)base)[i] : (uint32_t)((const uint16_t*)base)[i];
+}
+
+__device__ __forceinline__ float scale_value(uint32_t bits, bool f32) {
+  return f32 ? __uint_as_float(bits) : f16_bits_to_f32(bits);
+}
+
+// 8 int8 codes -> 8 bf16 of code * scale(j), computed in fp32 and rounded to nearest even (the reference's
+// dequantize(q, s, bf16): (q.float() * s.float()).to(bfloat16)).
+template <typename Scale>
+__device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
+  u32x4 out;
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const uint32_t w = codes[j >> 2];
+    const float a0 = (float)(int8_t)(w >> (8 * (j & 3))) * scale(j);
+    const float a1 = (float)(int8_t)(w >> (8 * ((j + 1) & 3))) * scale(j + 1);
+    out[j >> 1] = f32_to_bf16_bits(a0) | ((uint32_t)f32_to_bf16_bits(a1) << 16);
+  }
+  return out;
+}
+
 // NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
 // issued NPRE tiles before its LDS store.
-template <int D, int NPRE>
+template <int D, int NPRE, int MODE>
 __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
   constexpr int CPK = D / 8;                // 16-byte chunks per key row
@@ -173,21 +227,46 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   }
   __syncthreads();  // block ids staged
 
-  const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
-  const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
   const int ntiles = (kv_end - k_lo + 31) >> 5;
   // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
   // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
   // (temporal) loads: every query tile of the sequence reads the same keys, so L2 keeps serving them.
-  u32x4 kreg[NPRE][LPT], vreg[NPRE][LPT];
+  // INT8 pools: the chunk's 8 codes of K and of V with their scales; the LDS store dequantizes them to bf16,
+  // q * s in fp32 rounded to bf16, the values the reference's gather path attends over. Format B's keys at or
+  // past the sequence's last full block come from its bf16 staging slot instead.
+  const int nq = MODE == 2 ? ctx / 16 * 16 : 0;
+  const int tail = MODE == 2 ? a.tails[s] : -1;
+  KvRaw<MODE> raw[NPRE][LPT];
   auto gload = [&](int set, int t) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int c = threadIdx.x + kThreads * i;
+      const int c = threadIdx.x + kThreads * i, cg = c % CPK;
       const int rel = min(32 * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
-      const int64_t off = (int64_t)bids[rel >> 4] * a.kv_sn + (rel & 15) * D + 8 * (c % CPK);
-      kreg[set][i] = *(const u32x4*)(kh + off);
-      vreg[set][i] = *(const u32x4*)(vh + off);
+      const int64_t blk = bids[rel >> 4];
+      const int off = rel & 15;
+      KvRaw<MODE>& x = raw[set][i];
+      if constexpr (MODE == 0) {
+        const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + 8 * cg;
+        x.k = *(const u32x4*)((const uint16_t*)a.k + e);
+        x.v = *(const u32x4*)((const uint16_t*)a.v + e);
+      } else {
+        const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + 8 * cg;
+        x.k = *(const u32x2*)((const int8_t*)a.k + e);
+        x.v = *(const u32x2*)((const int8_t*)a.v + e);
+        x.vs = scale_bits(a.vs, a.vs_f32, (int64_t)h * a.vs_sh + blk * a.vs_sn + off);
+        if constexpr (MODE == 1) {
+          x.ks = scale_bits(a.ks, a.ks_f32, (int64_t)h * a.ks_sh + blk * a.ks_sn + off);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            x.ks[j] = scale_bits(a.ks, a.ks_f32, (int64_t)h * a.ks_sh + blk * a.ks_sn + 8 * cg + j);
+          const int pos = k_lo + rel;
+          x.staged = tail >= 0 && pos >= nq;
+          if (x.staged)
+            x.st = *(const u32x4*)(a.stage + (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn +
+                                   (int64_t)(pos & 15) * a.st_sb + 8 * cg);
+        }
+      }
     }
   };
   auto sstore = [&](int set, int buf) {
@@ -195,8 +274,21 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i;
       const int e = (c / CPK) * P + 8 * (c % CPK);
-      *(u32x4*)(&sm[buf][0][e]) = kreg[set][i];
-      *(u32x4*)(&sm[buf][1][e]) = vreg[set][i];
+      const KvRaw<MODE>& x = raw[set][i];
+      if constexpr (MODE == 0) {
+        *(u32x4*)(&sm[buf][0][e]) = x.k;
+        *(u32x4*)(&sm[buf][1][e]) = x.v;
+      } else {
+        const float vsf = scale_value(x.vs, a.vs_f32);
+        *(u32x4*)(&sm[buf][1][e]) = dequant8(x.v, [&](int) { return vsf; });
+        if constexpr (MODE == 1) {
+          const float ksf = scale_value(x.ks, a.ks_f32);
+          *(u32x4*)(&sm[buf][0][e]) = dequant8(x.k, [&](int) { return ksf; });
+        } else {
+          *(u32x4*)(&sm[buf][0][e]) =
+              x.staged ? x.st : dequant8(x.k, [&](int j) { return scale_value(x.ks[j], a.ks_f32); });
+        }
+      }
     }
   };
   const int tr_off = tr16_offset(r, q4, P);
@@ -447,8 +539,24 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
              "out rows must be 16-byte aligned");
   SIPA_CHECK(p->num_tokens > 0 && p->num_blocks > 0, SIPA_EINVAL, "num_tokens %d, num_blocks %d",
              p->num_tokens, p->num_blocks);
+  const int mode = p->kv_mode;
+  SIPA_CHECK(mode == SIPA_KV_PLAIN || mode == SIPA_KV_INT8_TOKEN || mode == SIPA_KV_INT8_KCHAN, SIPA_EINVAL,
+             "kv_mode %d", mode);
   SIPA_CHECK(aligned16p(p->k_cache) && aligned16p(p->v_cache) && p->kv_stride_h % 8 == 0 &&
                  p->kv_stride_n % 8 == 0, SIPA_EINVAL, "K/V pools must be 16-byte aligned");
+  if (mode != SIPA_KV_PLAIN) {
+    SIPA_CHECK(p->k_scale && p->v_scale, SIPA_EINVAL, "INT8 pools need k_scale and v_scale");
+    SIPA_CHECK((p->k_scale_dtype == SIPA_F16 || p->k_scale_dtype == SIPA_F32) &&
+                   (p->v_scale_dtype == SIPA_F16 || p->v_scale_dtype == SIPA_F32),
+               SIPA_EUNSUPPORTED, "scales must be fp16 or fp32");
+    const int ksz = p->k_scale_dtype == SIPA_F32 ? 4 : 2, vsz = p->v_scale_dtype == SIPA_F32 ? 4 : 2;
+    SIPA_CHECK(((uintptr_t)p->k_scale % ksz) == 0 && ((uintptr_t)p->v_scale % vsz) == 0, SIPA_EINVAL,
+               "scales must be aligned to their element size");
+    if (mode == SIPA_KV_INT8_KCHAN)
+      SIPA_CHECK(p->stage && p->tail_slots && aligned16p(p->stage) && p->st_stride_h % 8 == 0 &&
+                     p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
+                 SIPA_EINVAL, "format B needs a 16-byte aligned bf16 staging pool and tail slots");
+  }
   const int tt = prefill_subtiles(G);
   const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
   const int64_t units = (int64_t)S * Hkv * qtiles;
@@ -495,16 +603,35 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.scale_log2 = p->scale * 1.4426950408889634f;
   a.nsplit = nsplit;
   a.chunk = chunk;
+  a.ks = p->k_scale;
+  a.vs = p->v_scale;
+  a.ks_f32 = p->k_scale_dtype == SIPA_F32;
+  a.vs_f32 = p->v_scale_dtype == SIPA_F32;
+  a.ks_sh = p->ks_stride_h;
+  a.ks_sn = p->ks_stride_n;
+  a.vs_sh = p->vs_stride_h;
+  a.vs_sn = p->vs_stride_n;
+  a.stage = (const uint16_t*)p->stage;
+  a.st_sh = p->st_stride_h;
+  a.st_sn = p->st_stride_n;
+  a.st_sb = p->st_stride_b;
+  a.tails = p->tail_slots;
   char* ws = (char*)p->workspace;
   a.counters = nsplit > 1 ? (int*)(ws + lay.counters) : nullptr;
   a.pm = nsplit > 1 ? (float*)(ws + lay.pm) : nullptr;
   a.pl = nsplit > 1 ? (float*)(ws + lay.pl) : nullptr;
   a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
-  if (D == 64)
-    hipLaunchKernelGGL((prefill_mfma_bf16<64, 3>), dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((prefill_mfma_bf16<128, 2>), dim3((unsigned)wgs), dim3(kThreads), 0, st, a);
+  const dim3 grid((unsigned)wgs), block(kThreads);
+  if (D == 64) {
+    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 0>), grid, block, 0, st, a);
+    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 1>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 2>), grid, block, 0, st, a);
+  } else {
+    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 0>), grid, block, 0, st, a);
+    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 1>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 1, 2>), grid, block, 0, st, a);  // registers: one tile ahead
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
   return SIPA_OK;

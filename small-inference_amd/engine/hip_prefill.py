@@ -15,10 +15,18 @@ from .hip_decode import _workspace  # one split workspace per (device, stream) s
 
 def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
                       max_context: int) -> bool:
-    """Whether the prefill kernel covers this shape (bf16 q and pool, 16-token blocks, head_dim 64/128, GQA group
-    <= 8, contexts <= 32768); callers use the gather path otherwise."""
-    return (q_dtype == torch.bfloat16 and pool_dtype == torch.bfloat16 and block_size == 16 and
+    """Whether the prefill kernel covers this shape (bf16 q; bf16 or int8 pool; 16-token blocks, head_dim 64/128,
+    GQA group <= 8, contexts <= 32768); callers use the gather path otherwise."""
+    return (q_dtype == torch.bfloat16 and pool_dtype in (torch.bfloat16, torch.int8) and block_size == 16 and
             head_dim in (64, 128) and group <= 8 and 0 < max_context <= 32768)
+
+
+def _scale_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float16:
+        return _hip.F16
+    if t.dtype == torch.float32:
+        return _hip.F32
+    raise ValueError(f"scales must be fp16 or fp32, got {t.dtype}")
 
 
 def prefill_splits(num_q_heads: int, num_kv_heads: int, query_lens: list[int], max_context: int,
@@ -32,7 +40,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                             context_lens: torch.Tensor, query_starts: torch.Tensor, query_lens: torch.Tensor,
                             scale: float, max_context: int, max_query_len: int,
                             out: torch.Tensor | None = None, *, num_splits: int | None = None,
-                            host_query_lens: list[int] | None = None) -> torch.Tensor:
+                            host_query_lens: list[int] | None = None, quant=None) -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16, one layer
@@ -42,14 +50,18 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     max_query_len are the host-known maxima. Writes those rows of out ([T, Hq, D], q's dtype; other rows are left
     as they are) and returns out. Each 16-token query tile's keys are cut into num_splits splits (default: the
     library's policy over host_query_lens when given, else over S x ceil(max_query_len / 16) tiles).
+    INT8 pools take quant (engine.hip_decode.QuantKV: mode 1 per-token scales, mode 2 per-channel K scales with
+    format B's staging and tail slots, which must then cover these S sequences); K/V are dequantized as the
+    reference's gather path does, q * s in fp32 rounded to bf16.
     """
     S = block_tables.shape[0]
     T, Hq, D = q.shape
     Hkv, N, B, _ = k_cache.shape
     if out is None:
         out = torch.empty_like(q)
-    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise ValueError("the prefill kernel needs bf16 q and pools")
+    pool_dtype = torch.int8 if quant is not None else torch.bfloat16
+    if q.dtype != torch.bfloat16 or k_cache.dtype != pool_dtype or v_cache.dtype != pool_dtype:
+        raise ValueError("the prefill kernel needs bf16 q and bf16 pools, or int8 pools with quant")
     for t in (block_tables, context_lens, query_starts, query_lens):
         if t.dtype != torch.int32:
             raise ValueError("block tables, context lengths and query rows must be int32")
@@ -72,6 +84,21 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     p.context_lens, p.query_starts = context_lens.data_ptr(), query_starts.data_ptr()
     p.query_lens = query_lens.data_ptr()
     p.out, p.out_stride_t, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    if quant is not None:
+        if quant.mode not in (1, 2):
+            raise ValueError(f"QuantKV mode {quant.mode}")
+        p.kv_mode = quant.mode
+        ks, vs = quant.k_scale, quant.v_scale
+        p.k_scale, p.k_scale_dtype, p.ks_stride_h, p.ks_stride_n = ks.data_ptr(), _scale_dtype(ks), *ks.stride()[:2]
+        p.v_scale, p.v_scale_dtype, p.vs_stride_h, p.vs_stride_n = vs.data_ptr(), _scale_dtype(vs), *vs.stride()[:2]
+        if quant.mode == 2:
+            st, tails = quant.stage, quant.tail_slots
+            if st is None or tails is None or st.dtype != torch.bfloat16 or tails.dtype != torch.int32:
+                raise ValueError("format B needs bf16 staging and int32 tail slots")
+            if tails.numel() < S or not tails.is_contiguous():
+                raise ValueError("tail slots must be a contiguous vector covering every sequence")
+            p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = st.data_ptr(), *st.stride()[:3]
+            p.tail_slots = tails.data_ptr()
     lib = _hip.lib()
     if num_splits is None:
         lens = host_query_lens if host_query_lens is not None else [max_query_len] * S

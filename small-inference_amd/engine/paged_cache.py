@@ -212,6 +212,7 @@ class PagedKVCache:
             splits = prefill_splits(self.cfg.num_q_heads, self.cfg.num_kv_heads, [per_seq[i] for i in pf], max_ctx)
             self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):], max_ctx, max(per_seq[i] for i in pf),
                                     splits)
+            self._prefill_seqs = pf
             self._prefill = []
         if dec:
             # Once per forward, shared by every layer: the decode rows and their slice of the metadata.
@@ -274,7 +275,11 @@ class PagedKVCache:
 
         bt, ctx, qs, ql, max_ctx, max_q, splits = self._prefill_launch
         paged_prefill_attention(q, self.k[layer], self.v[layer], bt, ctx, qs, ql, scale, max_ctx, max_q, out=out,
-                                num_splits=splits)
+                                num_splits=splits, quant=self._prefill_quant(layer))
+
+    def _prefill_quant(self, layer: int):
+        """Extra prefill-kernel inputs of INT8 caches; None for the model-dtype pool."""
+        return None
 
     def attend(self, layer: int, q: torch.Tensor, positions: torch.Tensor, scale: float) -> torch.Tensor:
         """Attention of every sequence in the forward over its own context. Returns [T, Hq * d]."""

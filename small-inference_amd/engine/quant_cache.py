@@ -44,7 +44,6 @@ def blocks_for_budget(cfg: ModelConfig, fmt: str, budget_bytes: int, block_size:
 
 
 class QuantPagedKVCache(PagedKVCache):
-    _prefill_pool_kernel = False  # INT8 pools: multi-token rows attend over the dequantized gather
     def __init__(self, cfg: ModelConfig, num_blocks: int, block_size: int, device: str | torch.device,
                  dtype: torch.dtype, attn_backend: str = "gather", fmt: str = "int8",
                  manager: BlockManager | None = None, n_stage: int = 128):
@@ -126,6 +125,10 @@ class QuantPagedKVCache(PagedKVCache):
             self._tails_dec = self._tails[torch.tensor(self._decode_seqs, device=dev)]
         else:
             self._tails_dec = self._tails
+        if self._prefill_launch is not None and len(self._prefill_seqs) != meta.num_seqs:
+            self._tails_pf = self._tails[torch.tensor(self._prefill_seqs, device=dev)]
+        else:
+            self._tails_pf = self._tails
 
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """Quantize and store this forward's k, v [T, H_kv, d]."""
@@ -189,6 +192,13 @@ class QuantPagedKVCache(PagedKVCache):
             if ctx % B:
                 k[:, -1] = self.stage[layer][:, self._stage_of[m.block_ids_cpu[seq][-1]]].to(self.dtype)
         return k.view(H, -1, d)[:, :ctx], v.view(H, -1, d)[:, :ctx]
+
+    def _prefill_quant(self, layer: int) -> QuantKV:
+        """Scales (and format B's staging, with the tail slots of the forward's multi-token rows) for the prefill
+        kernel, which dequantizes K/V as gather() does."""
+        if self.fmt == "int8":
+            return QuantKV(1, self.k_scale[layer], self.v_scale[layer])
+        return QuantKV(2, self.k_scale[layer], self.v_scale[layer], self.stage[layer], self._tails_pf)
 
     def _kernel_quant(self, layer: int) -> QuantKV:
         """Scales (and format B's staging) for the decode kernel."""

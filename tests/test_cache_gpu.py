@@ -6,8 +6,8 @@ Checked against the oracle: each row's softmax attention over the cache contents
 INT8 caches, the dequantized contents), causal within a chunk. Tolerances: fp32 caches 1e-5; bf16 decode rows
 (the HIP decode kernel) 8e-3 max-abs; bf16 prefill rows of the model-dtype cache (the HIP prefill kernel) 8e-3
 max-abs where |out| < 2 and 2^-7 |out| above, whose bf16 rounding alone reaches 2^-8 |out|; bf16 prefill rows of
-the INT8 caches 3e-2, since they run the reference's gather path, which computes scores and probabilities in the
-model dtype (engine/attention.py).
+the INT8 caches 3e-2 against the oracle's fp32 dequantization, since the prefill kernel dequantizes K/V to bf16
+as the reference's gather path does (engine/quant_cache.py:179-190).
 """
 
 import numpy as np
@@ -75,7 +75,7 @@ def check_rows(cache, meta, q, out, layer, dtype, what):
         assert err[dec].max() <= 8e-3, f"{what}: decode rows {err[dec].max():.3e}"
     if not (~dec).any():
         return
-    if isinstance(cache, QuantPagedKVCache):  # gather path in the model dtype
+    if isinstance(cache, QuantPagedKVCache):  # K/V dequantized to the model dtype, as gather() does
         assert err[~dec].max() <= 3e-2, f"{what}: chunk rows {err[~dec].max():.3e}"
         return
     big = np.abs(ref[~dec]) >= 2

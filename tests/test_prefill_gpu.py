@@ -201,3 +201,69 @@ def test_workspace_shared_with_decode_in_any_order():
     check([3000] * 3, [400] * 3, "0.5B", seed=13)
     again = check([4096], [64], "0.5B", seed=11)
     assert torch.equal(first, again)
+
+
+def int8_pools(k, v, fmt, ctx, tables, g):
+    """Quantize bf16 pools with the reference's quantizer (engine/quant.py): per-token K and V (format "int8"), or
+    per-(block, channel) K (format "int8-kchannel") with each sequence's partial last block of K in a bf16 staging
+    slot and its int8 codes overwritten with noise (so only the staging can give the right answer). Returns the
+    QuantKV, the int8 pools, and the bf16 pools the reference's gather path would attend over."""
+    from engine.hip_decode import QuantKV
+    from engine.quant import dequantize, quantize_per_channel, quantize_per_token
+
+    vq, vs = quantize_per_token(v)
+    v_deq = dequantize(vq, vs[..., None], torch.bfloat16)
+    if fmt == "int8":
+        kq, ks = quantize_per_token(k)
+        return QuantKV(1, ks, vs), kq, vq, dequantize(kq, ks[..., None], torch.bfloat16), v_deq
+    kq, ks = quantize_per_channel(k, dim=2)
+    k_deq = dequantize(kq, ks[:, :, None], torch.bfloat16)
+    Hkv, _, B, D = k.shape
+    stage = torch.zeros(Hkv, len(ctx) + 1, B, D, dtype=torch.bfloat16, device=k.device)
+    tails = []
+    for s, (n, t) in enumerate(zip(ctx, tables)):
+        if n % B == 0:
+            tails.append(-1)
+            continue
+        blk = t[n // B]
+        stage[:, s + 1] = k[:, blk]  # the staged partial block, in the model dtype
+        kq[:, blk] = torch.randint(-127, 128, kq[:, blk].shape, generator=g, device=k.device, dtype=torch.int8)
+        k_deq[:, blk] = k[:, blk]
+        tails.append(s + 1)
+    tails = torch.tensor(tails, dtype=torch.int32, device=k.device)
+    return QuantKV(2, ks, vs, stage, tails), kq, vq, k_deq, v_deq
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int8-kchannel"])
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g4"])
+@pytest.mark.parametrize("splits", [1, None], ids=["one_split", "auto"])
+def test_int8_pools(fmt, shape, splits):
+    """INT8 pools: the kernel dequantizes as the reference's gather path (q * s in fp32, rounded to bf16; format B's
+    partial last block from staging), so its output equals, bit for bit, the bf16 kernel's on those dequantized
+    pools, and is within the bf16 bounds of the oracle on them; keys with outlier channels (x 20 .. 68)."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [300, 1000, 33, 517, 280, 64], [64, 7, 33, 500, 30, 64]
+    print(f"case int8 {fmt} shape={shape} splits={splits}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=21)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    outlier = torch.ones(Hkv, 1, 1, D, device="cuda")
+    outlier[:, :, :, :4] = 20 + 48 * torch.rand(Hkv, 1, 1, 4, generator=g, device="cuda")
+    k = (k.float() * outlier).bfloat16()
+    quant, kq, vq, k_deq, v_deq = int8_pools(k, v, fmt, ctx, tables, g)
+    scale = D ** -0.5
+    got = paged_prefill_attention(q, kq, vq, bt, c, st, ln, scale, max(ctx), max(qlen), num_splits=splits,
+                                  quant=quant)
+    ref_kernel = paged_prefill_attention(q, k_deq, v_deq, bt, c, st, ln, scale, max(ctx), max(qlen),
+                                         num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref_kernel)
+    args = (as_np32(q), as_np32(k_deq), as_np32(v_deq), tables, ctx, starts, qlen, scale)
+    ref32 = paged_ref.prefill(*args, dtype=np.float32)
+    rows = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, qlen)])
+    # The outlier channels make the softmax peaked, and the kernel (like the reference's gather path) rounds the
+    # probabilities to bf16 for P.V: beyond the usual bound, allow that rounding's own error, 2^-9 sum_k p_k |v_k|
+    # (the oracle's attention over |V|).
+    pv_abs = paged_ref.prefill(args[0], args[1], np.abs(args[2]), *args[3:], dtype=np.float32)[rows]
+    err = np.abs(got.double().cpu().numpy()[rows] - ref32[rows])
+    bound = np.where(np.abs(ref32[rows]) < 2, 8e-3, 2 ** -7 * np.abs(ref32[rows])) + 2 ** -9 * pv_abs
+    assert (err <= bound).all(), f"max excess {(err - bound).max():.3e}"
