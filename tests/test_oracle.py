@@ -273,3 +273,16 @@ def test_slots_known_answer():
     ka = GOLDEN["block_manager_allocate_append"]
     assert paged_ref.slots([0, 1], 0, 6, 4) == ka["ops"][0][3]
     assert paged_ref.slots([0, 1, 2, 3], 9, 14, 4) == ka["ops"][4][3]
+
+
+def test_per_channel_beats_per_token_with_outlier_channels():
+    """The reference's motivation for format B (tests/test_quant.py:39-50): with a few outlier channels, per-channel
+    scales over a block's tokens lose less than per-token scales over a token's channels."""
+    rng = np.random.default_rng(15)
+    x = rng.standard_normal((2, 64, 16, 128)).astype(np.float32)
+    x[..., :4] *= 40.0
+    qt, st = paged_ref.quantize_per_token(x)
+    qc, sc = paged_ref.quantize_per_channel(x, axis=2)
+    err_t = np.linalg.norm(paged_ref.dequant_tokens(qt, st) - x) / np.linalg.norm(x)
+    err_c = np.linalg.norm(paged_ref.dequant_channels(qc, sc) - x) / np.linalg.norm(x)
+    assert err_c < err_t / 2, (err_c, err_t)
