@@ -1,9 +1,11 @@
-"""Causal GQA attention over one sequence's gathered K/V: the cache's gather backend and its prefill rows.
+"""Causal GQA attention over one sequence's gathered K/V: the cache's gather backend (and, on the HIP backend, the
+rows of shapes the paged kernels do not cover).
 
 Same contract as the reference's attention() (engine/attention.py:6-28): q [T, Hq, d]; k, v [Hkv, S, d];
 query t sees key s iff k_pos[s] <= q_pos[t]; query head h uses KV head h // g; the g heads of a group are stacked
 along M so each KV head is read once; softmax in at least fp32; returns [T, Hq * d]. Decode rows (one new token
-per sequence) do not come here on the HIP backend: they go to the paged decode kernel.
+per sequence) and prefill chunks do not come here on the HIP backend: they go to the paged decode and prefill
+kernels.
 """
 
 import torch

@@ -7,7 +7,8 @@ Pool layout per layer: K and V as [H_kv, num_blocks, block_size, d] ([2, N, 16, 
 
 Backends (attn_backend, mutable after construction):
   "hip"    decode rows (one new token per sequence) go through the HIP paged-decode kernel in one launch per
-           layer, reading blocks in place; rows with several new tokens (prefill chunks) use the gather path.
+           layer, and rows with several new tokens (prefill chunks) through the HIP paged-prefill kernel in one
+           more, both reading blocks in place; shapes the prefill kernel does not cover use the gather path.
   "triton" the reference's name for the same in-place decode backend: selects the HIP kernel, so callers that
            pass it (the reference's ContinuousEngine defaults to it) run unchanged.
   "gather" every sequence gathers its blocks and runs attention() (the reference's default).
@@ -256,18 +257,14 @@ class PagedKVCache:
         k, v = self.gather(layer, i)
         return attention(q[a:b], k, v, positions[a:b], self._key_positions(m.context_lens[i]), scale)
 
-    # The paged prefill kernel reads the model-dtype pool; caches with other pool formats leave multi-token rows
-    # on the gather path.
-    _prefill_pool_kernel = True
-
     def _prefill_kernel_ok(self, max_context: int) -> bool:
-        """Whether this forward's multi-token rows can run the paged prefill kernel."""
+        """Whether this forward's multi-token rows can run the paged prefill kernel (bf16 model, bf16 or INT8 pool,
+        16-token blocks, head_dim 64/128, group <= 8, contexts <= 32768)."""
         from .hip_prefill import prefill_supported
 
         cfg = self.cfg
-        return (self._prefill_pool_kernel and
-                prefill_supported(self.dtype, self.k.dtype, self.block_size, cfg.head_dim,
-                                  cfg.num_q_heads // cfg.num_kv_heads, max_context))
+        return prefill_supported(self.dtype, self.k.dtype, self.block_size, cfg.head_dim,
+                                 cfg.num_q_heads // cfg.num_kv_heads, max_context)
 
     def _attend_prefill(self, layer: int, q: torch.Tensor, scale: float, out: torch.Tensor) -> None:
         """Multi-token rows of the forward, written into their rows of out [T, Hq, d] by the prefill kernel."""
