@@ -194,11 +194,11 @@ int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
 
 /* Key splits for a prefill call (no counterpart in the reference, whose gather path has no grid): about two
  * workgroups per CU over the call's units, at least 256 keys per split, at most 32 splits. A unit is a KV head
- * and 16 tt new tokens of one sequence, tt = 8 / G 16-token subtiles for a group of G = Hq / Hkv query heads
- * (1 for G > 4); query_tiles = sum over sequences of ceil(query_len / 16). cu_count <= 0 asks the current
- * device. */
-int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int64_t query_tiles, int32_t max_context,
-                            int32_t cu_count);
+ * and 16 tt new tokens of one sequence, tt = 8 / G 16-token subtiles (at least 1) for a group of G = Hq / Hkv
+ * query heads (head_dim is part of the policy's signature; both head dims use 8 column tiles today);
+ * query_tiles = sum over sequences of ceil(query_len / 16). cu_count <= 0 asks the current device. */
+int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t query_tiles,
+                            int32_t max_context, int32_t cu_count);
 
 /* Workspace bytes sipa_prefill needs for these sizes and num_splits (0 when one split runs). */
 int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,

@@ -9,7 +9,7 @@
 // [0, P0 + ntok) of the sequence, P0 the position of the tile's first token; they are cut into splits of `chunk`
 // keys, one workgroup each, so that a short chunk over a long context still fills the chip. The four waves of a
 // workgroup stream the same 32-key tiles, which the workgroup loads cooperatively into double-buffered LDS (one
-// HBM read per split), and each wave owns two query heads of the GQA group (heads w and w + 4), so no cross-wave
+// HBM read per split), and each wave owns its own column tiles (a query head and 16 of the unit's tokens), so no cross-wave
 // merge is needed. A unit with one split writes its rows; otherwise every split writes its softmax state
 // (m, l, unnormalised O) and the last split workgroup of the unit to finish merges them, as the decode kernels do.
 // Per tile and head, with the decode kernels' layouts (decode.hip) and the query tokens in place of the heads:
@@ -56,19 +56,24 @@ struct PrefillArgs {
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kPrefillColsPerWave = 2;                              // column tiles (head, 16 tokens) per wave
-constexpr int kPrefillCols = kPrefillColsPerWave * kWaves;           // column tiles per unit: G * tt <= 8
-constexpr int kPrefillSlots = kPrefillCols * 16;                     // (column, token) rows of a split state
+// Column tiles (head, 16 tokens) per wave. Two at either head_dim: four at head_dim 64 (more independent softmax
+// chains per wave, each K/V operand read serving four MFMA columns) measured slower, 86.7 -> 112 us on four 2048-token
+// prompts, with the register use halving the waves per SIMD and the 32-token units coarsening the causal tiles.
+constexpr int prefill_cols_per_wave(int /*D*/) { return 2; }
+constexpr int kPrefillMaxGroup = 8;
 
-// 16-token subtiles per unit for a GQA group of G heads: as many as fit the 8 column tiles (G = 7: 1, G = 4: 2,
-// G = 1: 8), so that every group size keeps the four waves busy.
-static inline int prefill_subtiles(int G) { return G >= 8 ? 1 : 8 / G; }
+// 16-token subtiles per unit for a GQA group of G heads: as many as fit the workgroup's 8 column tiles (G = 7: 1,
+// G = 4: 2, G = 1: 8), so every group size keeps the waves busy.
+static inline int prefill_subtiles(int G, int D) {
+  const int cols = prefill_cols_per_wave(D) * kWaves;
+  return G >= cols ? 1 : cols / G;
+}
 constexpr int kPrefillMaxSplits = 32;
 
 // Merge one round of up to KB splits j0 .. of one (head, token) row: every load issued before the first is used;
 // entries past nvalid re-read the last split and get weight 0. Split 0 always holds the row's first key, so M is
 // finite from the first round on.
-template <int KB>
+template <int KB, int SLOTS>
 __device__ __forceinline__ void prefill_merge_round(const PrefillArgs& a, __amdgpu_buffer_rsrc_t rows,
                                                     int64_t mrow, int off, int split_bytes, int j0, int nvalid,
                                                     float& M, float& den, f32x4& num) {
@@ -77,8 +82,8 @@ __device__ __forceinline__ void prefill_merge_round(const PrefillArgs& a, __amdg
 #pragma unroll
   for (int u = 0; u < KB; ++u) {
     const int j = min(j0 + u, nvalid - 1);
-    mj[u] = load_coherent(a.pm + mrow + (int64_t)j * kPrefillSlots);
-    lj[u] = load_coherent(a.pl + mrow + (int64_t)j * kPrefillSlots);
+    mj[u] = load_coherent(a.pm + mrow + (int64_t)j * SLOTS);
+    lj[u] = load_coherent(a.pl + mrow + (int64_t)j * SLOTS);
     pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, off + j * split_bytes, 0, kAuxSc1);
   }
 #pragma unroll
@@ -155,10 +160,11 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
 // issued NPRE tiles before its LDS store.
 template <int D, int NPRE, int MODE>
 __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
+  constexpr int CW = prefill_cols_per_wave(D);
+  constexpr int kSlots = CW * kWaves * 16;  // (column, token) rows of a split state
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
   constexpr int CPK = D / 8;                // 16-byte chunks per key row
   constexpr int LPT = 32 * CPK / kThreads;  // chunks per thread per K (or V) tile
-  constexpr int CW = kPrefillColsPerWave;
   static_assert(LPT * kThreads == 32 * CPK, "tile chunks must divide over the workgroup");
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
@@ -386,10 +392,10 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   for (int ci = 0; ci < CW; ++ci) lsum[ci] = l_run[ci][0];
   if (nvalid > 1) {
     // This split's state for column c, token r: m, l at slot 16 c + r, O at channels 16 dt + 4 q4 .. of that row.
-    const int64_t base = ((int64_t)u * a.nsplit + sp) * kPrefillSlots;
-    const int split_bytes = kPrefillSlots * D * 4;
+    const int64_t base = ((int64_t)u * a.nsplit + sp) * kSlots;
+    const int split_bytes = kSlots * D * 4;
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
-        a.part + (int64_t)u * a.nsplit * kPrefillSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
+        a.part + (int64_t)u * a.nsplit * kSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
       if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
@@ -413,20 +419,20 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     if (!last_flag) return;
     // The last split to arrive: one thread per (column, token, channel quad) merges every split's state.
     constexpr int Q = D / 4;
-    for (int idx = threadIdx.x; idx < kPrefillSlots * Q; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < kSlots * Q; idx += kThreads) {
       const int slot = idx / Q, cq = idx % Q;
       const int c = slot >> 4, rr = slot & 15;
       const int g = c % G, tok = 16 * (c / G) + rr;
       if (c / G >= TT || tok >= ntok) continue;
-      const int64_t mrow = (int64_t)u * a.nsplit * kPrefillSlots + slot;
+      const int64_t mrow = (int64_t)u * a.nsplit * kSlots + slot;
       const int off = (slot * D + 4 * cq) * 4;
       float M = kNegInf, den = 0.f;
       f32x4 num = {0.f, 0.f, 0.f, 0.f};
       if (nvalid <= 4) {
-        prefill_merge_round<4>(a, rows, mrow, off, split_bytes, 0, nvalid, M, den, num);
+        prefill_merge_round<4, kSlots>(a, rows, mrow, off, split_bytes, 0, nvalid, M, den, num);
       } else {
         for (int j0 = 0; j0 < nvalid; j0 += 8)
-          prefill_merge_round<8>(a, rows, mrow, off, split_bytes, j0, nvalid, M, den, num);
+          prefill_merge_round<8, kSlots>(a, rows, mrow, off, split_bytes, j0, nvalid, M, den, num);
       }
       const f32x4 o = num / den;
       uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
@@ -487,7 +493,7 @@ struct PrefillLayout {
 static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   PrefillLayout l;
-  const int64_t rows = units * nsplit * kPrefillSlots;
+  const int64_t rows = units * nsplit * prefill_cols_per_wave(D) * kWaves * 16;
   l.counters = 0;
   l.pm = kCounterBytes;
   l.pl = l.pm + up(rows * 4);
@@ -496,11 +502,11 @@ static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
   return l;
 }
 
-extern "C" int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int64_t query_tiles,
-                                       int32_t max_context, int32_t cu_count) {
+extern "C" int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       int64_t query_tiles, int32_t max_context, int32_t cu_count) {
   if (num_kv_heads <= 0 || num_q_heads < num_kv_heads) return 1;
   if (cu_count <= 0) cu_count = sipa_device_cu_count(-1);
-  const int tt = prefill_subtiles(num_q_heads / num_kv_heads);
+  const int tt = prefill_subtiles(num_q_heads / num_kv_heads, head_dim);
   return prefill_splits_host((int64_t)num_kv_heads * ((query_tiles + tt - 1) / tt), max_context, cu_count);
 }
 
@@ -512,7 +518,7 @@ extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_
   const int chunk = prefill_chunk(max_context, num_splits);
   const int nsplit = (max_context + chunk - 1) / chunk;
   if (nsplit <= 1) return 0;
-  const int nt = 16 * prefill_subtiles(num_q_heads / num_kv_heads);
+  const int nt = 16 * prefill_subtiles(num_q_heads / num_kv_heads, head_dim);
   const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + nt - 1) / nt);
   return prefill_layout(units, nsplit, head_dim).total;
 }
@@ -525,7 +531,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   if (S == 0 || p->max_query_len == 0) return SIPA_OK;
   SIPA_CHECK(S > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, SIPA_EINVAL, "bad sequence or head counts");
   const int G = Hq / Hkv;
-  SIPA_CHECK(G <= kPrefillCols, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kPrefillCols);
+  SIPA_CHECK(G <= kPrefillMaxGroup, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kPrefillMaxGroup);
   SIPA_CHECK(D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {64, 128}", D);
   SIPA_CHECK(p->block_size == 16, SIPA_EUNSUPPORTED, "block_size %d != 16", p->block_size);
   SIPA_CHECK(p->max_context > 0 && p->max_context <= kMaxSplitBlocks * 16, SIPA_EUNSUPPORTED,
@@ -557,7 +563,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
                      p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
                  SIPA_EINVAL, "format B needs a 16-byte aligned bf16 staging pool and tail slots");
   }
-  const int tt = prefill_subtiles(G);
+  const int tt = prefill_subtiles(G, D);
   const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
   const int64_t units = (int64_t)S * Hkv * qtiles;
   int splits = p->num_splits;
@@ -575,7 +581,8 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
     SIPA_CHECK(p->workspace != nullptr && ((uintptr_t)p->workspace & 255) == 0 && p->workspace_bytes >= lay.total,
                SIPA_EWORKSPACE, "%d key splits need a 256-byte aligned workspace of %lld bytes (have %lld)", nsplit,
                (long long)lay.total, (long long)p->workspace_bytes);
-    SIPA_CHECK((int64_t)nsplit * kPrefillSlots * D * 4 <= 0x7fffffff, SIPA_EINVAL, "split state too large");
+    SIPA_CHECK((int64_t)nsplit * prefill_cols_per_wave(D) * kWaves * 16 * D * 4 <= 0x7fffffff, SIPA_EINVAL,
+               "split state too large");
   }
   PrefillArgs a;
   a.q = p->q;

@@ -79,7 +79,7 @@ SIGNATURES = {
     "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp]),
     "sipa_prefill": (i32, [_c.POINTER(PrefillParams), vp]),
     "sipa_paged_metadata": (i32, [vp, i64, i32, i32, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
-    "sipa_prefill_splits": (i32, [i32, i32, i64, i32, i32]),
+    "sipa_prefill_splits": (i32, [i32, i32, i32, i64, i32, i32]),
     "sipa_prefill_workspace_bytes": (i64, [i32, i32, i32, i32, i32, i32, i32]),
     "sipa_quantize_store_tokens": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, i64, i64,
                                          vp]),

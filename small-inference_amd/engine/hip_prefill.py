@@ -29,11 +29,11 @@ def _scale_dtype(t: torch.Tensor) -> int:
     raise ValueError(f"scales must be fp16 or fp32, got {t.dtype}")
 
 
-def prefill_splits(num_q_heads: int, num_kv_heads: int, query_lens: list[int], max_context: int,
+def prefill_splits(num_q_heads: int, num_kv_heads: int, head_dim: int, query_lens: list[int], max_context: int,
                    cu_count: int = 0) -> int:
     """Key splits per query tile for a call whose sequences have these new-token counts (library policy)."""
     tiles = sum(-(-n // 16) for n in query_lens)
-    return _hip.lib().sipa_prefill_splits(num_q_heads, num_kv_heads, tiles, max_context, cu_count)
+    return _hip.lib().sipa_prefill_splits(num_q_heads, num_kv_heads, head_dim, tiles, max_context, cu_count)
 
 
 def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -102,7 +102,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     lib = _hip.lib()
     if num_splits is None:
         lens = host_query_lens if host_query_lens is not None else [max_query_len] * S
-        num_splits = prefill_splits(Hq, Hkv, lens, max_context)
+        num_splits = prefill_splits(Hq, Hkv, D, lens, max_context)
     p.num_splits = num_splits
     stream = _hip.stream_of(q)
     nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)

@@ -210,7 +210,8 @@ class PagedKVCache:
             from .hip_prefill import prefill_splits
 
             max_ctx = max(meta.context_lens[i] for i in pf)
-            splits = prefill_splits(self.cfg.num_q_heads, self.cfg.num_kv_heads, [per_seq[i] for i in pf], max_ctx)
+            cfg = self.cfg
+            splits = prefill_splits(cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, [per_seq[i] for i in pf], max_ctx)
             self._prefill_launch = (bt, ctx, rows[:len(pf)], rows[len(pf):], max_ctx, max(per_seq[i] for i in pf),
                                     splits)
             self._prefill_seqs = pf

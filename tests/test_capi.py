@@ -198,16 +198,18 @@ def test_prefill_split_policy_and_workspace():
     """About two workgroups per CU over (KV head, 16-token query tile) units, no split under 256 keys, at most
     32; the workspace holds (m, l, O) for 8 heads x 16 tokens per unit and split, and nothing for one split."""
     lib = _hip.lib()
-    assert lib.sipa_prefill_splits(14, 2, 32, 8192, 256) == 8     # one 512-token chunk at 8K: 64 units
-    assert lib.sipa_prefill_splits(14, 2, 512, 2048, 256) == 1    # 4 prompts of 2048: 1024 units
-    assert lib.sipa_prefill_splits(8, 2, 32, 8192, 256) == 16     # G = 4: 32-token units, 32 of them
-    assert lib.sipa_prefill_splits(14, 2, 1, 100, 256) == 1       # never under 256 keys per split
-    assert lib.sipa_prefill_splits(7, 1, 1, 32768, 256) == 32     # capped
-    assert lib.sipa_prefill_workspace_bytes(1, 14, 2, 64, 512, 8192, 1) == 0
+    assert lib.sipa_prefill_splits(12, 2, 128, 32, 8192, 256) == 8    # 1.5B, 512-token chunk at 8K: 64 units
+    assert lib.sipa_prefill_splits(14, 2, 64, 32, 8192, 256) == 8     # 0.5B likewise
+    assert lib.sipa_prefill_splits(14, 2, 64, 512, 2048, 256) == 1    # 4 prompts of 2048: 1024 units
+    assert lib.sipa_prefill_splits(8, 2, 128, 32, 8192, 256) == 16    # G = 4: 32-token units, 32 of them
+    assert lib.sipa_prefill_splits(14, 2, 64, 1, 100, 256) == 1       # never under 256 keys per split
+    assert lib.sipa_prefill_splits(7, 1, 128, 1, 32768, 256) == 32    # capped
+    assert lib.sipa_prefill_workspace_bytes(1, 12, 2, 128, 512, 8192, 1) == 0
     rows = 2 * 32 * 8 * 128           # units x splits x 8 columns x 16 tokens, after the 256 KiB of counters
-    got = lib.sipa_prefill_workspace_bytes(1, 14, 2, 64, 512, 8192, 8)
-    assert (1 << 18) + rows * (64 + 2) * 4 <= got <= (1 << 18) + rows * (64 + 2) * 4 + 3 * 256
-    assert lib.sipa_prefill_workspace_bytes(1, 14, 2, 128, 512, 8192, 8) > got
-    assert lib.sipa_prefill_workspace_bytes(1, 4, 2, 64, 512, 8192, 8) < got  # G = 2: 64-token units
+    got = lib.sipa_prefill_workspace_bytes(1, 12, 2, 128, 512, 8192, 8)
+    assert (1 << 18) + rows * (128 + 2) * 4 <= got <= (1 << 18) + rows * (128 + 2) * 4 + 3 * 256
+    d64 = lib.sipa_prefill_workspace_bytes(1, 14, 2, 64, 512, 8192, 8)
+    assert (1 << 18) + rows * (64 + 2) * 4 <= d64 <= (1 << 18) + rows * (64 + 2) * 4 + 3 * 256
+    assert lib.sipa_prefill_workspace_bytes(1, 4, 2, 64, 512, 8192, 8) < d64  # G = 2: 64-token units
     rc = lib.sipa_prefill(ctypes.byref(prefill_params(max_context=8192, num_splits=8)), None)
     assert rc == _hip.EWORKSPACE, lib.sipa_last_error()
