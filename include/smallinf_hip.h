@@ -179,9 +179,11 @@ typedef struct sipa_prefill_params {
   const void* v_scale;
   int32_t v_scale_dtype;
   int64_t vs_stride_h, vs_stride_n;
-  const void* stage;
+  const void* stage;            /* [Hkv, num_stage, B, D] bf16 */
   int64_t st_stride_h, st_stride_n, st_stride_b;
-  const int32_t* tail_slots;   /* [S] staging slot of each sequence's partial last block, -1 if none */
+  int32_t num_stage;
+  const int32_t* tail_slots;   /* [S] staging slot of each sequence's partial last block, -1 if none (slots are
+                                  clamped to [0, num_stage)) */
   /* Key splits per 16-token query tile (<= 0: sipa_prefill_splits with units = S x Hkv x query tiles) and the
      workspace they need when more than one split runs: sipa_prefill_workspace_bytes() bytes, laid out and reused
      as sipa_decode_params.workspace (the same buffer may serve both); at most 65536 KV heads x query tiles. */

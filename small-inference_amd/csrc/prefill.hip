@@ -46,6 +46,7 @@ struct PrefillArgs {
   int64_t ks_sh, ks_sn, vs_sh, vs_sn;
   const uint16_t* stage;
   int64_t st_sh, st_sn, st_sb;
+  int32_t n_stage;
   const int32_t* tails;
   float scale_log2;
   int* counters;           // [units] split arrivals, zero between launches
@@ -241,7 +242,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   // q * s in fp32 rounded to bf16, the values the reference's gather path attends over. Format B's keys at or
   // past the sequence's last full block come from its bf16 staging slot instead.
   const int nq = MODE == 2 ? ctx / 16 * 16 : 0;
-  const int tail = MODE == 2 ? a.tails[s] : -1;
+  const int tail = MODE == 2 ? min(a.tails[s], a.n_stage - 1) : -1;
   KvRaw<MODE> raw[NPRE][LPT];
   auto gload = [&](int set, int t) {
 #pragma unroll
@@ -559,7 +560,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
     SIPA_CHECK(((uintptr_t)p->k_scale % ksz) == 0 && ((uintptr_t)p->v_scale % vsz) == 0, SIPA_EINVAL,
                "scales must be aligned to their element size");
     if (mode == SIPA_KV_INT8_KCHAN)
-      SIPA_CHECK(p->stage && p->tail_slots && aligned16p(p->stage) && p->st_stride_h % 8 == 0 &&
+      SIPA_CHECK(p->stage && p->tail_slots && p->num_stage > 0 && aligned16p(p->stage) && p->st_stride_h % 8 == 0 &&
                      p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
                  SIPA_EINVAL, "format B needs a 16-byte aligned bf16 staging pool and tail slots");
   }
@@ -622,6 +623,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.st_sh = p->st_stride_h;
   a.st_sn = p->st_stride_n;
   a.st_sb = p->st_stride_b;
+  a.n_stage = p->num_stage;
   a.tails = p->tail_slots;
   char* ws = (char*)p->workspace;
   a.counters = nsplit > 1 ? (int*)(ws + lay.counters) : nullptr;

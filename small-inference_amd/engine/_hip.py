@@ -62,8 +62,8 @@ class PrefillParams(ctypes.Structure):
         ("out", vp), ("out_stride_t", i64), ("out_stride_h", i64),
         ("kv_mode", i32), ("k_scale", vp), ("k_scale_dtype", i32), ("ks_stride_h", i64), ("ks_stride_n", i64),
         ("v_scale", vp), ("v_scale_dtype", i32), ("vs_stride_h", i64), ("vs_stride_n", i64),
-        ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64), ("tail_slots", vp),
-        ("num_splits", i32), ("workspace", vp), ("workspace_bytes", i64),
+        ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64), ("num_stage", i32),
+        ("tail_slots", vp), ("num_splits", i32), ("workspace", vp), ("workspace_bytes", i64),
     ]
 
 

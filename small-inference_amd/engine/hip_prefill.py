@@ -43,9 +43,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                             host_query_lens: list[int] | None = None, quant=None) -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
-    q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16, one layer
-    of the pool with this forward's K/V already written; block_tables [S, >= ceil(max_context / 16)] int32;
-    context_lens [S] int32 (after the writes); query_starts, query_lens [S] int32: sequence s's new tokens are rows
+    q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16 (int8 with
+    quant), one layer of the pool with this forward's K/V already written; block_tables
+    [S, >= ceil(max_context / 16)] int32; context_lens [S] int32 (after the writes); query_starts, query_lens [S] int32: sequence s's new tokens are rows
     query_starts[s] .. + query_lens[s] - 1 of q at positions context_lens[s] - query_lens[s] ..; max_context and
     max_query_len are the host-known maxima. Writes those rows of out ([T, Hq, D], q's dtype; other rows are left
     as they are) and returns out. Each 16-token query tile's keys are cut into num_splits splits (default: the
@@ -98,7 +98,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
             if tails.numel() < S or not tails.is_contiguous():
                 raise ValueError("tail slots must be a contiguous vector covering every sequence")
             p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = st.data_ptr(), *st.stride()[:3]
-            p.tail_slots = tails.data_ptr()
+            p.num_stage, p.tail_slots = st.shape[1], tails.data_ptr()
+            _hip.require_gpu(q, st, tails)
+        _hip.require_gpu(q, ks, vs)
     lib = _hip.lib()
     if num_splits is None:
         lens = host_query_lens if host_query_lens is not None else [max_query_len] * S
