@@ -113,6 +113,10 @@ class BlockManager:
         of the tables follow these changes)."""
         self._table_listeners.append(fn)
 
+    def remove_table_listener(self, fn: Callable[[int, int], None]) -> None:
+        """Stop calling fn (added by add_table_listener)."""
+        self._table_listeners.remove(fn)
+
     def _pop_blocks(self, count: int) -> list[int]:
         taken = []
         for _ in range(count):

@@ -63,6 +63,10 @@ class DeviceBlockTables:
         for seq in manager.seq_ids():
             self._on_change(seq, 0)
 
+    def close(self) -> None:
+        """Stop following the block manager."""
+        self.manager.remove_table_listener(self._on_change)
+
     def row(self, seq_id: int) -> int:
         """The table row of a live sequence."""
         return self._row_of[seq_id]

@@ -60,6 +60,7 @@ class DecodeGraphRunner:
         if self.buckets[-1] < max_batch or self.buckets[0] < 1:
             raise ValueError("buckets must cover 1 .. max_batch")
         dev = cache.device
+        self._own_tables = device_tables is None
         if device_tables is None:
             device_tables = DeviceBlockTables(manager, dev, max_seqs or 4 * max_batch + 1, self.width)
         if device_tables.max_blocks < self.width:
@@ -178,6 +179,8 @@ class DecodeGraphRunner:
         return logits[:b]
 
     def close(self) -> None:
-        """Drop the graphs and return the scratch block to the manager."""
+        """Drop the graphs, return the scratch block to the manager, and detach device tables made here."""
         self._graphs.clear()
         self.manager.free(SCRATCH_SEQ)
+        if self._own_tables:
+            self.tables.close()
