@@ -5,12 +5,12 @@
 // (query at position p sees keys 0 .. p, query head g uses KV head g / G, softmax in fp32, probabilities rounded
 // to the model dtype before P.V). This kernel computes the same rows in place from the pool.
 //
-// Work unit: (sequence s, KV head h, tile j of 16 consecutive new tokens). The unit's keys are positions
-// [0, P0 + ntok) of the sequence, P0 the position of the tile's first token; they are cut into splits of `chunk`
-// keys, one workgroup each, so that a short chunk over a long context still fills the chip. The four waves of a
-// workgroup stream the same 32-key tiles, which the workgroup loads cooperatively into double-buffered LDS (one
-// HBM read per split), and each wave owns its own column tiles (a query head and 16 of the unit's tokens), so no cross-wave
-// merge is needed. A unit with one split writes its rows; otherwise every split writes its softmax state
+// Work unit: (sequence s, KV head h, 16 tt consecutive new tokens). The unit's keys are positions [0, P0 + ntok)
+// of the sequence, P0 the position of the unit's first token; they are cut into splits of `chunk` keys, one
+// workgroup each, so that a short chunk over a long context still fills the chip. The four waves of a workgroup
+// stream the same key tiles (64 keys at head_dim 64, 32 at 128), which the workgroup loads cooperatively into
+// double-buffered LDS (one HBM read per split), and each wave owns its own column tiles (a query head and 16 of
+// the unit's tokens), so no cross-wave merge is needed. A unit with one split writes its rows; otherwise every split writes its softmax state
 // (m, l, unnormalised O) and the last split workgroup of the unit to finish merges them, as the decode kernels do.
 // Per tile and head, with the decode kernels' layouts (decode.hip) and the query tokens in place of the heads:
 //   S^T[16 keys x 16 tokens] = K[16 x 32 d] . Q^T[32 d x 16 tokens]     v_mfma_f32_16x16x32_bf16
@@ -38,7 +38,7 @@ struct PrefillArgs {
   int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / (16 tt))
   int32_t tt;              // 16-token subtiles per unit: G * tt <= 8 column tiles
   int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
-  int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 32)
+  int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 64)
   // INT8 pools (kernel MODE 1, 2): scales and format B's staging, as in sipa_prefill_params
   const void* ks;
   const void* vs;
@@ -106,7 +106,7 @@ __device__ __forceinline__ void prefill_merge_round(const PrefillArgs& a, __amdg
 }
 
 template <int D>
-struct PrefillSmem {
+struct PrefillSmem {  // one 32-key row group; a KT-key tile is KT / 32 of them
   static constexpr int kPitch = D + 8;       // bf16 per LDS row of a 32-key tile
   static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
 };
@@ -159,14 +159,16 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
 
 // NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
 // issued NPRE tiles before its LDS store.
-template <int D, int NPRE, int MODE>
+template <int D, int NPRE, int MODE, int KT>
 __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
+  static_assert(KT == 32 || KT == 64, "key tiles of 32 or 64 keys");
+  constexpr int MT = KT / 16, HT = KT / 32;  // 16-key row tiles, 32-key halves
   constexpr int CW = prefill_cols_per_wave(D);
   constexpr int kSlots = CW * kWaves * 16;  // (column, token) rows of a split state
-  constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = PrefillSmem<D>::kTile;
+  constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = HT * PrefillSmem<D>::kTile;
   constexpr int CPK = D / 8;                // 16-byte chunks per key row
-  constexpr int LPT = 32 * CPK / kThreads;  // chunks per thread per K (or V) tile
-  static_assert(LPT * kThreads == 32 * CPK, "tile chunks must divide over the workgroup");
+  constexpr int LPT = KT * CPK / kThreads;  // chunks per thread per K (or V) tile
+  static_assert(LPT * kThreads == KT * CPK, "tile chunks must divide over the workgroup");
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
@@ -234,7 +236,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   }
   __syncthreads();  // block ids staged
 
-  const int ntiles = (kv_end - k_lo + 31) >> 5;
+  const int ntiles = (kv_end - k_lo + KT - 1) / KT;
   // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
   // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
   // (temporal) loads: every query tile of the sequence reads the same keys, so L2 keeps serving them.
@@ -248,7 +250,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i, cg = c % CPK;
-      const int rel = min(32 * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
+      const int rel = min(KT * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
       const int64_t blk = bids[rel >> 4];
       const int off = rel & 15;
       KvRaw<MODE>& x = raw[set][i];
@@ -305,23 +307,23 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 
   auto tile = [&](int t) {
     const int buf = t & 1;
-    const int t0 = k_lo + 32 * t;
-    const bool masked = t0 + 31 > P0 || t0 + 32 > kv_end;  // some key of the tile is hidden from some token
+    const int t0 = k_lo + KT * t;
+    const bool masked = t0 + KT - 1 > P0 || t0 + KT > kv_end;  // some key of the tile is hidden from some token
     const uint16_t* ks = sm[buf][0];
     const uint16_t* vs = sm[buf][1];
     // The K operands of the tile serve both column tiles of the wave.
-    bf16x8 kop[2][KS];
+    bf16x8 kop[MT][KS];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int jj = 0; jj < KS; ++jj) kop[mt][jj] = *(const bf16x8*)(ks + (16 * mt + r) * P + 32 * jj + 8 * q4);
-    bf16x8 pop[CW];
+    bf16x8 pop[CW][HT];
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
       if (!cvalid[ci]) continue;  // wave-uniform
-      f32x4 sc[2];
+      f32x4 sc[MT];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         sc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int jj = 0; jj < KS; ++jj)
@@ -330,15 +332,16 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       if (masked) {
         const int tok_pos = P0 + ctok[ci] + r;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = t0 + 16 * mt + 4 * q4 + i;  // key position of accumulator row (mt, q4, i)
             if (kp > tok_pos || kp >= kv_end) sc[mt][i] = kNegInf;
           }
       }
-      float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      float mx = kNegInf;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) mx = fmaxf(mx, fmaxf(fmaxf(sc[mt][0], sc[mt][1]), fmaxf(sc[mt][2], sc[mt][3])));
       mx = max_over_rows_swap(mx) * a.scale_log2;
       // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
       // below are taken as 0 then, so that -inf - -inf never forms.
@@ -352,19 +355,27 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       }
       const float m_off = m_run[ci] == kNegInf ? 0.f : m_run[ci];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pop[ci][i] = (__bf16)fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_off));
+      for (int hf = 0; hf < HT; ++hf)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          pop[ci][hf][i] = (__bf16)fast_exp2(fmaf(sc[2 * hf + (i >> 2)][i & 3], a.scale_log2, -m_off));
       // The denominators on the matrix cores: ones . P^T sums each token's bf16 probabilities (the values the
-      // P.V product uses) into every row of l_run, in place of eight VALU adds and a cross-row reduction.
-      l_run[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[ci], l_run[ci], 0, 0, 0);
-    }
-    // V^T operands, each shared by both column tiles.
+      // P.V product uses) into every row of l_run, in place of VALU adds and a cross-row reduction.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const bf16x8 vop = read_v_operand<bf16x8>(vs, tr_off, P, 16 * dt);
-#pragma unroll
-      for (int ci = 0; ci < CW; ++ci)
-        if (cvalid[ci]) acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci], acc[ci][dt], 0, 0, 0);
+      for (int hf = 0; hf < HT; ++hf)
+        l_run[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[ci][hf], l_run[ci], 0, 0, 0);
     }
+    // V^T operands (32 keys each), each shared by both column tiles.
+#pragma unroll
+    for (int hf = 0; hf < HT; ++hf)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 vop = read_v_operand<bf16x8>(vs + 32 * P * hf, tr_off, P, 16 * dt);
+#pragma unroll
+        for (int ci = 0; ci < CW; ++ci)
+          if (cvalid[ci])
+            acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci][hf], acc[ci][dt], 0, 0, 0);
+      }
   };
 
   // Register set k % NPRE carries tile k from its global loads to its LDS store; LDS is double-buffered (tile t
@@ -469,12 +480,12 @@ using namespace sipa;
 
 static bool aligned16p(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Keys per split for a requested split count: ceil(max_context / splits) rounded up to a multiple of 32 (the key
+// Keys per split for a requested split count: ceil(max_context / splits) rounded up to a multiple of 64 (the key
 // tile), at least 256; the launch then has ceil(max_context / chunk) splits.
 static int prefill_chunk(int max_context, int splits) {
   splits = std::max(1, std::min(splits, kPrefillMaxSplits));
   const int c = (max_context + splits - 1) / splits;
-  return std::max(256, (c + 31) / 32 * 32);
+  return std::max(256, (c + 63) / 64 * 64);
 }
 
 // Split count policy: about two workgroups per CU over all units (units = KV heads x query tiles of
@@ -632,14 +643,17 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)wgs), block(kThreads);
+  // Key tiles: 64 keys at head_dim 64 (one barrier, one max reduction and one rescale test per 64 keys: four
+  // 2048-token prompts 94 -> 84 us), 32 at head_dim 128, whose registers would otherwise halve the waves per SIMD
+  // (166 -> 221 us). Tiles in flight (NPRE) within the register budget.
   if (D == 64) {
-    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 0>), grid, block, 0, st, a);
-    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 1>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_mfma_bf16<64, 3, 2>), grid, block, 0, st, a);
+    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 0, 64>), grid, block, 0, st, a);
+    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 1, 64>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 2, 64>), grid, block, 0, st, a);
   } else {
-    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 0>), grid, block, 0, st, a);
-    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 1>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 1, 2>), grid, block, 0, st, a);  // registers: one tile ahead
+    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 0, 32>), grid, block, 0, st, a);
+    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 1, 32>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 1, 2, 32>), grid, block, 0, st, a);  // registers: one tile ahead
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
