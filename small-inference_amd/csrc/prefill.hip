@@ -10,8 +10,9 @@
 // workgroup each, so that a short chunk over a long context still fills the chip. The four waves of a workgroup
 // stream the same key tiles (64 keys at head_dim 64, 32 at 128), which the workgroup loads cooperatively into
 // double-buffered LDS (one HBM read per split), and each wave owns its own column tiles (a query head and 16 of
-// the unit's tokens), so no cross-wave merge is needed. A unit with one split writes its rows; otherwise every split writes its softmax state
-// (m, l, unnormalised O) and the last split workgroup of the unit to finish merges them, as the decode kernels do.
+// the unit's tokens), so no cross-wave merge is needed. A unit with one split writes its rows; otherwise every
+// split writes its softmax state (m, l, unnormalised O) and the last split workgroup of the unit to finish merges
+// them, as the decode kernels do.
 // Per tile and head, with the decode kernels' layouts (decode.hip) and the query tokens in place of the heads:
 //   S^T[16 keys x 16 tokens] = K[16 x 32 d] . Q^T[32 d x 16 tokens]     v_mfma_f32_16x16x32_bf16
 //   causal mask: key position > token position -> -inf; online softmax per token (exp2 domain, lazy rescale)
