@@ -45,8 +45,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16 (int8 with
     quant), one layer of the pool with this forward's K/V already written; block_tables
-    [S, >= ceil(max_context / 16)] int32; context_lens [S] int32 (after the writes); query_starts, query_lens [S] int32: sequence s's new tokens are rows
-    query_starts[s] .. + query_lens[s] - 1 of q at positions context_lens[s] - query_lens[s] ..; max_context and
+    [S, >= ceil(max_context / 16)] int32; context_lens [S] int32 (after the writes); query_starts, query_lens [S]
+    int32: sequence s's new tokens are rows query_starts[s] .. + query_lens[s] - 1 of q at positions
+    context_lens[s] - query_lens[s] ..; max_context and
     max_query_len are the host-known maxima. Writes those rows of out ([T, Hq, D], q's dtype; other rows are left
     as they are) and returns out. Each 16-token query tile's keys are cut into num_splits splits (default: the
     library's policy over host_query_lens when given, else over S x ceil(max_query_len / 16) tiles).
