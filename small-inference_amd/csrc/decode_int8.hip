@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
   __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
-  __shared__ int bids[kMaxSplitBlocks];
+  __shared__ int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
   __shared__ int last_flag;
 
   const WorkItem w = work_item(a);
