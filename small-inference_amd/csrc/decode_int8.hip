@@ -18,8 +18,9 @@
 //   O^T += V_int^T . P'^T on the fp16 MFMA with the per-token V scale folded into P (P' = p s_v, fp16), as the
 //     reference does (acc += (p s_v) v_int; l keeps the unscaled p). The V tile goes to LDS already converted to
 //     fp16 and is read back transposed.
-// Each lane loads a contiguous D/4-byte piece of a K row (channels (D/4) q4 .. (D/4)(q4+1)), so the query operand
-// uses that channel order too: k-slot 8 j + i of lane group q4 is channel (D/4) q4 + 8 j + i.
+// Lane (r, q4) loads 16-byte pieces 64 j + 16 q4 of K row r (one load instruction covers 64 contiguous bytes of each
+// of 16 rows), so the query operand uses that channel order too: k-slot 8 jj + i of lane group q4 is channel
+// 64 (jj / 2) + 16 q4 + 8 (jj % 2) + i.
 #include "decode_common.h"
 
 namespace sipa {
@@ -64,7 +65,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   constexpr int VC = D / 64;   // 16-byte V chunks (16 codes) per lane per block
   constexpr int VP = MfmaSmem<D>::kVPitch;
   constexpr int CPR = D / 16;  // 16-code chunks per token row
-  constexpr int QW = D / 4;    // channels per lane group
+
   __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
   __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
@@ -78,6 +79,9 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int G = a.G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  // K codes: load j of lane (r, q4) is bytes 64 j + 16 q4 .. + 15 of row r, so that each load instruction covers 64
+  // contiguous bytes of each of 16 rows; k-step jj of lane group q4 then holds channels kchan(jj) .. kchan(jj) + 7.
+  auto kchan = [&](int jj) { return 64 * (jj >> 1) + 16 * q4 + 8 * (jj & 1); };
 
   const int wend = min(w.end, start + kMaxInt8Split);  // the host never makes longer splits; LDS holds no more
   int ids[kIdsPerThread];
@@ -85,7 +89,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   // The query group in bf16, channel order of the int8 K layout: k-step j of lane (r, q4) (zero for r >= G).
   const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
   auto load_qb = [&](int j) {
-    u32x4 u = *(const u32x4*)(qrow + QW * q4 + 8 * j);
+    u32x4 u = *(const u32x4*)(qrow + kchan(j));
     if (r >= G) u = u32x4{0, 0, 0, 0};
     return __builtin_bit_cast(bf16x8, u);
   };
@@ -102,7 +106,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     for (int i = 0; i < 8; ++i) {
       float qf = (float)qb[j][i];
       if (kconst) {
-        const int64_t ci = (int64_t)h * a.ks_sh + QW * q4 + 8 * j + i;
+        const int64_t ci = (int64_t)h * a.ks_sh + kchan(j) + i;
         qf *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
       }
       qh[j][i] = (_Float16)qf;
@@ -140,7 +144,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       const int8_t* kb = kh + blk * a.kv_sn;
       const int8_t* vb = vh + blk * a.kv_sn;
 #pragma unroll
-      for (int j = 0; j < KL; ++j) tl.k[mt][j] = __builtin_nontemporal_load((const u32x4*)(kb + r * D + QW * q4 + 16 * j));
+      for (int j = 0; j < KL; ++j)
+        tl.k[mt][j] = __builtin_nontemporal_load((const u32x4*)(kb + r * D + 64 * j + 16 * q4));
 #pragma unroll
       for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
       if (MODE == 2)  // lane L holds channels 2L, 2L + 1 (lanes past D / 2 repeat the first half)
@@ -192,10 +197,10 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       if (MODE >= 2 && tail >= 0 && tb == n_quant && tb < end) {
         // The sequence's partial last block: bf16 K from its staging slot, exact bf16 products.
         const uint16_t* st = (const uint16_t*)a.stage + (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn +
-                             (int64_t)r * a.st_sb + QW * q4;
+                             (int64_t)r * a.st_sb;
 #pragma unroll
         for (int j = 0; j < KS; ++j)
-          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4*)(st + 8 * j)),
+          sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4*)(st + kchan(j))),
                                                            load_qb(j), sc[mt], 0, 0, 0);  // reloaded: rare
         continue;
       }
@@ -212,7 +217,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
           // Q' = q * s with the block's fp16 channel scales s, as an exact high part plus a low part: s_hi keeps
           // the top 3 significant bits of s (sign, exponent, 2 mantissa bits), so q * s_hi (8 x 3 bits) is exact
           // in fp16; s_lo = s - s_hi is exact and q * s_lo is rounded relative to that small remainder only.
-          const u32x4 cw = *(const u32x4*)(kcw + 64 * mt + (QW * q4 + 8 * j) / 2);
+          const u32x4 cw = *(const u32x4*)(kcw + 64 * mt + kchan(j) / 2);
           const f16x8 s_all = __builtin_bit_cast(f16x8, cw);
           const f16x8 s_hi = __builtin_bit_cast(f16x8, cw & 0xff00ff00u);
           const f16x8 q_hi = qh[j] * s_hi;
