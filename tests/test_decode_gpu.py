@@ -67,6 +67,14 @@ def test_single_sequence_lengths(n, impl):
         run([n], "0.5B", 16, torch.bfloat16, splits, impl=impl)
 
 
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_context_longer_than_one_split_holds(heads):
+    """A 40,000-token sequence asked for a single pass: a split stages at most 32,768 tokens of block ids, so the
+    library cuts it into two and the output still matches the oracle; on the split grid and the work list."""
+    run([40000, 5], heads, 16, torch.bfloat16, 1)
+    run([40000, 5], heads, 16, torch.bfloat16, None, work_list="on")
+
+
 @pytest.mark.parametrize("impl", ["mfma", "valu"])
 def test_more_splits_than_tokens(impl):
     """Splits past a short sequence's end contribute nothing (reference tests/test_decode_kernel.py:84-86)."""

@@ -320,6 +320,24 @@ def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
         assert err32 <= 8e-3, f"fp32 max-abs {err32:.3e}"
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_int8_context_longer_than_one_split_holds(fmt):
+    """The INT8 kernels stage the token scales of at most 4,096 tokens per split: a 9,000-token sequence asked
+    for a single pass is cut into three splits (and into pieces of at most 4,096 tokens on the work list)."""
+    Hq, Hkv, D = HEADS["1.5B"]
+    lengths = [9000, 17]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=8)
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    for splits, lists in ((1, {}), (None, dict(host_context_lens=lengths, work_list="on"))):
+        print(f"case {fmt} lengths {lengths} splits={splits} {lists.get('work_list', 'grid')}", flush=True)
+        out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                     max(lengths), num_splits=splits, quant=quant, impl="mfma", **lists)
+        got = out.double().cpu().numpy()
+        beyond = bf16_error_beyond_rounding(got, ref)
+        assert beyond <= 8e-3, f"error beyond bf16 output rounding {beyond:.3e}"
+
+
 @pytest.mark.parametrize("heads", list(HEADS))
 @pytest.mark.parametrize("impl", ["mfma", "valu"])
 def test_int8_constant_channel_scales(heads, impl):
