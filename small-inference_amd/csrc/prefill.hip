@@ -37,6 +37,7 @@ struct PrefillArgs {
   void* out;
   int64_t o_st, o_sh;
   int32_t S, G, qtiles;   // qtiles = ceil(max new tokens / (16 tt))
+  int32_t npair;           // S * Hkv
   int32_t tt;              // 16-token subtiles per unit: G * tt <= 8 column tiles
   int32_t T, nb, max_ctx;  // rows of q / out, pool blocks, context clamp
   int32_t nsplit, chunk;   // key splits per unit, keys per split (a multiple of 64)
@@ -175,12 +176,13 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   __shared__ int last_flag;
 
   // Splits fastest: consecutive workgroups (which the dispatcher deals round-robin to the 8 XCDs) take the
-  // splits of one unit, so each XCD's L2 serves one key range to every query tile of a sequence.
+  // splits of one unit. Units go out last query tile first, over all (sequence, KV head) pairs: under the causal
+  // mask a unit's keys grow with its tile index, so the longest units start first and the short ones fill in.
   const int L = blockIdx.x;
   const int sp = L % a.nsplit;
   const int u = L / a.nsplit;
-  const int j = u % a.qtiles;
-  const int pair = u / a.qtiles;
+  const int pair = u % a.npair;
+  const int j = a.qtiles - 1 - u / a.npair;
   const int s = pair % a.S, h = pair / a.S;
   const int G = a.G, TT = a.tt, NT = 16 * a.tt;  // query heads, token subtiles, tokens per unit
   const int n = a.qlen[s];
@@ -616,6 +618,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.S = S;
   a.G = G;
   a.qtiles = qtiles;
+  a.npair = S * Hkv;
   a.tt = tt;
   a.T = p->num_tokens;
   a.nb = p->num_blocks;
