@@ -717,6 +717,8 @@ def main() -> int:
                     "graph replay")
     ap.add_argument("--c5", action="store_true", help="only run config C5 (decode steps of a random-init 0.5B "
                     "model at batch 512 through the paged cache) and print its JSON")
+    ap.add_argument("--c4", action="store_true", help="only run config C4 (INT8 decode, 1.5B shape, 64 x 4096: "
+                    "per-token, then per-channel K) for --steps calls each and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the probe library's plain copy kernel over MIB MiB, 10 times (the reference "
                          "point for rocprof's FETCH_SIZE / WRITE_SIZE counters), and print its byte count")
@@ -740,6 +742,15 @@ def main() -> int:
         return 0
     if args.graph:
         print(json.dumps(graph_step_bench()), flush=True)
+        return 0
+    if args.c4:
+        res = {}
+        for fmt, key in (("int8", "c4b_int8_per_token"), ("int8-kchannel", "c4a_int8_kchannel")):
+            wl = int8_decode(key, fmt, [4096] * 64, 32768)
+            res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
+            del wl
+            torch.cuda.empty_cache()
+        print(json.dumps(res), flush=True)
         return 0
     if args.c5:
         res = {}
