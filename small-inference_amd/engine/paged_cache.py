@@ -96,6 +96,12 @@ def build_metadata(manager: BlockManager, batch: list[tuple[int, int, int]],
     S = len(batch)
     if S == 0:
         raise ValueError("a forward needs at least one sequence")
+    # This package's BlockManager keeps an int32 mirror of every table; a manager with only the reference's
+    # block_table() list (engine/block_manager.py:106-108) works too, at the cost of one conversion per sequence.
+    table_of = getattr(manager, "table_array", None)
+    if table_of is None:
+        def table_of(seq_id: int) -> np.ndarray:
+            return np.asarray(manager.block_table(seq_id), dtype=np.int32)
     starts, lens, tables = [0], [], []
     positions: list[int] = []
     slot_list: list[int] = []
@@ -108,7 +114,7 @@ def build_metadata(manager: BlockManager, batch: list[tuple[int, int, int]],
             raise ValueError(f"sequence {seq_id} holds {held} tokens, forward needs {ctx}")
         if start < 0:
             raise ValueError(f"sequence {seq_id}: negative start {start}")
-        table = manager.table_array(seq_id)[:(ctx + B - 1) // B]
+        table = table_of(seq_id)[:(ctx + B - 1) // B]
         if n == 1:  # a decode row: one slot, no array work
             positions.append(start)
             slot_list.append(int(table[start // B]) * B + start % B)

@@ -355,6 +355,30 @@ def test_metadata_matches_oracle_on_random_batches(seed):
     assert meta.context_lens_t.dtype == meta.block_tables.dtype == torch.int32
 
 
+def test_metadata_from_a_manager_with_only_the_reference_api():
+    """build_metadata also takes a block manager that offers only the reference's API (block_table() lists,
+    seq_len(), block_size; engine/block_manager.py:106-113), as when the reference's own manager stays in place:
+    same metadata as from this package's manager with its int32 mirrors."""
+
+    class ReferenceApi:
+        def __init__(self, m):
+            self.block_size = m.block_size
+            self.block_table = m.block_table
+            self.seq_len = m.seq_len
+
+    m = fragmented(1024, 16, 3)
+    batch = [(0, 0, 37), (1, 100, 1), (2, 15, 2), (3, 0, 1)]
+    for s, start, n in batch:
+        m.allocate(s, start + n)
+    ours, ref_api = build_metadata(m, batch, "cpu"), build_metadata(ReferenceApi(m), batch, "cpu")
+    assert not hasattr(ReferenceApi(m), "table_array")
+    for key in ("query_starts", "context_lens", "positions", "slot_mapping", "slot_blocks", "slot_offsets",
+                "block_tables", "context_lens_t", "last_token_indices"):
+        a, b = getattr(ours, key), getattr(ref_api, key)
+        assert (torch.equal(a, b) if isinstance(a, torch.Tensor) else a == b), key
+    assert list(ours.block_ids_cpu) == list(ref_api.block_ids_cpu)
+
+
 def test_graph_runner_needs_a_gpu_kernel_cache():
     """Graph capture is for the HIP backend on a GPU pool: a CPU or gather cache is refused before any device
     allocation."""
