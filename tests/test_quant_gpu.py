@@ -145,9 +145,9 @@ def test_store_tokens_is_exact(dtype):
 
 # ---- INT8 caches: fused writes and decode ------------------------------------------------------------------------
 
-def make_cache(fmt, num_blocks, B, dtype, cfg):
+def make_cache(fmt, num_blocks, B, dtype, cfg, n_stage=32):
     m = BlockManager(num_blocks, B)
-    return m, QuantPagedKVCache(cfg, num_blocks, B, "cuda", dtype, "hip", fmt, m, n_stage=32)
+    return m, QuantPagedKVCache(cfg, num_blocks, B, "cuda", dtype, "hip", fmt, m, n_stage=n_stage)
 
 
 def write_chunks(m, cache, seq, k, v, chunks, layer=0):
@@ -240,9 +240,12 @@ def test_kernel_matches_dequantized_reference(dtype, fmt, heads, B, splits):
 
 def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False):
     """INT8 pools built by the HIP quantizers (through the cache), outlier channels in K, and the oracle's fp32
-    dequantized K/V per sequence. Returns (q, cache, meta, k32 list, v32 list)."""
+    dequantized K/V per sequence. Returns (q, cache, meta, k32 list, v32 list). The closing step re-writes every
+    sequence's last token, so format B stages one block per sequence: twice as many staging slots as sequences
+    (the reference engine's n_stage = 2 max_num_seqs)."""
     B = 16
-    m, cache = make_cache(fmt, sum(-(-n // B) for n in lengths) * 2, B, torch.bfloat16, tiny_cfg(Hq, Hkv, D))
+    m, cache = make_cache(fmt, sum(-(-n // B) for n in lengths) * 2, B, torch.bfloat16, tiny_cfg(Hq, Hkv, D),
+                          n_stage=max(32, 2 * len(lengths)))
     g = torch.Generator().manual_seed(seed)
     outlier = torch.ones(Hkv, D)
     for h in range(Hkv):
