@@ -120,15 +120,23 @@ const char* sipa_last_error(void);
 int32_t sipa_device_cu_count(int32_t device);
 
 /*
- * Splits per sequence for a call. Replaces the reference's 20-SM policy choose_splits (reference
- * engine/triton_decode.py:164-172) with one sized from the CU count: about one (sequence, KV head, split)
- * workgroup per CU, ceil(cu_count / (num_seqs * num_kv_heads)) splits, but no split under 256 tokens of
- * max_context and none over 2048 (so a long sequence in a ragged batch is spread over many CUs).
+ * Splits per sequence for a call over bf16/fp32 pools. Replaces the reference's 20-SM policy choose_splits
+ * (reference engine/triton_decode.py:164-172) with one sized from the CU count: at most one (sequence, KV head,
+ * split) workgroup per CU, ceil(cu_count / (num_seqs * num_kv_heads)) splits, but no split under 512 tokens of
+ * max_context past 8 splits (short contexts: up to 8 splits of at least 128 tokens), and none over 2048 (so a
+ * long sequence in a full grid is spread over several CUs).
  */
 int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count);
-/* sipa_decode with num_splits <= 0 applies it with cu_count = the device's CUs for bf16/fp32 pools and twice
- * that for INT8 pools, whose kernels run two workgroups per CU. INT8 pools also use at least
- * ceil(max_context / 4096) splits whatever num_splits asks (size the workspace for that count). */
+
+/*
+ * The split count sipa_decode uses when num_splits <= 0, for pools of kv_mode (SIPA_KV_*): sipa_choose_splits
+ * for bf16/fp32 pools; for INT8 pools, whose kernels run two workgroups per CU, twice the CUs, splits of at
+ * least 256 tokens, and at least ceil(max_context / 4096) (INT8 calls use that many whatever num_splits asks:
+ * size the workspace for the larger count). cu_count <= 0: the current device's. No counterpart in the
+ * reference (its one policy serves every mode).
+ */
+int32_t sipa_choose_splits_for(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t cu_count,
+                               int32_t kv_mode);
 
 /* Tokens per split for a call with num_splits splits: ceil(max_context / num_splits) rounded up to a multiple
  * of 64 tokens, at most 32768. Calls launch ceil(max_context / chunk) splits, which may be fewer than asked. */

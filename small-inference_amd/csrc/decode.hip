@@ -442,16 +442,24 @@ static WorkspaceLayout workspace_layout(int64_t S, int64_t Hq, int64_t Hkv, int6
 
 static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// About one workgroup per CU: each workgroup pays a fixed cost of two dependent memory round trips before its
+// At most one workgroup per CU: each workgroup pays a fixed cost of two dependent memory round trips before its
 // first tile and the split merge after its last, so a few long-running workgroups beat many short ones (measured
-// on MI355X, bf16 32 x 8192: 4 splits 27.9 us, 8 splits 29.2 us, 16 splits 44.6 us). Splits stay within
-// [kMinChunk, kMaxChunk] tokens; the cap spreads a long sequence of a ragged batch over several CUs.
-int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count) {
+// on MI355X, bf16 32 x 8192: 4 splits 27.9 us, 8 splits 29.2 us, 16 splits 44.6 us). A small batch does not fill
+// the chip either: past 8 splits every 8 more add a round trip to the merge, so splits stay at 512 tokens or more
+// unless a short context fits 8 splits of at least 128 (bf16, 2 KV heads: 1 x 1024 best at 8 splits, 6.3 us
+// against 6.9 at 4; 1 x 8192 at 16, 9.8 against 10.3 at 32; 4 x 8192 at 16, 10.9 against 12.8 at 32; 8 x 4096
+// at 8, 10.4 against 11.5 at 16). The INT8 kernels, two workgroups per CU, keep splits of 256 tokens and more
+// (1 x 4096: 9.8 us at 16 splits against 11.6 at 8). kMaxChunk spreads a long sequence of a full grid over several
+// CUs.
+int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count, bool int8) {
   if (S <= 0 || Hkv <= 0 || max_ctx <= 0) return 1;
   if (cu_count <= 0) cu_count = 256;
   const int64_t programs = (int64_t)S * Hkv;
   int64_t splits = (cu_count + programs - 1) / programs;
-  splits = std::min<int64_t>(splits, ceil_div(max_ctx, kMinChunk));
+  const int64_t most = int8 ? ceil_div(max_ctx, kMinChunk)
+                            : std::max<int64_t>(ceil_div(max_ctx, kLatencyChunk),
+                                                std::min<int64_t>(kShortSplits, ceil_div(max_ctx, kShortChunk)));
+  splits = std::min<int64_t>(splits, most);
   splits = std::max<int64_t>(splits, ceil_div(max_ctx, kMaxChunk));
   return (int)std::max<int64_t>(1, std::min<int64_t>(splits, 1 << 20));
 }
@@ -535,18 +543,27 @@ using namespace sipa;
 
 extern "C" int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context,
                                       int32_t cu_count) {
-  return choose_splits_host(num_seqs, num_kv_heads, max_context, cu_count);
+  return choose_splits_host(num_seqs, num_kv_heads, max_context, cu_count, false);
 }
 
 extern "C" int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits) {
   return split_chunk_host(max_context, num_splits);
 }
 
-// wgs_per_cu: workgroups of the chosen kernel that run on one CU at once (the INT8 kernels fit two); int8: the
-// INT8 kernels' splits are at most kMaxInt8Split tokens (more splits than requested if need be).
-static int resolve_splits(int S, int Hkv, int max_ctx, int requested, int wgs_per_cu, bool int8, int* chunk) {
+// The INT8 kernels run two workgroups per CU and stage at most kMaxInt8Split tokens of scales per split.
+extern "C" int32_t sipa_choose_splits_for(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context,
+                                          int32_t cu_count, int32_t kv_mode) {
+  const bool int8 = kv_mode != SIPA_KV_PLAIN;
+  const int cu = cu_count > 0 ? cu_count : sipa_device_cu_count(-1);
+  int splits = choose_splits_host(num_seqs, num_kv_heads, max_context, (int8 ? 2 : 1) * cu, int8);
+  if (int8 && max_context > 0) splits = std::max(splits, ceil_div(max_context, kMaxInt8Split));
+  return splits;
+}
+
+// int8: the INT8 kernels' splits are at most kMaxInt8Split tokens (more splits than requested if need be).
+static int resolve_splits(int S, int Hkv, int max_ctx, int requested, bool int8, int* chunk) {
   int splits = requested;
-  if (splits <= 0) splits = choose_splits_host(S, Hkv, max_ctx, wgs_per_cu * sipa_device_cu_count(-1));
+  if (splits <= 0) splits = sipa_choose_splits_for(S, Hkv, max_ctx, 0, int8 ? SIPA_KV_INT8_TOKEN : SIPA_KV_PLAIN);
   if (int8) splits = std::max(splits, ceil_div(max_ctx, kMaxInt8Split));
   *chunk = split_chunk_host(max_ctx, splits);
   return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
@@ -651,8 +668,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
     SIPA_CHECK(p->num_splits >= 1, SIPA_EINVAL, "with a work list, num_splits must be its largest split count");
     splits = p->num_splits;
   } else {
-    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, mode == SIPA_KV_PLAIN ? 1 : 2,
-                            mode != SIPA_KV_PLAIN, &chunk);
+    splits = resolve_splits(S, Hkv, p->max_context, p->num_splits, mode != SIPA_KV_PLAIN, &chunk);
   }
   SIPA_CHECK((int64_t)(Hq / Hkv) * splits * D * 4 < INT32_MAX, SIPA_EUNSUPPORTED,
              "%d splits: a KV head's partial rows exceed 2 GiB", splits);

@@ -20,6 +20,9 @@ constexpr int kMaxGroup = 16;      // query heads per KV head the kernels accept
 constexpr int kChunkAlign = 64;    // split chunks are multiples of 64 tokens (the reference's TILE)
 constexpr int kMinChunk = 256;     // smallest split the CU-count policy makes
 constexpr int kMaxChunk = 2048;    // largest split the policy makes when the grid is already full
+constexpr int kLatencyChunk = 512;  // smallest split of a small batch past kShortSplits splits
+constexpr int kShortChunk = 128;    // smallest split of a short context ...
+constexpr int kShortSplits = 8;     // ... cut into at most this many (one merge round)
 // Split workspaces (decode and prefill) keep their merge counters in a fixed region at the start, which no call
 // writes partials into: every call leaves the counters it used at zero, so one zero-filled workspace serves calls
 // of any size, decode and prefill alike, in any order on one stream.

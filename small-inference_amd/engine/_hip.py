@@ -73,6 +73,7 @@ SIGNATURES = {
     "sipa_last_error": (_c.c_char_p, []),
     "sipa_device_cu_count": (i32, [i32]),
     "sipa_choose_splits": (i32, [i32, i32, i32, i32]),
+    "sipa_choose_splits_for": (i32, [i32, i32, i32, i32, i32]),
     "sipa_split_chunk": (i32, [i32, i32]),
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),

@@ -61,7 +61,8 @@ def device_cu_count(device: torch.device | int | None = None) -> int:
 
 
 def choose_splits(num_seqs: int, num_kv_heads: int, max_context: int, cu_count: int | None = None) -> int:
-    """Splits per sequence for a call: about one workgroup per CU, splits of 256 to 2048 tokens."""
+    """Splits per sequence for a bf16/fp32 call: at most one workgroup per CU, splits of at most 2048 tokens and
+    at least 512 past 8 splits (short contexts: up to 8 splits of at least 128 tokens)."""
     cu = device_cu_count() if cu_count is None else cu_count
     return int(_hip.lib().sipa_choose_splits(num_seqs, num_kv_heads, max_context, cu))
 
@@ -164,9 +165,9 @@ class DecodePlan:
             self.requested = self.splits = max_splits
             self.chunk = None
         else:
-            # The INT8 kernels run two workgroups per CU: size their grid for twice the CUs.
-            wgs_per_cu = 1 if quant is None else 2
-            self.requested = num_splits or choose_splits(S, Hkv, max_context, wgs_per_cu * device_cu_count(q.device))
+            # The library's policy for this kernel family (the INT8 kernels run two workgroups per CU).
+            self.requested = num_splits or int(self.lib.sipa_choose_splits_for(
+                S, Hkv, max_context, device_cu_count(q.device), self.quant_mode))
             if quant is not None:  # the library splits INT8 work into pieces of at most INT8_MAX_SPLIT tokens
                 self.requested = max(self.requested, math.ceil(max_context / INT8_MAX_SPLIT))
             self.splits, self.chunk = split_plan(max_context, self.requested)

@@ -83,19 +83,30 @@ def test_store_entry_points_reject_bad_arguments():
 
 
 def test_split_policy_host_side():
-    """CU-count split policy: about one workgroup per CU, splits of 256..2048 tokens (64-token multiples); a
-    grid that is already full is not split unless a sequence is longer than 2048 tokens."""
+    """CU-count split policy: at most one workgroup per CU; splits of at most 2048 tokens (64-token multiples) and,
+    past 8 splits, at least 512 (short contexts: up to 8 splits of at least 128); a grid that is already full is
+    not split unless a sequence is longer than 2048 tokens. The INT8 policy sizes for two workgroups per CU,
+    splits of at least 256 tokens and at most 4096."""
     lib = _hip.lib()
-    for S, Hkv, ctx in [(1, 2, 8192), (32, 2, 8192), (256, 2, 8192), (64, 2, 4096), (1, 2, 1024), (512, 2, 300)]:
+    for S, Hkv, ctx in [(1, 2, 8192), (32, 2, 8192), (256, 2, 8192), (64, 2, 4096), (1, 2, 1024), (512, 2, 300),
+                        (1, 2, 16384), (8, 2, 4096)]:
         req = lib.sipa_choose_splits(S, Hkv, ctx, 256)
         chunk = lib.sipa_split_chunk(ctx, req)
         launched = -(-ctx // chunk)
         assert chunk % 64 == 0 and chunk <= 2048
-        assert S * Hkv * launched >= min(256, S * Hkv * -(-ctx // 256)), (S, Hkv, ctx, req, chunk)
-    assert lib.sipa_choose_splits(32, 2, 8192, 256) == 4
+        assert S * Hkv * launched <= max(256, S * Hkv * -(-ctx // 2048)), (S, Hkv, ctx, req, chunk)
+        assert launched <= 8 or chunk >= 512, (S, Hkv, ctx, req, chunk)
+        assert lib.sipa_choose_splits_for(S, Hkv, ctx, 256, 0) == req
+    # the measured optima of the policy's comment (bf16, 2 KV heads)
+    for S, ctx, want in [(1, 1024, 8), (1, 8192, 16), (1, 16384, 32), (4, 8192, 16), (8, 4096, 8), (16, 2048, 8),
+                         (32, 8192, 4), (256, 8192, 4), (512, 300, 1)]:
+        assert lib.sipa_choose_splits(S, 2, ctx, 256) == want, (S, ctx)
     assert lib.sipa_split_chunk(8192, 4) == 2048
-    assert lib.sipa_choose_splits(256, 2, 8192, 256) == 4      # long sequences still split at 2048 tokens
-    assert lib.sipa_choose_splits(512, 2, 300, 256) == 1
+    # INT8: twice the CUs, 256-token floor, 4096-token ceiling
+    assert lib.sipa_choose_splits_for(1, 2, 4096, 256, 1) == 16
+    assert lib.sipa_choose_splits_for(64, 2, 4096, 256, 1) == 4
+    assert lib.sipa_choose_splits_for(128, 2, 9000, 256, 2) == 5    # a full grid: splits of at most 2048 tokens
+    assert lib.sipa_choose_splits_for(1, 2, 9000, 256, 2) == 36     # 256-token splits (2 x 256 CUs / 2 programs)
     assert lib.sipa_decode_workspace_bytes(32, 14, 2, 64, 1) == 0
 
 
