@@ -131,7 +131,7 @@ int32_t sipa_choose_splits(int32_t num_seqs, int32_t num_kv_heads, int32_t max_c
 /*
  * The split count sipa_decode uses when num_splits <= 0, for pools of kv_mode (SIPA_KV_*): sipa_choose_splits
  * for bf16/fp32 pools; for INT8 pools, whose kernels run two workgroups per CU, twice the CUs, splits of at
- * least 256 tokens, and at least ceil(max_context / 4096) (INT8 calls use that many whatever num_splits asks:
+ * least 256 tokens past 8 splits, and at least ceil(max_context / 4096) (INT8 calls use that many whatever num_splits asks:
  * size the workspace for the larger count). cu_count <= 0: the current device's. No counterpart in the
  * reference (its one policy serves every mode).
  */

@@ -448,17 +448,16 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // the chip either: past 8 splits every 8 more add a round trip to the merge, so splits stay at 512 tokens or more
 // unless a short context fits 8 splits of at least 128 (bf16, 2 KV heads: 1 x 1024 best at 8 splits, 6.3 us
 // against 6.9 at 4; 1 x 8192 at 16, 9.8 against 10.3 at 32; 4 x 8192 at 16, 10.9 against 12.8 at 32; 8 x 4096
-// at 8, 10.4 against 11.5 at 16). The INT8 kernels, two workgroups per CU, keep splits of 256 tokens and more
-// (1 x 4096: 9.8 us at 16 splits against 11.6 at 8). kMaxChunk spreads a long sequence of a full grid over several
-// CUs.
+// at 8, 10.4 against 11.5 at 16). The INT8 kernels, two workgroups per CU, take splits down to 256 tokens past 8
+// splits (1 x 4096: 9.8 us at 16 splits against 11.6 at 8; 1 x 1024: 7.6 us at 8 against 8.6 at 4). kMaxChunk
+// spreads a long sequence of a full grid over several CUs.
 int choose_splits_host(int S, int Hkv, int max_ctx, int cu_count, bool int8) {
   if (S <= 0 || Hkv <= 0 || max_ctx <= 0) return 1;
   if (cu_count <= 0) cu_count = 256;
   const int64_t programs = (int64_t)S * Hkv;
   int64_t splits = (cu_count + programs - 1) / programs;
-  const int64_t most = int8 ? ceil_div(max_ctx, kMinChunk)
-                            : std::max<int64_t>(ceil_div(max_ctx, kLatencyChunk),
-                                                std::min<int64_t>(kShortSplits, ceil_div(max_ctx, kShortChunk)));
+  const int64_t most = std::max<int64_t>(ceil_div(max_ctx, int8 ? kMinChunk : kLatencyChunk),
+                                         std::min<int64_t>(kShortSplits, ceil_div(max_ctx, kShortChunk)));
   splits = std::min<int64_t>(splits, most);
   splits = std::max<int64_t>(splits, ceil_div(max_ctx, kMaxChunk));
   return (int)std::max<int64_t>(1, std::min<int64_t>(splits, 1 << 20));

@@ -86,7 +86,7 @@ def test_split_policy_host_side():
     """CU-count split policy: at most one workgroup per CU; splits of at most 2048 tokens (64-token multiples) and,
     past 8 splits, at least 512 (short contexts: up to 8 splits of at least 128); a grid that is already full is
     not split unless a sequence is longer than 2048 tokens. The INT8 policy sizes for two workgroups per CU,
-    splits of at least 256 tokens and at most 4096."""
+    splits of at least 256 tokens past 8 splits and at most 4096."""
     lib = _hip.lib()
     for S, Hkv, ctx in [(1, 2, 8192), (32, 2, 8192), (256, 2, 8192), (64, 2, 4096), (1, 2, 1024), (512, 2, 300),
                         (1, 2, 16384), (8, 2, 4096)]:
@@ -104,6 +104,7 @@ def test_split_policy_host_side():
     assert lib.sipa_split_chunk(8192, 4) == 2048
     # INT8: twice the CUs, 256-token floor, 4096-token ceiling
     assert lib.sipa_choose_splits_for(1, 2, 4096, 256, 1) == 16
+    assert lib.sipa_choose_splits_for(1, 2, 1024, 256, 1) == 8      # short context: 8 splits of 128
     assert lib.sipa_choose_splits_for(64, 2, 4096, 256, 1) == 4
     assert lib.sipa_choose_splits_for(128, 2, 9000, 256, 2) == 5    # a full grid: splits of at most 2048 tokens
     assert lib.sipa_choose_splits_for(1, 2, 9000, 256, 2) == 36     # 256-token splits (2 x 256 CUs / 2 programs)
