@@ -218,9 +218,11 @@ int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int3
 /*
  * Work list for a ragged batch (no counterpart in the reference, whose grid is always (sequence, KV head,
  * split)): every (sequence, KV head) pair is cut into ceil(ctx / piece) splits of near-equal length, piece about
- * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, 256 .. max_piece; max_piece <= 0
+ * sum(ctx) * num_kv_heads / (cu_count * items_per_cu) tokens (a multiple of 64, at most max_piece; max_piece <= 0
  * means 32768, and INT8 pools need max_piece <= 4096), and the items are ordered longest first, so the longest
- * work starts first and consecutive workgroups spread over the XCDs.
+ * work starts first and consecutive workgroups spread over the XCDs. Pieces are at least 512 tokens (a small
+ * batch's long sequence is not cut into more merges than its streaming saves), or 256 when max_piece <= 4096:
+ * the INT8 kernels, two workgroups per CU, do better with the shorter pieces.
  * context_lens_host [num_seqs] (each >= 1) are the lengths the decode call will read. Writes at most capacity
  * items (8 int32 each) to items_out and the largest split count of a pair to *max_splits; returns the number of
  * items, or a negative SIPA_E* code (items_out may be NULL to ask for the count).
