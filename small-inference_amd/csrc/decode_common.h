@@ -167,8 +167,8 @@ __device__ __forceinline__ void combine_round(const DecodeArgs& a, __amdgpu_buff
 }
 
 // Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). One thread per
-// (query head, 4-channel quad), so all loads of a round are in flight together; 4 (nvalid <= 4) or 8 splits per
-// round, merged online, so the usual 2..8 splits cost one memory round trip. COHERENT: the partials were written
+// (query head, 4-channel quad), so all loads of a round are in flight together; 4 (nvalid <= 4), 8 (<= 8) or 16
+// splits per round, merged online, so up to 8 splits cost one memory round trip and 32 cost two. COHERENT: the partials were written
 // by other workgroups of this launch (the fused merge).
 template <int D, bool OUT_F32, bool COHERENT>
 __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
@@ -182,8 +182,11 @@ __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     if (nvalid <= 4) {
       combine_round<4, D, COHERENT>(a, rows, row0, g, c, 0, nvalid, M, den, num);
+    } else if (nvalid <= 8) {
+      combine_round<8, D, COHERENT>(a, rows, row0, g, c, 0, nvalid, M, den, num);
     } else {
-      for (int j0 = 0; j0 < nvalid; j0 += 8) combine_round<8, D, COHERENT>(a, rows, row0, g, c, j0, nvalid, M, den, num);
+      for (int j0 = 0; j0 < nvalid; j0 += 16)
+        combine_round<16, D, COHERENT>(a, rows, row0, g, c, j0, nvalid, M, den, num);
     }
     store_out4<OUT_F32>(a, s, h * G + g, 4 * c, num / den);
   }
