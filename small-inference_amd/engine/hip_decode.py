@@ -2,9 +2,10 @@
 engine/triton_decode.py (paged_decode_attention, choose_splits, QuantKV; reference :164-238).
 
 One query token per sequence, K/V read in place from the [Hkv, N, B, D] pool of one layer through the block
-tables. The split count comes from the GPU's CU count instead of the reference's 20-SM constants: about one
-(sequence, KV head, split) workgroup per CU, splits of 256 to 2048 tokens, so that long sequences in ragged
-batches spread over many CUs. A split past a sequence's end does no work; the last split workgroup of a
+tables. The split count comes from the GPU's CU count instead of the reference's 20-SM constants: at most one
+(sequence, KV head, split) workgroup per CU, splits of at most 2048 tokens (so that long sequences spread over
+several CUs) and, for small batches, not so short that the merge's round trips outweigh the streaming they save
+(the library's sipa_choose_splits_for). A split past a sequence's end does no work; the last split workgroup of a
 (sequence, KV head) to finish merges the partials (combine="fused"), or a second kernel does (combine="kernel").
 
 Kernels: bf16 queries with 16-token blocks and head_dim 64/128 run the MFMA kernels (bf16 pools, and both INT8
