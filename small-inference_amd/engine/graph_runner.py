@@ -13,8 +13,11 @@ block manager.
 
 The cache keeps its begin / write / attend interface: the runner hands it PagedMetadata whose device fields are
 views of the persistent buffers and whose host context lengths are max_context for every row, which is what fixes
-the decode grid. Pools of the model dtype and INT8 format "int8" (per-token scales) are supported; format
-"int8-kchannel" plans its staging writes on the host each forward and is not captured.
+the decode grid. Pools of the model dtype and both INT8 formats are supported. Format "int8-kchannel" keeps each
+sequence's partial last block of K in a bf16 staging slot; its per-step staging plan (slot per row, the block
+each row's slot is quantized into, the tail slot the decode reads) is kept by the cache's host bookkeeping as in
+an eager forward and uploaded with the step's other host data, and the captured write stages every row and
+quantizes every row's slot, into the row's block when the row completes it and into the scratch block otherwise.
 """
 
 from __future__ import annotations
@@ -47,8 +50,6 @@ class DecodeGraphRunner:
                  max_seqs: int | None = None):
         if not cache.on_gpu or cache.attn_backend not in ("hip", "triton"):
             raise ValueError("graph capture needs a GPU cache on the HIP backend")
-        if getattr(cache, "fmt", "int8") != "int8":
-            raise ValueError("format int8-kchannel plans staging writes per forward and cannot be captured")
         if max_batch < 1 or max_context < 1:
             raise ValueError("max_batch and max_context must be positive")
         self.model, self.cache, self.manager = model, cache, manager
@@ -77,6 +78,17 @@ class DecodeGraphRunner:
         self._ninfo = self._hinfo.numpy()
         self._dinfo = torch.empty(3 * n + 1, dtype=torch.int32, device=dev)
         self._copied = torch.cuda.Event()
+        self._kchannel = getattr(cache, "fmt", None) == "int8-kchannel"
+        self._plan = None
+        if self._kchannel:
+            # format B's staging plan: int64 stage slots, quantization sources, quantization destinations
+            # [3n] and int32 tail slots [n], one pinned copy each; rows 0 .. n - 1 are the stage writes' sources
+            self._hplan = torch.empty(3 * n, dtype=torch.int64, pin_memory=True)
+            self._htail = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            self._dplan = torch.zeros(3 * n, dtype=torch.int64, device=dev)
+            self._dtail = torch.zeros(n, dtype=torch.int32, device=dev)
+            self._plan = (torch.arange(n, dtype=torch.int64, device=dev), self._dplan[:n], self._dplan[n:2 * n],
+                          self._dplan[2 * n:], self._dtail)
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self._pool = None
         self._stream = torch.cuda.Stream(device=dev)  # capture stream (default priority)
@@ -118,6 +130,8 @@ class DecodeGraphRunner:
         info[bucket + b:2 * bucket] = 0
         info[2 * bucket:3 * bucket + 1] = np.arange(bucket + 1)
         self._dinfo[:3 * bucket + 1].copy_(self._hinfo[:3 * bucket + 1], non_blocking=True)
+        if self._kchannel:
+            self._stage_plan(seq_ids, lens, bucket)
         self._copied.record()
         self.tables.sync()
         ids, pos, slots, blocks, offs, last, bt, ctx = self._views(bucket)
@@ -126,6 +140,23 @@ class DecodeGraphRunner:
             p(self.tables.table), self.tables.table.stride(0), self.tables.max_seqs, self.tables.max_blocks,
             p(self._dinfo), bucket, bucket, self.B, self.width, p(pos), p(slots), p(blocks), p(offs), p(last),
             p(bt), p(ctx), _hip.stream_of(self._d64)), "graph runner metadata")
+
+    def _stage_plan(self, seq_ids: list[int], lens: np.ndarray, bucket: int) -> None:
+        """Format B: the step's staging plan from the cache's slot bookkeeping (row i writes position lens[i] - 1
+        of its sequence; padding rows write offset 0 of the scratch block, whose staging slot stays held),
+        uploaded into the persistent plan buffers."""
+        B, m, n = self.B, self.manager, self.max_batch
+        blocks = [int(m.table_array(s)[(int(L) - 1) // B]) for s, L in zip(seq_ids, lens)]
+        offsets = [(int(L) - 1) % B for L in lens]
+        scratch = int(m.table_array(SCRATCH_SEQ)[0])
+        pad = bucket - len(seq_ids)
+        slots, src, dst, tails = self.cache.plan_static_decode(blocks + [scratch] * pad, offsets + [0] * pad,
+                                                               scratch)
+        h = self._hplan.numpy()
+        h[:bucket], h[n:n + bucket], h[2 * n:2 * n + bucket] = slots, src, dst
+        self._htail.numpy()[:bucket] = tails
+        self._dplan.copy_(self._hplan, non_blocking=True)
+        self._dtail.copy_(self._htail, non_blocking=True)
 
     # ---- capture and replay -------------------------------------------------------------------------------------
 
@@ -137,7 +168,13 @@ class DecodeGraphRunner:
 
     def _forward(self, bucket: int) -> torch.Tensor:
         ids, pos = self._views(bucket)[:2]
-        return self.model.forward(ids, pos, self.cache, self._meta(bucket))
+        if self._plan is None:
+            return self.model.forward(ids, pos, self.cache, self._meta(bucket))
+        self.cache.use_static_plan(self._plan)  # only this forward's begin() takes the persistent plan
+        try:
+            return self.model.forward(ids, pos, self.cache, self._meta(bucket))
+        finally:
+            self.cache.use_static_plan(None)
 
     def capture(self, bucket: int) -> None:
         """Record the decode step of `bucket` rows (one eager warm-up step on the capture stream first, which

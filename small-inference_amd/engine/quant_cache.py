@@ -55,6 +55,7 @@ class QuantPagedKVCache(PagedKVCache):
         super().__init__(cfg, num_blocks, block_size, device, dtype, attn_backend)
         self.fused_writes = self.on_gpu  # HIP quantize-and-store on GPU pools; torch quantizer otherwise
         self._staged = self._done = self._direct = None
+        self._static = None  # format B's staging plan in persistent buffers (graph-replayed decode steps)
         if fmt == "int8-kchannel":
             if manager is None:
                 raise ValueError("int8-kchannel needs the BlockManager to track partial blocks")
@@ -81,10 +82,53 @@ class QuantPagedKVCache(PagedKVCache):
             if slot is not None:
                 self._free_stage.append(slot)
 
+    def use_static_plan(self, buffers: tuple | None) -> None:
+        """For decode steps replayed from graphs (engine/graph_runner.py): begin() binds format B's staging plan to
+        persistent device buffers (rows int64 [n] = 0 .. n - 1, stage slots, done sources, done destinations, all
+        int64 [n], and tail slots int32 [n]), which the caller fills from plan_static_decode() before each step,
+        instead of building it per forward. None returns to per-forward plans."""
+        self._static = buffers
+
+    def plan_static_decode(self, blocks: list[int], offsets: list[int],
+                           scratch_block: int) -> tuple[list[int], list[int], list[int], list[int]]:
+        """Host side of a fixed-shape decode step whose row i writes one token at (blocks[i], offsets[i]): per row
+        its block's staging slot (allocated on the block's first staged token), the slot and block of the
+        block quantization (the row writing a block's last token quantizes it from its slot into the block and
+        gives the slot back; every other row's quantization goes to scratch_block, which only padding rows read),
+        and its tail slot (-1 once the block is full). Same slots and values as begin() plans for the same rows."""
+        B = self.block_size
+        slots, src, dst, tails, done = [], [], [], [], []
+        for b, off in zip(blocks, offsets):
+            slot = self._stage_of.get(b)
+            if slot is None:
+                if not self._free_stage:
+                    raise RuntimeError("out of INT8 staging slots; raise n_stage")
+                slot = self._stage_of[b] = self._free_stage.pop()
+            slots.append(slot)
+            src.append(slot)
+            if off == B - 1:
+                dst.append(b)
+                tails.append(-1)
+                done.append(b)
+            else:
+                dst.append(scratch_block)
+                tails.append(slot)
+        for b in done:
+            self._free_stage.append(self._stage_of.pop(b))
+        return slots, src, dst, tails
+
     def begin(self, n_tokens: int, meta: PagedMetadata | None) -> None:
         """Base bookkeeping, then (format B) the staging plan of every block this forward writes."""
         super().begin(n_tokens, meta)
         if self.fmt != "int8-kchannel":
+            return
+        if self._static is not None:  # a graph-replayed decode step: every row staged, every block quantized
+            rows, slots, src, dst, tails = self._static
+            T = meta.num_tokens
+            self._staged = (rows[:T], slots[:T], meta.slot_offsets)
+            self._done = (dst[:T], src[:T])
+            self._direct = None
+            self._tails = self._tails_dec = self._tails_pf = tails[:T]
             return
         B, dev = self.block_size, meta.positions.device
         rows_of: dict[int, list[tuple[int, int]]] = {}  # block -> [(token row, offset)] in token order

@@ -297,6 +297,61 @@ def test_staging_slots_follow_partial_blocks():
     assert cache._stage_of == {} and len(cache._free_stage) == cache.n_stage
 
 
+def test_static_decode_plan_matches_begin():
+    """Format B under the graph runner: the host plan of a decode step (plan_static_decode, with padding rows at
+    offset 0 of a scratch block that holds its own slot) hands out the staging slots, frees and tail slots that
+    begin() plans for the same rows, and the static begin path (every row staged, every row's slot quantized,
+    into the scratch block unless the row completes its block) leaves the pools as the per-forward plan does,
+    outside the scratch block and its slot."""
+    torch.manual_seed(4)
+    B, seqs = 4, [0, 1, 2, 3]
+    m, cache = make_quant_cache("int8-kchannel", num_blocks=64, B=B)
+    m.allocate(-1, 1)
+    scratch = m.block_table(-1)[0]
+    cache.plan_static_decode([scratch], [0], scratch)  # the runner's first plan: the scratch block's slot
+    scratch_slot = cache._stage_of[scratch]
+    for s, n in zip(seqs, [3, 6, 8, 1]):
+        write_chunks(m, cache, s, torch.randn(n, 2, 16), torch.randn(n, 2, 16), [n])
+    names = ("k", "k_scale", "v", "v_scale", "stage")
+    completed = 0
+    for step in range(7):
+        for s in seqs:
+            m.append_slot(s)
+        lens = [m.seq_len(s) for s in seqs]
+        k, v = torch.randn(6, 2, 16), torch.randn(6, 2, 16)
+        books = (dict(cache._stage_of), list(cache._free_stage))
+        pools = {n: getattr(cache, n).clone() for n in names}
+        cache.begin(4, build_metadata(m, [(s, L - 1, 1) for s, L in zip(seqs, lens)], "cpu"))
+        cache.write(0, k[:4], v[:4])
+        want_books, want_tails = (dict(cache._stage_of), list(cache._free_stage)), cache._tails.tolist()
+        want = {n: getattr(cache, n).clone() for n in names}
+        cache._stage_of.clear()
+        cache._stage_of.update(books[0])
+        cache._free_stage[:] = books[1]
+        for n in names:
+            getattr(cache, n).copy_(pools[n])
+        blocks = [m.block_table(s)[(L - 1) // B] for s, L in zip(seqs, lens)] + [scratch] * 2
+        offsets = [(L - 1) % B for L in lens] + [0, 0]
+        slots, src, dst, tails = cache.plan_static_decode(blocks, offsets, scratch)
+        assert (dict(cache._stage_of), list(cache._free_stage)) == want_books
+        assert tails == want_tails + [scratch_slot] * 2
+        completed += sum(o == B - 1 for o in offsets)
+        i64 = lambda xs: torch.tensor(xs, dtype=torch.int64)  # noqa: E731
+        cache.use_static_plan((torch.arange(6), i64(slots), i64(src), i64(dst), torch.tensor(tails, dtype=torch.int32)))
+        cache.begin(6, build_metadata(m, [(s, L - 1, 1) for s, L in zip(seqs, lens)] + [(-1, 0, 1)] * 2, "cpu"))
+        cache.use_static_plan(None)
+        cache.write(0, k, v)
+        assert cache._tails.tolist() == tails
+        keep = torch.ones(64, dtype=torch.bool)
+        keep[scratch] = False
+        for n in ("k", "k_scale", "v", "v_scale"):
+            assert torch.equal(getattr(cache, n)[:, :, keep], want[n][:, :, keep]), (step, n)
+        live = torch.ones(cache.n_stage, dtype=torch.bool)
+        live[scratch_slot] = False
+        assert torch.equal(cache.stage[:, :, live], want["stage"][:, :, live]), step
+    assert completed >= 4  # blocks completed (and new ones started) along the way
+
+
 def test_bytes_and_budget():
     ka = GOLDEN["budgets"]
     cfg = ModelConfig(**ka["qwen2_5_0_5b"])
