@@ -77,9 +77,10 @@ typedef struct sipa_decode_params {
   const void* k_cache;   /* [Hkv, N, B, D] */
   const void* v_cache;   /* [Hkv, N, B, D] */
   int64_t kv_stride_h, kv_stride_n; /* block rows are contiguous: offset stride D, channel stride 1 */
-  const int32_t* block_tables; /* [S, >= ceil(max_context / B)], padding never read */
+  const int32_t* block_tables; /* [S, >= ceil(max_context / B)]; entries past a sequence's context are loaded
+                                  but never used; ids are clamped to [0, num_blocks) */
   int64_t bt_stride_s;
-  const int32_t* context_lens; /* [S], each >= 1, the new token included */
+  const int32_t* context_lens; /* [S], each >= 1, the new token included; clamped to max_context */
   void* out;             /* [S, Hq, D] in q_dtype */
   int64_t out_stride_s, out_stride_h;
   /* SIPA_KV_INT8_TOKEN: k_scale, v_scale [Hkv, N, B].  SIPA_KV_INT8_KCHAN: k_scale [Hkv, N, D] (a zero block

@@ -76,11 +76,11 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
       qop[j] = __builtin_bit_cast(bf16x8, u);
     }
   }
-  const int ctx = a.ctx[s];
+  const int ctx = context_len(a, s);
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
   const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
-  commit_split_ids(nb_spec, ids, bids);
+  commit_split_ids(nb_spec, ids, bids, a.nb);
   __syncthreads();  // block ids staged
 
   const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
@@ -266,7 +266,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
 
   const WorkItem w = work_item(a);
   const int sp = w.sp, h = w.h, s = w.s;
-  const int ctx = a.ctx[s];
+  const int ctx = context_len(a, s);
   const int start = w.start;
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
@@ -302,7 +302,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
     for (int g = 0; g < kMaxGroup; ++g) sc[g] = 0.f;
     float vscale = 1.f;
     if (valid) {
-      blk = btr[t / B];
+      blk = min(max(btr[t / B], 0), a.nb - 1);
       off = t % B;
       const int64_t row = (int64_t)h * a.kv_sh + (int64_t)blk * a.kv_sn + (int64_t)off * D;
       const bool staged = (MODE == 2) && (t >= n_quant) && (tail >= 0);  // -1: no staging slot to read
@@ -417,7 +417,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
 template <int D, bool OUT_F32>
 __global__ void __launch_bounds__(kThreads) combine_splits(const DecodeArgs a) {
   const int h = blockIdx.x, s = blockIdx.y;
-  const int nvalid = (a.ctx[s] + a.chunk - 1) / a.chunk;
+  const int nvalid = (context_len(a, s) + a.chunk - 1) / a.chunk;
   if (nvalid <= 1) return;  // the single split wrote the output itself
   combine_group<D, OUT_F32, false>(a, s, h, nvalid);
 }
@@ -641,6 +641,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   SIPA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {16,32,64,128}", D);
   SIPA_CHECK(B > 0 && 64 % B == 0, SIPA_EINVAL, "block_size %d must divide 64 (block-aligned 64-token tiles)", B);
   SIPA_CHECK(p->max_context > 0, SIPA_EINVAL, "max_context %d must be >= 1", p->max_context);
+  SIPA_CHECK(p->num_blocks > 0, SIPA_EINVAL, "num_blocks %d must be >= 1", p->num_blocks);
   SIPA_CHECK(p->q_dtype == SIPA_F32 || p->q_dtype == SIPA_BF16, SIPA_EUNSUPPORTED, "q_dtype %d not f32/bf16",
              p->q_dtype);
   SIPA_CHECK(p->kv_mode >= 0 && p->kv_mode <= 2, SIPA_EINVAL, "kv_mode %d", p->kv_mode);
@@ -712,6 +713,7 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.splits = splits;
   a.chunk = chunk;
   a.max_ctx = p->max_context;
+  a.nb = p->num_blocks;
   a.items = n_items > 0 ? p->work_items : nullptr;
   a.fused = n_items > 0 || p->combine == SIPA_COMBINE_FUSED;  // a work list always merges in place
   a.scale_log2 = p->scale * 1.4426950408889634f;

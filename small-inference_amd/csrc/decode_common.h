@@ -316,13 +316,19 @@ __device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int s
   return nb_spec;
 }
 
-__device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[kIdsPerThread], int* bids) {
+// Ids outside the pool are clamped into it: a bad table gives wrong results, never an access out of bounds.
+__device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[kIdsPerThread], int* bids,
+                                                 int nblocks) {
 #pragma unroll
   for (int i = 0; i < kIdsPerThread; ++i) {
     const int j = threadIdx.x + kThreads * i;
-    if (j < nb_spec) bids[j] = ids[i];
+    if (j < nb_spec) bids[j] = min(max(ids[i], 0), nblocks - 1);
   }
 }
+
+// A sequence's context length as the kernels use it: at most max_context, so that the splits a sequence reports
+// (and the merge waits for) are always ones the launch has.
+__device__ __forceinline__ int context_len(const DecodeArgs& a, int s) { return min(a.ctx[s], a.max_ctx); }
 
 // MFMA epilogue: each wave's softmax state (m_run per lane for head g = r, l_run partial per lane, acc in the
 // O^T accumulator layout: lane (r, q4) holds head r, channels 16 dt + 4 q4 + i) goes to LDS; then thread

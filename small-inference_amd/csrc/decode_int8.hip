@@ -113,13 +113,13 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       ql[j][i] = (_Float16)(qf - (float)qh[j][i]);
     }
   }
-  const int ctx = a.ctx[s];
+  const int ctx = context_len(a, s);
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(wend, ctx));
   const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
   const int tail = (MODE >= 2) ? a.tail[s] : -1;       // staging slot of the partial last block, -1 if none
-  commit_split_ids(nb_spec, ids, bids);
+  commit_split_ids(nb_spec, ids, bids, a.nb);
   __syncthreads();
 
   const int8_t* kh = (const int8_t*)a.k + (int64_t)h * a.kv_sh;

@@ -90,7 +90,8 @@ struct DecodeArgs {
   float* pl;          // [S, Hq, splits] split softmax denominators
   int32_t* counters;  // [S, Hkv] splits finished, for the last-arriving merge
   int32_t S, Hq, Hkv, G, B, splits, chunk;
-  int32_t max_ctx;    // every block-table row covers ceil(max_ctx / B) blocks
+  int32_t max_ctx;    // every block-table row covers ceil(max_ctx / B) blocks; context lengths are clamped to it
+  int32_t nb;         // blocks in the pool: block ids are clamped to [0, nb)
   int32_t ks_f32, vs_f32;
   int32_t fused;      // 1: the last split workgroup of a (sequence, KV head) merges the splits
   float scale_log2;   // softmax scale * log2(e): scores are kept in the exp2 domain

@@ -141,6 +141,12 @@ class DecodePlan:
         _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens)
         if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
             raise ValueError("block_tables and context_lens must be int32")
+        # the kernels load every sequence's table entries up to max_context before they read its length
+        if block_tables.dim() != 2 or block_tables.shape[0] < S or block_tables.shape[1] * B < max_context:
+            raise ValueError(f"block_tables {tuple(block_tables.shape)} must hold {S} rows of at least "
+                             f"ceil({max_context} / {B}) entries")
+        if context_lens.numel() < S:
+            raise ValueError(f"context_lens holds {context_lens.numel()} lengths for {S} sequences")
         if impl not in _hip.IMPL or combine not in _hip.COMBINE:
             raise ValueError(f"impl {impl!r} / combine {combine!r}")
         self.shape, self.dtype, self.device = (S, Hq, D), q.dtype, q.device

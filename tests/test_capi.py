@@ -38,7 +38,7 @@ def bad_params(**over):
     p = _hip.DecodeParams()
     p.struct_size = ctypes.sizeof(_hip.DecodeParams)
     p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = 1, 14, 2, 64, 16
-    p.max_context, p.q_dtype, p.scale = 16, _hip.BF16, 0.125
+    p.max_context, p.num_blocks, p.q_dtype, p.scale = 16, 64, _hip.BF16, 0.125
     for ptr in ("q", "k_cache", "v_cache", "block_tables", "context_lens", "out"):
         setattr(p, ptr, 4096)
     for k, v in over.items():
@@ -53,6 +53,7 @@ def bad_params(**over):
     ({"head_dim": 96}, _hip.EUNSUPPORTED),
     ({"block_size": 12}, _hip.EINVAL),                  # must divide 64
     ({"max_context": 0}, _hip.EINVAL),
+    ({"num_blocks": 0}, _hip.EINVAL),
     ({"q_dtype": _hip.F16}, _hip.EUNSUPPORTED),
     ({"kv_mode": 1}, _hip.EINVAL),                      # INT8 without scales
     ({"k_cache": 4100}, _hip.EINVAL),                   # unaligned pool

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import HEADS, RAGGED, make_case, oracle_decode
+from cases import HEADS, RAGGED, bf16_error_beyond_rounding, make_case, oracle_decode
 from engine.hip_decode import choose_splits, paged_decode_attention, split_plan
 
 pytestmark = pytest.mark.gpu
@@ -179,3 +179,80 @@ def test_workspace_reuse_with_more_pairs():
     both split 4 ways; the second call's merge counters must not overlap the first call's partials."""
     run([3000, 2000], "0.5B", 16, torch.bfloat16, 4)
     run([600] * 300, "0.5B", 16, torch.bfloat16, 4, seed=1)
+
+
+def clamped_case(seed):
+    """A batch whose tables hold ids outside the pool (past N and negative): what the kernels read instead is
+    the clamped table (ids into [0, N))."""
+    Hq, Hkv, D = HEADS["0.5B"]
+    lengths = [700, 1500, 90]
+    q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=seed)
+    N = k.shape[1]
+    bad = bt.clone()
+    fixed = [list(t) for t in tables]
+    for s, j, b, c in ((0, 3, N + 5, N - 1), (1, 0, -7, 0), (1, 50, 1 << 30, N - 1), (2, 5, -1, 0)):
+        bad[s, j] = b
+        fixed[s][j] = c
+    return q, k, v, bad, ctx, fixed, lengths
+
+
+@pytest.mark.parametrize("impl,work_list,over", [("auto", "off", True), ("valu", "off", True),
+                                                 ("auto", "on", False)])
+def test_bad_ids_and_lengths_are_clamped(impl, work_list, over):
+    """Block ids outside the pool are clamped into it and context lengths to max_context, as the prefill kernel
+    does: the output is the clamped inputs' (every access stays in the pool), and the merge counters are back at
+    zero afterwards (a length past max_context would otherwise report splits the grid does not have), so the
+    next call on the same workspace is exact."""
+    q, k, v, bad, ctx, fixed, lengths = clamped_case(seed=21)
+    D, B, max_ctx = q.shape[2], k.shape[2], max(lengths)
+    want_lengths = list(lengths)
+    if over:  # sequence 2 reports 5500 tokens; the kernels read max_context of them, padding ids clamped to 0
+        ctx = ctx.clone()
+        ctx[2] = max_ctx + 4000
+        want_lengths[2] = max_ctx
+        fixed[2] = fixed[2] + [0] * (-(-max_ctx // B) - len(fixed[2]))
+    print(f"case clamp impl={impl} work_list={work_list} over={over}", flush=True)
+    kw = dict(impl=impl, host_context_lens=lengths, work_list=work_list)
+    if work_list == "off":
+        kw["num_splits"] = 3
+    out = paged_decode_attention(q, k, v, bad, ctx, D ** -0.5, max_ctx, **kw)
+    torch.cuda.synchronize()
+    ref = oracle_decode(q, k, v, fixed, want_lengths, D ** -0.5, np.float32)
+    assert np.abs(out.double().cpu().numpy() - ref).max() <= 8e-3
+    # the same workspace, valid inputs: exact against a plan whose counters were never touched by the bad call
+    q2, k2, v2, bt2, ctx2, tables2 = make_case(lengths, q.shape[1], k.shape[0], D, B, torch.bfloat16, seed=22)
+    again = paged_decode_attention(q2, k2, v2, bt2, ctx2, D ** -0.5, max_ctx, **kw)
+    torch.cuda.synchronize()
+    ref2 = oracle_decode(q2, k2, v2, tables2, lengths, D ** -0.5, np.float32)
+    assert np.abs(again.double().cpu().numpy() - ref2).max() <= 8e-3
+
+
+def test_int8_bad_ids_are_clamped():
+    """The INT8 kernel clamps block ids into the pool the same way (per-token scales)."""
+    from engine.hip_decode import QuantKV
+
+    q, k, v, bad, ctx, fixed, lengths = clamped_case(seed=23)
+    Hkv, N, B, D = k.shape
+    g = torch.Generator(device="cuda").manual_seed(23)
+    kq = torch.randint(-127, 128, (Hkv, N, B, D), device="cuda", dtype=torch.int8, generator=g)
+    vq = torch.randint(-127, 128, (Hkv, N, B, D), device="cuda", dtype=torch.int8, generator=g)
+    ks = (torch.rand(Hkv, N, B, device="cuda", generator=g) / 64 + 1 / 256).half()
+    vs = (torch.rand(Hkv, N, B, device="cuda", generator=g) / 64 + 1 / 256).half()
+    print("case clamp int8", flush=True)
+    out = paged_decode_attention(q, kq, vq, bad, ctx, D ** -0.5, max(lengths), num_splits=3,
+                                 quant=QuantKV(1, ks, vs))
+    torch.cuda.synchronize()
+    kf, vf = kq.float() * ks.float()[..., None], vq.float() * vs.float()[..., None]
+    ref = oracle_decode(q, kf, vf, fixed, lengths, D ** -0.5, np.float32)
+    assert bf16_error_beyond_rounding(out.double().cpu().numpy(), ref) <= 8e-3
+
+
+def test_table_narrower_than_max_context_is_refused():
+    """The kernels load table entries up to max_context for every sequence: a narrower table is refused on the
+    host, before any launch."""
+    Hq, Hkv, D = HEADS["0.5B"]
+    q, k, v, bt, ctx, tables = make_case([100, 300], Hq, Hkv, D, 16, torch.bfloat16, seed=5)
+    with pytest.raises(ValueError):
+        paged_decode_attention(q, k, v, bt[:, :10], ctx, D ** -0.5, 300)
+    with pytest.raises(ValueError):
+        paged_decode_attention(q, k, v, bt, ctx[:1], D ** -0.5, 300)
