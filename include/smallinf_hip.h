@@ -250,6 +250,13 @@ int32_t sipa_paged_metadata(const int32_t* tables, int64_t table_stride, int32_t
                             int32_t* context_lens, void* stream);
 
 /*
+ * The four store entry points below use their indices as given, as the reference's store kernels and index_put
+ * stores do with valid input: blocks and dst in [0, N), offsets in [0, B), src in [0, n_src), rows in [0, T).
+ * The caches derive them from the block manager's slots; a caller with indices of unknown origin checks them
+ * first (the decode and prefill kernels, which only read, clamp theirs instead).
+ */
+
+/*
  * Per-token INT8 quantize-and-store (reference engine/triton_quant.py:24-39,61-71 and the quantizer
  * engine/quant.py:22-31): for every (t, h),
  *   s = fp16(max_d |x[t,h,d]| / 127);  q[d] = s > 0 ? clamp(rint(x[t,h,d] / float(s)), -127, 127) : 0
