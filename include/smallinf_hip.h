@@ -250,7 +250,7 @@ int32_t sipa_paged_metadata(const int32_t* tables, int64_t table_stride, int32_t
                             int32_t* context_lens, void* stream);
 
 /*
- * The four store entry points below use their indices as given, as the reference's store kernels and index_put
+ * The five store entry points below use their indices as given, as the reference's store kernels and index_put
  * stores do with valid input: blocks and dst in [0, N), offsets in [0, B), src in [0, n_src), rows in [0, T).
  * The caches derive them from the block manager's slots; a caller with indices of unknown origin checks them
  * first (the decode and prefill kernels, which only read, clamp theirs instead).
@@ -270,6 +270,19 @@ int32_t sipa_quantize_store_tokens(const void* x, int32_t x_dtype, int64_t x_str
                                    const int64_t* offsets, int8_t* q_pool, int64_t q_stride_h,
                                    int64_t q_stride_n, int32_t B, void* s_pool, int64_t s_stride_h,
                                    int64_t s_stride_n, void* stream);
+
+/*
+ * Two sipa_quantize_store_tokens calls in one launch, with no reference counterpart (the reference's cache
+ * makes the two calls, engine/quant_cache.py:161-163): x -> (q_pool, s_pool) and x2 -> (q_pool2, s_pool2) at the
+ * same (blocks[t], offsets[t]), x2 with its own row and head strides, the second pools with the first's strides.
+ * For the per-token format's V and K of one layer. Results equal the two separate calls bit for bit.
+ */
+int32_t sipa_quantize_store_tokens_kv(const void* x, const void* x2, int32_t x_dtype, int64_t x_stride_t,
+                                      int64_t x_stride_h, int64_t x2_stride_t, int64_t x2_stride_h, int32_t T,
+                                      int32_t H, int32_t D, const int64_t* blocks, const int64_t* offsets,
+                                      int8_t* q_pool, int8_t* q_pool2, int64_t q_stride_h, int64_t q_stride_n,
+                                      int32_t B, void* s_pool, void* s_pool2, int64_t s_stride_h,
+                                      int64_t s_stride_n, void* stream);
 
 /*
  * Per-channel INT8 quantize-and-store of whole blocks (reference engine/triton_quant.py:42-58,74-84): for every

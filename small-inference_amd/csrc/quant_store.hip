@@ -36,6 +36,11 @@ struct QTokArgs {
   uint16_t* s;
   int64_t s_sh, s_sn;
   int32_t T, H, D, B, x_dtype;
+  // a second pair (grid row blockIdx.y == 1) at the same slots, pools with the first pair's strides
+  const void* x2;
+  int64_t x2_st, x2_sh;
+  int8_t* q2;
+  uint16_t* s2;
 };
 
 template <int EPL>  // channels per lane: D / 16
@@ -44,12 +49,14 @@ __global__ void __launch_bounds__(256) quantize_tokens_kernel(const QTokArgs a) 
   const int sub = threadIdx.x & 15;
   if (vec >= a.T * a.H) return;  // whole 16-lane groups leave together; shuffles stay inside a group
   const int t = vec / a.H, h = vec % a.H;
-  const int64_t xi = (int64_t)t * a.x_st + (int64_t)h * a.x_sh + sub * EPL;
+  const bool second = blockIdx.y != 0;
+  const void* xs = second ? a.x2 : a.x;
+  const int64_t xi = (int64_t)t * (second ? a.x2_st : a.x_st) + (int64_t)h * (second ? a.x2_sh : a.x_sh) + sub * EPL;
   float x[EPL];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    x[i] = load_as_f32(a.x, xi + i, a.x_dtype);
+    x[i] = load_as_f32(xs, xi + i, a.x_dtype);
     amax = fmaxf(amax, fabsf(x[i]));
   }
 #pragma unroll
@@ -57,10 +64,10 @@ __global__ void __launch_bounds__(256) quantize_tokens_kernel(const QTokArgs a) 
   const _Float16 sh = (_Float16)(amax / kQMax);
   const float s32 = (float)sh;
   const int64_t blk = a.blocks[t], off = a.offsets[t];
-  int8_t* qrow = a.q + (int64_t)h * a.q_sh + blk * a.q_sn + off * a.D + sub * EPL;
+  int8_t* qrow = (second ? a.q2 : a.q) + (int64_t)h * a.q_sh + blk * a.q_sn + off * a.D + sub * EPL;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) qrow[i] = quantize_code(x[i], s32);
-  if (sub == 0) a.s[(int64_t)h * a.s_sh + blk * a.s_sn + off] = __builtin_bit_cast(uint16_t, sh);
+  if (sub == 0) (second ? a.s2 : a.s)[(int64_t)h * a.s_sh + blk * a.s_sn + off] = __builtin_bit_cast(uint16_t, sh);
 }
 
 struct QBlkArgs {
@@ -141,20 +148,16 @@ static int check_launch(const char* what) {
 
 using namespace sipa;
 
-extern "C" int32_t sipa_quantize_store_tokens(const void* x, int32_t x_dtype, int64_t x_stride_t, int64_t x_stride_h,
-                                              int32_t T, int32_t H, int32_t D, const int64_t* blocks,
-                                              const int64_t* offsets, int8_t* q_pool, int64_t q_stride_h,
-                                              int64_t q_stride_n, int32_t B, void* s_pool, int64_t s_stride_h,
-                                              int64_t s_stride_n, void* stream) {
+static int quantize_tokens(const QTokArgs& a, void* stream) {
+  const int T = a.T, H = a.H, D = a.D;
   if (T == 0) return SIPA_OK;
   SIPA_CHECK(T > 0 && H > 0, SIPA_EINVAL, "T %d, H %d", T, H);
   SIPA_CHECK(D > 0 && D % 16 == 0 && D <= 256, SIPA_EUNSUPPORTED, "head_dim %d must be a multiple of 16 <= 256", D);
-  SIPA_CHECK(B > 0, SIPA_EINVAL, "block_size %d", B);
-  SIPA_CHECK(float_dtype(x_dtype), SIPA_EUNSUPPORTED, "x dtype %d", x_dtype);
-  SIPA_CHECK(x && blocks && offsets && q_pool && s_pool, SIPA_EINVAL, "NULL pointer");
-  QTokArgs a{x, x_stride_t, x_stride_h, blocks, offsets, q_pool, q_stride_h, q_stride_n,
-             (uint16_t*)s_pool, s_stride_h, s_stride_n, T, H, D, B, x_dtype};
-  const dim3 grid((unsigned)(((int64_t)T * H + 15) / 16));
+  SIPA_CHECK(a.B > 0, SIPA_EINVAL, "block_size %d", a.B);
+  SIPA_CHECK(float_dtype(a.x_dtype), SIPA_EUNSUPPORTED, "x dtype %d", a.x_dtype);
+  SIPA_CHECK(a.x && a.blocks && a.offsets && a.q && a.s, SIPA_EINVAL, "NULL pointer");
+  SIPA_CHECK(!a.x2 || (a.q2 && a.s2), SIPA_EINVAL, "the second pair needs both pools");
+  const dim3 grid((unsigned)(((int64_t)T * H + 15) / 16), a.x2 ? 2 : 1);
   hipStream_t st = (hipStream_t)stream;
   switch (D / 16) {
     case 1: hipLaunchKernelGGL(quantize_tokens_kernel<1>, grid, dim3(256), 0, st, a); break;
@@ -165,6 +168,30 @@ extern "C" int32_t sipa_quantize_store_tokens(const void* x, int32_t x_dtype, in
     default: return fail(SIPA_EUNSUPPORTED, "head_dim %d not in {16,32,64,128,256}", D);
   }
   return check_launch("quantize_store_tokens");
+}
+
+extern "C" int32_t sipa_quantize_store_tokens(const void* x, int32_t x_dtype, int64_t x_stride_t, int64_t x_stride_h,
+                                              int32_t T, int32_t H, int32_t D, const int64_t* blocks,
+                                              const int64_t* offsets, int8_t* q_pool, int64_t q_stride_h,
+                                              int64_t q_stride_n, int32_t B, void* s_pool, int64_t s_stride_h,
+                                              int64_t s_stride_n, void* stream) {
+  QTokArgs a{x, x_stride_t, x_stride_h, blocks, offsets, q_pool, q_stride_h, q_stride_n,
+             (uint16_t*)s_pool, s_stride_h, s_stride_n, T, H, D, B, x_dtype, nullptr, 0, 0, nullptr, nullptr};
+  return quantize_tokens(a, stream);
+}
+
+extern "C" int32_t sipa_quantize_store_tokens_kv(const void* x, const void* x2, int32_t x_dtype, int64_t x_stride_t,
+                                                 int64_t x_stride_h, int64_t x2_stride_t, int64_t x2_stride_h,
+                                                 int32_t T, int32_t H, int32_t D, const int64_t* blocks,
+                                                 const int64_t* offsets, int8_t* q_pool, int8_t* q_pool2,
+                                                 int64_t q_stride_h, int64_t q_stride_n, int32_t B, void* s_pool,
+                                                 void* s_pool2, int64_t s_stride_h, int64_t s_stride_n,
+                                                 void* stream) {
+  SIPA_CHECK(x2 != nullptr, SIPA_EINVAL, "NULL pointer");
+  QTokArgs a{x, x_stride_t, x_stride_h, blocks, offsets, q_pool, q_stride_h, q_stride_n,
+             (uint16_t*)s_pool, s_stride_h, s_stride_n, T, H, D, B, x_dtype,
+             x2, x2_stride_t, x2_stride_h, q_pool2, (uint16_t*)s_pool2};
+  return quantize_tokens(a, stream);
 }
 
 static int launch_blocks(const QBlkArgs& a, void* stream) {

@@ -84,6 +84,8 @@ SIGNATURES = {
     "sipa_prefill_workspace_bytes": (i64, [i32, i32, i32, i32, i32, i32, i32]),
     "sipa_quantize_store_tokens": (i32, [vp, i32, i64, i64, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, i64, i64,
                                          vp]),
+    "sipa_quantize_store_tokens_kv": (i32, [vp, vp, i32, i64, i64, i64, i64, i32, i32, i32, vp, vp, vp, vp, i64, i64,
+                                            i32, vp, vp, i64, i64, vp]),
     "sipa_quantize_store_blocks": (i32, [vp, i32, i64, i64, i64, vp, vp, i32, i32, i32, i32, vp, i64, i64, vp, i64,
                                          i64, vp]),
     "sipa_quantize_store_block_rows": (i32, [vp, i32, i64, i64, vp, vp, i32, i32, i32, i32, vp, i64, i64, vp, i64,

@@ -20,9 +20,11 @@ def _i64(t: torch.Tensor) -> torch.Tensor:
 
 
 def quantize_store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, q_pool: torch.Tensor,
-                          s_pool: torch.Tensor) -> None:
+                          s_pool: torch.Tensor, *, x2: torch.Tensor | None = None, q_pool2: torch.Tensor | None = None,
+                          s_pool2: torch.Tensor | None = None) -> None:
     """x [T, H, D] (rows may be strided; last dim contiguous) -> q_pool [H, N, B, D] int8 and s_pool [H, N, B]
-    fp16 at (blocks[t], offsets[t]). One launch."""
+    fp16 at (blocks[t], offsets[t]). With x2, q_pool2, s_pool2 (the other of K and V, same shapes) both pairs are
+    stored in the same launch, equal bit for bit to two calls. One launch."""
     T, H, D = x.shape
     if T == 0:
         return
@@ -31,6 +33,22 @@ def quantize_store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.
         raise ValueError("q_pool must be int8 and s_pool fp16")
     _hip.require_gpu(x, blocks, offsets, q_pool, s_pool)
     blocks, offsets = _i64(blocks), _i64(offsets)
+    if x2 is not None:
+        if q_pool2 is None or s_pool2 is None:
+            raise ValueError("x2 needs q_pool2 and s_pool2")
+        if x2.shape != x.shape or x2.dtype != x.dtype or x2.stride(-1) != 1:
+            raise ValueError("x2 must match x in shape and dtype, last dim contiguous")
+        if (q_pool2.shape, q_pool2.stride(), q_pool2.dtype) != (q_pool.shape, q_pool.stride(), q_pool.dtype) or \
+                (s_pool2.shape, s_pool2.stride(), s_pool2.dtype) != (s_pool.shape, s_pool.stride(), s_pool.dtype):
+            raise ValueError("the second pools must match the first in shape, strides and dtype")
+        _hip.require_gpu(x2, q_pool2, s_pool2)
+        rc = _hip.lib().sipa_quantize_store_tokens_kv(
+            x.data_ptr(), x2.data_ptr(), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), x2.stride(0),
+            x2.stride(1), T, H, D, blocks.data_ptr(), offsets.data_ptr(), q_pool.data_ptr(), q_pool2.data_ptr(),
+            q_pool.stride(0), q_pool.stride(1), q_pool.shape[2], s_pool.data_ptr(), s_pool2.data_ptr(),
+            s_pool.stride(0), s_pool.stride(1), _hip.stream_of(x))
+        _hip.check(rc, "quantize_store_tokens")
+        return
     rc = _hip.lib().sipa_quantize_store_tokens(
         x.data_ptr(), _hip.dtype_code(x.dtype), x.stride(0), x.stride(1), T, H, D, blocks.data_ptr(),
         offsets.data_ptr(), q_pool.data_ptr(), q_pool.stride(0), q_pool.stride(1), q_pool.shape[2],

@@ -210,10 +210,11 @@ class QuantPagedKVCache(PagedKVCache):
         from .hip_quant import quantize_store_block_rows, quantize_store_blocks, quantize_store_tokens, store_tokens
 
         m = self.meta
-        quantize_store_tokens(v, m.slot_blocks, m.slot_offsets, self.v[layer], self.v_scale[layer])
-        if self.fmt == "int8":
-            quantize_store_tokens(k, m.slot_blocks, m.slot_offsets, self.k[layer], self.k_scale[layer])
+        if self.fmt == "int8":  # V and K in one launch
+            quantize_store_tokens(v, m.slot_blocks, m.slot_offsets, self.v[layer], self.v_scale[layer],
+                                  x2=k, q_pool2=self.k[layer], s_pool2=self.k_scale[layer])
             return
+        quantize_store_tokens(v, m.slot_blocks, m.slot_offsets, self.v[layer], self.v_scale[layer])
         if self._staged is not None:
             rows, slots, offs = self._staged
             store_tokens(k, slots, offs, self.stage[layer], rows=rows)

@@ -51,6 +51,36 @@ def test_token_quantization_is_exact(dtype, D):
     assert np.array_equal(bits16(sp[:, blocks, offsets].t().cpu().numpy()), bits16(s_ref))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_token_quantization_of_k_and_v_in_one_launch(dtype, D):
+    """The two-pair launch (V and K views of one fused projection, different strides from the pools') stores
+    what two single calls store, bit for bit, and both equal the oracle."""
+    g = torch.Generator().manual_seed(1)
+    qkv = (torch.randn(41, 18, D, generator=g) * 3).to("cuda", dtype)  # [T, Hq + 2 Hkv, D]
+    k, v = qkv[:, 14:16], qkv[:, 16:18]
+    v[7, 0] = 0
+    N, B = 24, 16
+    blocks = torch.randperm(N, generator=g)[:3].repeat_interleave(B)[:41].cuda()
+    offsets = (torch.arange(41) % B).cuda()
+    pools = [torch.zeros(2, N, B, D, dtype=torch.int8, device="cuda") for _ in range(4)]
+    scales = [torch.zeros(2, N, B, dtype=torch.float16, device="cuda") for _ in range(4)]
+    print(f"case tokens kv {dtype} D={D}", flush=True)
+    quantize_store_tokens(v, blocks, offsets, pools[0], scales[0], x2=k, q_pool2=pools[1], s_pool2=scales[1])
+    quantize_store_tokens(v, blocks, offsets, pools[2], scales[2])
+    quantize_store_tokens(k, blocks, offsets, pools[3], scales[3])
+    torch.cuda.synchronize()
+    for a, b in ((0, 2), (1, 3)):
+        assert torch.equal(pools[a], pools[b]) and torch.equal(scales[a].view(torch.int16), scales[b].view(torch.int16))
+    for x, i in ((v, 0), (k, 1)):
+        q_ref, s_ref = paged_ref.quantize_per_token(as_np32(x))
+        assert np.array_equal(pools[i][:, blocks, offsets].transpose(0, 1).cpu().numpy(), q_ref)
+        assert np.array_equal(bits16(scales[i][:, blocks, offsets].t().cpu().numpy()), bits16(s_ref))
+    with pytest.raises(ValueError):  # a second pool of another shape
+        quantize_store_tokens(v, blocks, offsets, pools[0], scales[0], x2=k, q_pool2=pools[1][:1],
+                              s_pool2=scales[1])
+
+
 def test_token_quantization_edge_values():
     """Scales that round to zero or to fp16 subnormals, exact .5 ties of x / s, values at the +-127 edge, and
     absmax near fp16 rounding ties: codes and scales still equal the oracle's."""
