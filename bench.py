@@ -631,11 +631,12 @@ def decode_step_bench(steps: int = 5, warmup: int = 2, batch: int = 512, pool_fr
     return r
 
 
-def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed: int = 0) -> dict:
+def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed: int = 0, fmt: str = "bf16") -> dict:
     """Decode steps of a random-init Qwen2.5-0.5B-shaped model (24 layers) at small batches, contexts ~ U[512, 2048],
-    bf16 pool: the ordinary eager step (build_metadata, ~300 launches from Python) against the same step replayed
-    from a HIP graph (engine/graph_runner.py: one metadata copy, one replay). Wall time per step, synchronised
-    each step as a serving loop is (it needs the sampled tokens), host work included."""
+    pool in `fmt` (bf16, int8 or int8-kchannel): the ordinary eager step (build_metadata, ~300 launches from
+    Python) against the same step replayed from a HIP graph (engine/graph_runner.py: one metadata copy, one
+    replay). Wall time per step, synchronised each step as a serving loop is (it needs the sampled tokens), host
+    work included."""
     import random
     import time
 
@@ -644,6 +645,7 @@ def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed:
     from engine.graph_runner import DecodeGraphRunner
     from engine.model import Qwen2Model
     from engine.paged_cache import PagedKVCache, build_metadata
+    from engine.quant_cache import QuantPagedKVCache
 
     res = {}
     model = Qwen2Model(cfg, "cuda", torch.bfloat16, seed=seed, max_positions=4096)
@@ -652,9 +654,18 @@ def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed:
         rng = random.Random(seed + batch)
         m = BlockManager(N, B)
         rng.shuffle(m._free)
-        cache = PagedKVCache(cfg, N, B, "cuda", torch.bfloat16, attn_backend="triton")
-        cache.k.normal_()
-        cache.v.normal_()
+        if fmt == "bf16":
+            cache = PagedKVCache(cfg, N, B, "cuda", torch.bfloat16, attn_backend="triton")
+            cache.k.normal_()
+            cache.v.normal_()
+        else:
+            cache = QuantPagedKVCache(cfg, N, B, "cuda", torch.bfloat16, "triton", fmt, m, n_stage=2 * batch + 2)
+            cache.k.random_(-127, 128)
+            cache.v.random_(-127, 128)
+            cache.k_scale.fill_(1 / 64)
+            cache.v_scale.fill_(1 / 64)
+            if fmt == "int8-kchannel":
+                cache.stage.normal_()
         ctx = [rng.randint(512, 2048) for _ in range(batch)]
         for s, n in enumerate(ctx):
             m.allocate(s, n)
@@ -686,7 +697,7 @@ def graph_step_bench(batches=(1, 8, 64), steps: int = 20, warmup: int = 3, seed:
                                 "context_mean": round(sum(ctx) / batch)}
         del cache, runner
         torch.cuda.empty_cache()
-    log(f"[bench] graph decode steps: {json.dumps(res)}")
+    log(f"[bench] graph decode steps ({fmt}): {json.dumps(res)}")
     return res
 
 
@@ -753,7 +764,7 @@ def main() -> int:
         print(json.dumps(prefill_bench(args.steps, args.warmup)), flush=True)
         return 0
     if args.graph:
-        print(json.dumps(graph_step_bench()), flush=True)
+        print(json.dumps({f: graph_step_bench(fmt=f) for f in ("bf16", "int8", "int8-kchannel")}), flush=True)
         return 0
     if args.c4:
         res = {}
