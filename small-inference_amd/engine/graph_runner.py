@@ -203,6 +203,8 @@ class DecodeGraphRunner:
         b = len(seq_ids)
         if input_ids.shape != (b,):
             raise ValueError("one input id per sequence")
+        if len(set(seq_ids)) != b:
+            raise ValueError("a decode step holds each sequence once")
         bucket = self._bucket(b)
         if graph and bucket not in self._graphs:
             self.capture(bucket)

@@ -147,6 +147,10 @@ def test_runner_rejects_what_it_cannot_capture():
     m2.append_slot(0)
     with pytest.raises(ValueError):  # context past max_context
         runner.step([0], torch.tensor([1], device="cuda"))
+    with pytest.raises(ValueError):  # a sequence twice in one step
+        runner.step([0, 0], torch.tensor([1, 2], device="cuda"))
+    m2.allocate(1, 10)
+    m2.allocate(2, 10)
     with pytest.raises(ValueError):  # more rows than max_batch
-        runner.step([0, 0, 0], torch.tensor([1, 2, 3], device="cuda"))
+        runner.step([0, 1, 2], torch.tensor([1, 2, 3], device="cuda"))
     runner.close()
