@@ -92,7 +92,8 @@ typedef struct sipa_decode_params {
   int32_t v_scale_dtype;
   int64_t vs_stride_h, vs_stride_n;
   /* SIPA_KV_INT8_KCHAN only: bf16 staging [Hkv, n_stage, B, D] and the staging slot of each sequence's partial
-     last block (-1 when ctx % B == 0). */
+     last block (-1 when ctx % B == 0); slots are used as given and must lie in [0, n_stage), as the cache's own
+     slot bookkeeping guarantees. */
   const void* stage;
   int64_t st_stride_h, st_stride_n, st_stride_b;
   const int32_t* tail_slots;
