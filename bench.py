@@ -777,7 +777,7 @@ def main() -> int:
         return 0
     if args.c5:
         res = {}
-        for fmt in ("bf16", "int8"):
+        for fmt in ("bf16", "int8", "int8-kchannel"):
             res[fmt] = decode_step_bench(fmt=fmt)
             torch.cuda.empty_cache()
         print(json.dumps({"c5_decode_step": res}), flush=True)

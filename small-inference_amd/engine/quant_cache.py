@@ -152,19 +152,24 @@ class QuantPagedKVCache(PagedKVCache):
             if items[-1][1] == B - 1:
                 done.append(b)
 
-        def dev64(xs):
-            return torch.tensor(xs, dtype=torch.int64, device=dev)
-
-        self._staged = (dev64(staged_rows), dev64(staged_slots), dev64(staged_offs)) if staged_rows else None
-        self._done = (dev64(done), dev64([self._stage_of[b] for b in done])) if done else None
-        self._direct = (dev64(direct), dev64(direct_rows)) if direct else None
+        done_slots = [self._stage_of[b] for b in done]
         for b in done:  # free now: nothing reassigns a slot before the next forward's begin()
             self._free_stage.append(self._stage_of.pop(b))
         # Per sequence: the staging slot of its partial last block, -1 if the last block is full (the last block
         # is the one holding the sequence's last new token).
         last_slots = [meta.slots_cpu[e - 1] for e in meta.query_starts[1:]]
         tails = [self._stage_of[last_slots[i] // B] if ctx % B else -1 for i, ctx in enumerate(meta.context_lens)]
-        self._tails = torch.tensor(tails, dtype=torch.int32, device=dev)
+        # The whole plan in one host array and one asynchronous copy from pinned memory (separate uploads from
+        # pageable lists would each hold the host until the device has caught up).
+        parts = (staged_rows, staged_slots, staged_offs, done, done_slots, direct, direct_rows, tails)
+        flat = torch.tensor([x for part in parts for x in part], dtype=torch.int64)
+        if dev.type == "cuda":
+            flat = flat.pin_memory().to(dev, non_blocking=True)
+        views = torch.split(flat, [len(part) for part in parts])
+        self._staged = views[0:3] if staged_rows else None
+        self._done = views[3:5] if done else None
+        self._direct = views[5:7] if direct else None
+        self._tails = views[7].to(torch.int32)
         if self._decode is not None and len(self._decode_seqs) != meta.num_seqs:
             self._tails_dec = self._tails[torch.tensor(self._decode_seqs, device=dev)]
         else:
