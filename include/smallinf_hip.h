@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 2
+#define SIPA_ABI_VERSION 3
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -58,7 +58,7 @@ enum { SIPA_COMBINE_FUSED = 0, SIPA_COMBINE_KERNEL = 1 };
  * 188-238).
  */
 typedef struct sipa_decode_params {
-  int32_t struct_size;   /* sizeof(sipa_decode_params): guards against a stale binding */
+  int32_t struct_size;   /* sizeof(sipa_decode_params) of this ABI: guards against a stale binding */
   int32_t num_seqs;      /* S */
   int32_t num_q_heads;   /* Hq */
   int32_t num_kv_heads;  /* Hkv; Hq % Hkv == 0 */
@@ -77,8 +77,8 @@ typedef struct sipa_decode_params {
   const void* k_cache;   /* [Hkv, N, B, D] */
   const void* v_cache;   /* [Hkv, N, B, D] */
   int64_t kv_stride_h, kv_stride_n; /* block rows are contiguous: offset stride D, channel stride 1 */
-  const int32_t* block_tables; /* [S, >= ceil(max_context / B)]; entries past a sequence's context are loaded
-                                  but never used; ids are clamped to [0, num_blocks) */
+  const int32_t* block_tables; /* [S, bt_width]; entries past a sequence's context (up to ceil(max_context / B))
+                                  may be loaded but are never used; ids are clamped to [0, num_blocks) */
   int64_t bt_stride_s;
   const int32_t* context_lens; /* [S], each >= 1, the new token included; clamped to max_context */
   void* out;             /* [S, Hq, D] in q_dtype */
@@ -91,9 +91,9 @@ typedef struct sipa_decode_params {
   const void* v_scale;
   int32_t v_scale_dtype;
   int64_t vs_stride_h, vs_stride_n;
-  /* SIPA_KV_INT8_KCHAN only: bf16 staging [Hkv, n_stage, B, D] and the staging slot of each sequence's partial
-     last block (-1 when ctx % B == 0); slots are used as given and must lie in [0, n_stage), as the cache's own
-     slot bookkeeping guarantees. */
+  /* SIPA_KV_INT8_KCHAN only: bf16 staging [Hkv, num_stage, B, D] and the staging slot of each sequence's partial
+     last block (-1 when ctx % B == 0); slots past num_stage - 1 are clamped to it (wrong results, no access
+     outside the staging pool). */
   const void* stage;
   int64_t st_stride_h, st_stride_n, st_stride_b;
   const int32_t* tail_slots;
@@ -104,15 +104,19 @@ typedef struct sipa_decode_params {
      workspace must be ordered (one stream). May be NULL when 1 split runs. */
   void* workspace;
   int64_t workspace_bytes;
-  /* Optional work list (fields read only when struct_size covers them): num_items > 0 launches one workgroup
+  /* Optional work list: num_items > 0 launches one workgroup
      per item instead of the (sequence, KV head, split) grid. Items are 8 int32 each, 16-byte aligned, in device
      memory: {seq, kv_head, split, splits_of_pair, start, end, 0, 0}, the pair's tokens [start, end) and its
      splits numbered 0 .. splits_of_pair - 1. num_splits must be the largest splits_of_pair (it sizes the
      workspace); splits are always merged by the last-arriving workgroup. Built by sipa_build_work_list from the
-     host-side context lengths; a list that does not match context_lens gives wrong results (every access stays
-     in bounds). */
+     host-side context lengths (sipa_check_work_list validates a list built elsewhere). A list that does not match
+     context_lens gives wrong results (every access stays in bounds); a list inconsistent with itself (a pair
+     with more or fewer items than its splits_of_pair) also leaves that pair's merge counter non-zero, and every
+     later call on the same workspace then merges wrongly until the counter region is zeroed again. */
   const int32_t* work_items;
   int32_t num_items;
+  int32_t bt_width;      /* entries per block_tables row; must be >= ceil(max_context / B) (SIPA_EINVAL otherwise) */
+  int32_t num_stage;     /* SIPA_KV_INT8_KCHAN: staging slots in stage (>= 1); ignored by the other modes */
 } sipa_decode_params;
 
 int32_t sipa_abi_version(void);
@@ -172,7 +176,7 @@ typedef struct sipa_prefill_params {
   const void* k_cache;   /* [Hkv, N, B, D] bf16 */
   const void* v_cache;
   int64_t kv_stride_h, kv_stride_n;
-  const int32_t* block_tables; /* [S, >= ceil(max_context / B)] */
+  const int32_t* block_tables; /* [S, bt_width]; a sequence's first ceil(context / B) entries are read */
   int64_t bt_stride_s;
   const int32_t* context_lens; /* [S] tokens in the cache, this forward's included */
   const int32_t* query_starts; /* [S] first row of each sequence's new tokens */
@@ -200,6 +204,7 @@ typedef struct sipa_prefill_params {
   int32_t num_splits;
   void* workspace;
   int64_t workspace_bytes;
+  int32_t bt_width;             /* entries per block_tables row; must be >= ceil(max_context / 16) */
 } sipa_prefill_params;
 
 int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
@@ -232,6 +237,16 @@ int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int3
 int32_t sipa_build_work_list(const int32_t* context_lens_host, int32_t num_seqs, int32_t num_kv_heads,
                              int32_t cu_count, int32_t items_per_cu, int32_t max_piece, int32_t* items_out,
                              int32_t capacity, int32_t* max_splits);
+
+/*
+ * Checks a host copy of a work list before it is uploaded (no counterpart in the reference): every item's
+ * sequence and KV head in range, each pair's items numbered 0 .. splits_of_pair - 1 exactly once with the same
+ * splits_of_pair, their token ranges [start, end) within [0, max_context), in order and without overlap, and
+ * no split count above num_splits. Returns SIPA_OK or SIPA_EINVAL (sipa_last_error() names the first bad item).
+ * Lists from sipa_build_work_list always pass.
+ */
+int32_t sipa_check_work_list(const int32_t* items_host, int32_t num_items, int32_t num_seqs, int32_t num_kv_heads,
+                             int32_t max_context, int32_t num_splits);
 
 /*
  * Per-forward packed metadata on the device (the device-side form of reference engine/paged_cache.py:55-90,

@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
 
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss;
   const int n_quant = (ctx / B) * B;  // MODE 2: tokens in full (quantized) blocks; the rest are staged
-  const int tail = (MODE == 2) ? a.tail[s] : 0;
+  const int tail = (MODE == 2) ? tail_slot(a, s) : 0;
   float* pw = (float*)smem + wave * 64 * kMaxGroup;
 
   float m_run[kMaxGroup], l_run[kMaxGroup], acc[kMaxGroup][DPL];
@@ -302,7 +302,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
     for (int g = 0; g < kMaxGroup; ++g) sc[g] = 0.f;
     float vscale = 1.f;
     if (valid) {
-      blk = min(max(btr[t / B], 0), a.nb - 1);
+      blk = min(max(btr[min(t / B, a.bt_w - 1)], 0), a.nb - 1);
       off = t % B;
       const int64_t row = (int64_t)h * a.kv_sh + (int64_t)blk * a.kv_sn + (int64_t)off * D;
       const bool staged = (MODE == 2) && (t >= n_quant) && (tail >= 0);  // -1: no staging slot to read
@@ -618,6 +618,44 @@ extern "C" int32_t sipa_build_work_list(const int32_t* ctx, int32_t S, int32_t H
   return (int32_t)v.size();
 }
 
+extern "C" int32_t sipa_check_work_list(const int32_t* items, int32_t n, int32_t S, int32_t Hkv, int32_t max_ctx,
+                                        int32_t num_splits) {
+  SIPA_CHECK(items != nullptr && n >= 0 && S >= 0 && Hkv > 0 && max_ctx > 0, SIPA_EINVAL, "work list: bad arguments");
+  struct Entry {
+    int64_t pair;
+    int32_t sp, ns, start, end, index;
+  };
+  std::vector<Entry> e((size_t)n);
+  for (int i = 0; i < n; ++i) {
+    const int32_t* it = items + 8 * (int64_t)i;
+    const int32_t s = it[0], h = it[1], sp = it[2], ns = it[3], st = it[4], en = it[5];
+    SIPA_CHECK(s >= 0 && s < S && h >= 0 && h < Hkv, SIPA_EINVAL, "work item %d: pair (%d, %d) out of range", i, s, h);
+    SIPA_CHECK(ns >= 1 && ns <= num_splits && sp >= 0 && sp < ns, SIPA_EINVAL,
+               "work item %d: split %d of %d (num_splits %d)", i, sp, ns, num_splits);
+    SIPA_CHECK(st >= 0 && st < en && en <= max_ctx && en - st <= kMaxSplitBlocks * 16, SIPA_EINVAL,
+               "work item %d: tokens [%d, %d) outside [0, %d) or longer than %d", i, st, en, max_ctx,
+               kMaxSplitBlocks * 16);
+    e[i] = Entry{(int64_t)s * Hkv + h, sp, ns, st, en, i};
+  }
+  std::sort(e.begin(), e.end(), [](const Entry& x, const Entry& y) {
+    return x.pair != y.pair ? x.pair < y.pair : x.sp < y.sp;
+  });
+  // Within a pair (sorted by split): splits 0, 1, ..., ns - 1 exactly once, one stated ns, ranges in order.
+  for (size_t k = 0; k < e.size(); ++k) {
+    const bool first = k == 0 || e[k].pair != e[k - 1].pair;
+    const int expect = first ? 0 : e[k - 1].sp + 1;
+    SIPA_CHECK(e[k].sp == expect && (first || e[k].ns == e[k - 1].ns), SIPA_EINVAL,
+               "work item %d: pair (%lld, %lld) lists split %d where split %d (of %d stated) is due", e[k].index,
+               (long long)(e[k].pair / Hkv), (long long)(e[k].pair % Hkv), e[k].sp, expect, e[k].ns);
+    SIPA_CHECK(first || e[k].start >= e[k - 1].end, SIPA_EINVAL, "work item %d: overlaps split %d of its pair",
+               e[k].index, e[k - 1].sp);
+    const bool last = k + 1 == e.size() || e[k + 1].pair != e[k].pair;
+    SIPA_CHECK(!last || e[k].sp == e[k].ns - 1, SIPA_EINVAL, "pair (%lld, %lld): %d splits stated, %d listed",
+               (long long)(e[k].pair / Hkv), (long long)(e[k].pair % Hkv), e[k].ns, e[k].sp + 1);
+  }
+  return SIPA_OK;
+}
+
 extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                                                int32_t head_dim, int32_t num_splits) {
   if (num_splits <= 1) return 0;
@@ -626,11 +664,9 @@ extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_h
 
 extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   SIPA_CHECK(p != nullptr, SIPA_EINVAL, "params is NULL");
-  // Callers built against the first ABI pass the struct without the work-list fields.
-  const int32_t size_v1 = (int32_t)offsetof(sipa_decode_params, work_items);
-  SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params) || p->struct_size == size_v1, SIPA_EINVAL,
-             "struct_size %d does not match this library's sipa_decode_params (%d bytes)", p->struct_size,
-             (int)sizeof(sipa_decode_params));
+  SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params), SIPA_EINVAL,
+             "struct_size %d does not match this library's sipa_decode_params (%d bytes, ABI %d)", p->struct_size,
+             (int)sizeof(sipa_decode_params), SIPA_ABI_VERSION);
   const int S = p->num_seqs, Hq = p->num_q_heads, Hkv = p->num_kv_heads, D = p->head_dim, B = p->block_size;
   if (S == 0) return SIPA_OK;
   SIPA_CHECK(S > 0 && S <= 65535, SIPA_EINVAL, "num_seqs %d outside [0, 65535]", S);
@@ -642,6 +678,9 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   SIPA_CHECK(B > 0 && 64 % B == 0, SIPA_EINVAL, "block_size %d must divide 64 (block-aligned 64-token tiles)", B);
   SIPA_CHECK(p->max_context > 0, SIPA_EINVAL, "max_context %d must be >= 1", p->max_context);
   SIPA_CHECK(p->num_blocks > 0, SIPA_EINVAL, "num_blocks %d must be >= 1", p->num_blocks);
+  SIPA_CHECK(p->bt_width > 0 && (int64_t)p->bt_width * B >= p->max_context, SIPA_EINVAL,
+             "block_tables rows of %d entries cannot cover max_context %d (block size %d)", p->bt_width,
+             p->max_context, B);
   SIPA_CHECK(p->q_dtype == SIPA_F32 || p->q_dtype == SIPA_BF16, SIPA_EUNSUPPORTED, "q_dtype %d not f32/bf16",
              p->q_dtype);
   SIPA_CHECK(p->kv_mode >= 0 && p->kv_mode <= 2, SIPA_EINVAL, "kv_mode %d", p->kv_mode);
@@ -658,12 +697,13 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
                SIPA_EUNSUPPORTED, "scales must be f16 or f32");
   }
   if (mode == SIPA_KV_INT8_KCHAN) {
-    SIPA_CHECK(p->stage && p->tail_slots, SIPA_EINVAL, "int8 per-channel K needs stage and tail_slots");
+    SIPA_CHECK(p->stage && p->tail_slots && p->num_stage > 0, SIPA_EINVAL,
+               "int8 per-channel K needs stage, tail_slots and num_stage >= 1");
     SIPA_CHECK(aligned16(p->stage) && p->st_stride_h % 8 == 0 && p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
                SIPA_EINVAL, "staging must be 16-byte aligned with strides multiple of 8");
   }
 
-  const int n_items = p->struct_size == size_v1 ? 0 : p->num_items;
+  const int n_items = p->num_items;
   SIPA_CHECK(n_items >= 0, SIPA_EINVAL, "num_items %d < 0", n_items);
   int chunk = 0, splits = 1;
   if (n_items > 0) {
@@ -714,6 +754,8 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.chunk = chunk;
   a.max_ctx = p->max_context;
   a.nb = p->num_blocks;
+  a.bt_w = p->bt_width;
+  a.n_stage = mode == SIPA_KV_INT8_KCHAN ? p->num_stage : 1;
   a.items = n_items > 0 ? p->work_items : nullptr;
   a.fused = n_items > 0 || p->combine == SIPA_COMBINE_FUSED;  // a work list always merges in place
   a.scale_log2 = p->scale * 1.4426950408889634f;

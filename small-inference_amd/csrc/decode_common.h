@@ -306,7 +306,7 @@ constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
 
 __device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int end_spec,
                                                int (&ids)[kIdsPerThread]) {
-  const int nb_spec = (end_spec - start + 15) >> 4;
+  const int nb_spec = min((end_spec - start + 15) >> 4, a.bt_w - (start >> 4));  // never past the row's width
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
 #pragma unroll
   for (int i = 0; i < kIdsPerThread; ++i) {
@@ -329,6 +329,10 @@ __device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[k
 // A sequence's context length as the kernels use it: at most max_context, so that the splits a sequence reports
 // (and the merge waits for) are always ones the launch has.
 __device__ __forceinline__ int context_len(const DecodeArgs& a, int s) { return min(a.ctx[s], a.max_ctx); }
+
+// The staging slot of sequence s's partial last block (INT8 per-channel K): -1 (none) stays -1, slots past the
+// staging pool are clamped into it.
+__device__ __forceinline__ int tail_slot(const DecodeArgs& a, int s) { return min(a.tail[s], a.n_stage - 1); }
 
 // MFMA epilogue: each wave's softmax state (m_run per lane for head g = r, l_run partial per lane, acc in the
 // O^T accumulator layout: lane (r, q4) holds head r, channels 16 dt + 4 q4 + i) goes to LDS; then thread

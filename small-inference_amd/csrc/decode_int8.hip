@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int end = max(start, min(wend, ctx));
   const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
   const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
-  const int tail = (MODE >= 2) ? a.tail[s] : -1;       // staging slot of the partial last block, -1 if none
+  const int tail = (MODE >= 2) ? tail_slot(a, s) : -1;  // staging slot of the partial last block, -1 if none
   commit_split_ids(nb_spec, ids, bids, a.nb);
   __syncthreads();
 

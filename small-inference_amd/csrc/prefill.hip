@@ -31,6 +31,7 @@ struct PrefillArgs {
   int64_t kv_sh, kv_sn;
   const int32_t* bt;
   int64_t bt_ss;
+  int32_t bt_w;  // entries per table row (>= ceil(max_ctx / 16)): columns are clamped below it
   const int32_t* ctx;     // [S] context lengths after this forward's writes
   const int32_t* qstart;  // [S] first row of each sequence's new tokens in q / out
   const int32_t* qlen;    // [S] new tokens per sequence
@@ -203,7 +204,8 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
-  for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[i], 0), a.nb - 1);
+  const int last_col = a.bt_w - 1 - (k_lo >> 4);  // >= nblk - 1 when the host's width check held
+  for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[min(i, last_col)], 0), a.nb - 1);
 
   // Column tiles c = wave + 4 ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15 with
   // tt = c / G (G * TT <= 8). A column tile's B operand holds token r of head g (zero past the unit's tokens).
@@ -552,6 +554,8 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   SIPA_CHECK(p->max_context > 0 && p->max_context <= kMaxSplitBlocks * 16, SIPA_EUNSUPPORTED,
              "max_context %d outside [1, %d]", p->max_context, kMaxSplitBlocks * 16);
   SIPA_CHECK(p->max_query_len > 0, SIPA_EINVAL, "max_query_len %d", p->max_query_len);
+  SIPA_CHECK(p->bt_width > 0 && (int64_t)p->bt_width * 16 >= p->max_context, SIPA_EINVAL,
+             "block_tables rows of %d entries cannot cover max_context %d", p->bt_width, p->max_context);
   SIPA_CHECK(p->q && p->k_cache && p->v_cache && p->block_tables && p->context_lens && p->query_starts &&
                  p->query_lens && p->out, SIPA_EINVAL, "NULL pointer");
   SIPA_CHECK(aligned16p(p->q) && p->q_stride_t % 8 == 0 && p->q_stride_h % 8 == 0, SIPA_EINVAL,
@@ -609,6 +613,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.kv_sn = p->kv_stride_n;
   a.bt = p->block_tables;
   a.bt_ss = p->bt_stride_s;
+  a.bt_w = p->bt_width;
   a.ctx = p->context_lens;
   a.qstart = p->query_starts;
   a.qlen = p->query_lens;

@@ -92,6 +92,8 @@ struct DecodeArgs {
   int32_t S, Hq, Hkv, G, B, splits, chunk;
   int32_t max_ctx;    // every block-table row covers ceil(max_ctx / B) blocks; context lengths are clamped to it
   int32_t nb;         // blocks in the pool: block ids are clamped to [0, nb)
+  int32_t bt_w;       // entries per block-table row (>= ceil(max_ctx / B)): table columns are clamped below it
+  int32_t n_stage;    // staging slots (INT8 per-channel K): tail slots are clamped below it
   int32_t ks_f32, vs_f32;
   int32_t fused;      // 1: the last split workgroup of a (sequence, KV head) merges the splits
   float scale_log2;   // softmax scale * log2(e): scores are kept in the exp2 domain

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library; see th
 
 # SIPA_LIB overrides the location (for copies of these modules placed inside another package).
 LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # element types (SIPA_F32 ...)
 F32, BF16, F16, I8 = 0, 1, 2, 3
@@ -46,7 +46,7 @@ class DecodeParams(ctypes.Structure):
         ("v_scale", vp), ("v_scale_dtype", i32), ("vs_stride_h", i64), ("vs_stride_n", i64),
         ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64),
         ("tail_slots", vp), ("workspace", vp), ("workspace_bytes", i64),
-        ("work_items", vp), ("num_items", i32),
+        ("work_items", vp), ("num_items", i32), ("bt_width", i32), ("num_stage", i32),
     ]
 
 
@@ -63,7 +63,7 @@ class PrefillParams(ctypes.Structure):
         ("kv_mode", i32), ("k_scale", vp), ("k_scale_dtype", i32), ("ks_stride_h", i64), ("ks_stride_n", i64),
         ("v_scale", vp), ("v_scale_dtype", i32), ("vs_stride_h", i64), ("vs_stride_n", i64),
         ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64), ("num_stage", i32),
-        ("tail_slots", vp), ("num_splits", i32), ("workspace", vp), ("workspace_bytes", i64),
+        ("tail_slots", vp), ("num_splits", i32), ("workspace", vp), ("workspace_bytes", i64), ("bt_width", i32),
     ]
 
 
@@ -78,6 +78,7 @@ SIGNATURES = {
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp]),
+    "sipa_check_work_list": (i32, [vp, i32, i32, i32, i32, i32]),
     "sipa_prefill": (i32, [_c.POINTER(PrefillParams), vp]),
     "sipa_paged_metadata": (i32, [vp, i64, i32, i32, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "sipa_prefill_splits": (i32, [i32, i32, i32, i64, i32, i32]),

@@ -10,7 +10,7 @@ import ctypes
 import torch
 
 from . import _hip
-from .hip_decode import _workspace  # one split workspace per (device, stream) serves decode and prefill
+from .hip_decode import reserve_workspace  # one split workspace per (device, stream) serves decode and prefill
 
 
 def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
@@ -81,7 +81,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     p.q, p.q_stride_t, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
     p.kv_stride_h, p.kv_stride_n = k_cache.stride(0), k_cache.stride(1)
-    p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
+    p.block_tables, p.bt_stride_s, p.bt_width = block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1]
     p.context_lens, p.query_starts = context_lens.data_ptr(), query_starts.data_ptr()
     p.query_lens = query_lens.data_ptr()
     p.out, p.out_stride_t, p.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
@@ -110,7 +110,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     stream = _hip.stream_of(q)
     nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)
     if nbytes > 0:
-        ws = _workspace(q.device, stream, nbytes)
+        ws = reserve_workspace(q.device, stream, nbytes)
         p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
     _hip.check(lib.sipa_prefill(ctypes.byref(p), stream), "paged_prefill_attention")
     return out

@@ -19,6 +19,22 @@ def _i64(t: torch.Tensor) -> torch.Tensor:
     return t if (t.dtype == torch.int64 and t.is_contiguous()) else t.to(torch.int64).contiguous()
 
 
+def _require(ok: bool, msg: str) -> None:
+    """The kernels index the pools with the shapes given here: a mismatch is refused before any launch."""
+    if not ok:
+        raise ValueError(msg)
+
+
+def _token_pools(x: torch.Tensor, q_pool: torch.Tensor, s_pool: torch.Tensor) -> None:
+    T, H, D = x.shape
+    _require(q_pool.dim() == 4 and q_pool.shape[0] == H and q_pool.shape[3] == D,
+             f"q_pool {tuple(q_pool.shape)} must be [H={H}, N, B, D={D}]")
+    _require(tuple(s_pool.shape) == tuple(q_pool.shape[:3]),
+             f"s_pool {tuple(s_pool.shape)} must be [H, N, B] = {tuple(q_pool.shape[:3])}")
+    _require(q_pool.dtype == torch.int8 and s_pool.dtype == torch.float16, "q_pool must be int8 and s_pool fp16")
+    _require(q_pool.is_contiguous() and s_pool.is_contiguous(), "the pools must be contiguous")
+
+
 def quantize_store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, q_pool: torch.Tensor,
                           s_pool: torch.Tensor, *, x2: torch.Tensor | None = None, q_pool2: torch.Tensor | None = None,
                           s_pool2: torch.Tensor | None = None) -> None:
@@ -28,9 +44,9 @@ def quantize_store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.
     T, H, D = x.shape
     if T == 0:
         return
-    assert x.stride(-1) == 1 and q_pool.is_contiguous() and s_pool.is_contiguous()
-    if q_pool.dtype != torch.int8 or s_pool.dtype != torch.float16:
-        raise ValueError("q_pool must be int8 and s_pool fp16")
+    _require(x.stride(-1) == 1, "x needs a contiguous last dim")
+    _require(blocks.numel() == T and offsets.numel() == T, f"{T} tokens need {T} blocks and offsets")
+    _token_pools(x, q_pool, s_pool)
     _hip.require_gpu(x, blocks, offsets, q_pool, s_pool)
     blocks, offsets = _i64(blocks), _i64(offsets)
     if x2 is not None:
@@ -63,9 +79,13 @@ def quantize_store_blocks(src_pool: torch.Tensor, src: torch.Tensor, dst: torch.
     if src.numel() == 0:
         return
     H, _, B, D = src_pool.shape
-    assert src_pool.is_contiguous() and q_pool.is_contiguous() and s_pool.is_contiguous()
-    if q_pool.dtype != torch.int8 or s_pool.dtype != torch.float16:
-        raise ValueError("q_pool must be int8 and s_pool fp16")
+    _require(src.numel() == dst.numel(), f"{src.numel()} sources for {dst.numel()} destinations")
+    _require(q_pool.dim() == 4 and (q_pool.shape[0], q_pool.shape[2], q_pool.shape[3]) == (H, B, D),
+             f"q_pool {tuple(q_pool.shape)} must be [H={H}, N, B={B}, D={D}]")
+    _require(tuple(s_pool.shape) == (H, q_pool.shape[1], D), f"s_pool {tuple(s_pool.shape)} must be [H, N, D]")
+    _require(q_pool.dtype == torch.int8 and s_pool.dtype == torch.float16, "q_pool must be int8 and s_pool fp16")
+    _require(src_pool.is_contiguous() and q_pool.is_contiguous() and s_pool.is_contiguous(),
+             "the pools must be contiguous")
     _hip.require_gpu(src_pool, src, dst, q_pool, s_pool)
     src, dst = _i64(src), _i64(dst)
     rc = _hip.lib().sipa_quantize_store_blocks(
@@ -83,9 +103,12 @@ def quantize_store_block_rows(x: torch.Tensor, rows: torch.Tensor, dst: torch.Te
     if dst.numel() == 0:
         return
     H, _, B, D = q_pool.shape
-    assert x.stride(-1) == 1 and q_pool.is_contiguous() and s_pool.is_contiguous()
-    if rows.numel() != dst.numel() * B:
-        raise ValueError(f"{rows.numel()} rows for {dst.numel()} blocks of {B}")
+    _require(x.dim() == 3 and x.shape[1] == H and x.shape[2] == D and x.stride(-1) == 1,
+             f"x {tuple(x.shape)} must be [T, H={H}, D={D}] with a contiguous last dim")
+    _require(tuple(s_pool.shape) == (H, q_pool.shape[1], D), f"s_pool {tuple(s_pool.shape)} must be [H, N, D]")
+    _require(q_pool.dtype == torch.int8 and s_pool.dtype == torch.float16, "q_pool must be int8 and s_pool fp16")
+    _require(q_pool.is_contiguous() and s_pool.is_contiguous(), "the pools must be contiguous")
+    _require(rows.numel() == dst.numel() * B, f"{rows.numel()} rows for {dst.numel()} blocks of {B}")
     _hip.require_gpu(x, rows, dst, q_pool, s_pool)
     rows, dst = _i64(rows), _i64(dst)
     rc = _hip.lib().sipa_quantize_store_block_rows(
@@ -104,11 +127,18 @@ def store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, p
     n = blocks.numel()
     if n == 0:
         return
-    _, H, D = x.shape
-    assert x.stride(-1) == 1 and pool.stride(-1) == 1
+    T, H, D = x.shape
+    _require(x.stride(-1) == 1 and pool.stride(-1) == 1, "x and the pool need a contiguous last dim")
+    _require(pool.dim() == 4 and pool.shape[0] == H and pool.shape[3] == D,
+             f"pool {tuple(pool.shape)} must be [H={H}, N, B, D={D}]")
+    _require(offsets.numel() == n, f"{n} blocks but {offsets.numel()} offsets")
+    _require(n <= T if rows is None else rows.numel() == n, "one source row per stored token")
     if x2 is not None:
-        assert x2.shape == x.shape and x2.stride(-1) == 1 and x2.dtype == x.dtype
-        assert pool2 is not None and pool2.stride() == pool.stride() and pool2.dtype == pool.dtype
+        _require(x2.shape == x.shape and x2.stride(-1) == 1 and x2.dtype == x.dtype,
+                 "x2 must match x in shape and dtype, last dim contiguous")
+        _require(pool2 is not None and pool2.shape == pool.shape and pool2.stride() == pool.stride() and
+                 pool2.dtype == pool.dtype, "pool2 must match the pool in shape, strides and dtype")
+        _hip.require_gpu(x2, pool2)
     _hip.require_gpu(x, blocks, offsets, pool)
     blocks, offsets = _i64(blocks), _i64(offsets)
     rows = None if rows is None else _i64(rows)

@@ -27,11 +27,14 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_and_struct_layout():
-    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION
+    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 3
     # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives; the
-    # work-list fields come last (a first-ABI caller's struct ends at workspace_bytes).
+    # work-list fields, then the table width and staging count come last.
     assert _hip.DecodeParams.work_items.offset == _hip.DecodeParams.workspace_bytes.offset + 8
-    assert ctypes.sizeof(_hip.DecodeParams) == _hip.DecodeParams.num_items.offset + 8
+    assert _hip.DecodeParams.bt_width.offset == _hip.DecodeParams.num_items.offset + 4
+    pad8 = lambda n: -(-n // 8) * 8  # noqa: E731  (the structs hold 8-byte members: their size rounds up to 8)
+    assert ctypes.sizeof(_hip.DecodeParams) == pad8(_hip.DecodeParams.num_stage.offset + 4)
+    assert ctypes.sizeof(_hip.PrefillParams) == pad8(_hip.PrefillParams.bt_width.offset + 4)
 
 
 def bad_params(**over):
@@ -39,6 +42,7 @@ def bad_params(**over):
     p.struct_size = ctypes.sizeof(_hip.DecodeParams)
     p.num_seqs, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = 1, 14, 2, 64, 16
     p.max_context, p.num_blocks, p.q_dtype, p.scale = 16, 64, _hip.BF16, 0.125
+    p.bt_width = 1024  # covers 16384 tokens
     for ptr in ("q", "k_cache", "v_cache", "block_tables", "context_lens", "out"):
         setattr(p, ptr, 4096)
     for k, v in over.items():
@@ -59,6 +63,11 @@ def bad_params(**over):
     ({"k_cache": 4100}, _hip.EINVAL),                   # unaligned pool
     ({"out": None}, _hip.EINVAL),
     ({"max_context": 8192, "num_splits": 16}, _hip.EWORKSPACE),
+    ({"bt_width": 0}, _hip.EINVAL),
+    ({"max_context": 16385}, _hip.EINVAL),              # a table row of 1024 entries covers 16384 tokens
+    ({"bt_width": 511, "max_context": 8192}, _hip.EINVAL),
+    ({"kv_mode": 2, "k_scale": 4096, "v_scale": 4096, "k_scale_dtype": _hip.F16, "v_scale_dtype": _hip.F16,
+      "stage": 4096, "tail_slots": 4096, "num_stage": 0}, _hip.EINVAL),  # per-channel K without staging slots
 ])
 def test_decode_rejects_bad_arguments_before_launch(over, code):
     lib = _hip.lib()
@@ -166,13 +175,46 @@ def test_work_list_piece_size_and_errors():
     assert max(e - b for *_, b, e, _, _ in items) <= 4096 and maxs == 10
 
 
+def check_list(items, S, Hkv, max_ctx, splits):
+    flat = (ctypes.c_int32 * (8 * max(1, len(items))))(*[x for it in items for x in it])
+    return _hip.lib().sipa_check_work_list(flat, len(items), S, Hkv, max_ctx, splits)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_work_list_check_accepts_built_lists_and_rejects_broken_ones(seed):
+    """Lists from sipa_build_work_list pass the checker; a dropped, duplicated, renumbered, overlapping or
+    out-of-range item is refused with SIPA_EINVAL (such a list would leave a merge counter non-zero)."""
+    import random
+
+    rng = random.Random(seed)
+    lengths = [rng.randint(1, 20000) for _ in range(rng.randint(2, 40))]
+    items, maxs = work_list(lengths, 2)
+    S, mx = len(lengths), max(lengths)
+    assert check_list(items, S, 2, mx, maxs) == _hip.OK
+    multi = [i for i, it in enumerate(items) if it[3] > 1]
+    assert multi, "the case needs a pair with several splits"
+    k = multi[0]
+    bad = {
+        "dropped": items[:k] + items[k + 1:],
+        "duplicated": items + [items[k]],
+        "renumbered": items[:k] + [items[k][:2] + (items[k][3],) + items[k][3:]] + items[k + 1:],
+        "overlap": items[:k] + [items[k][:4] + (max(0, items[k][4] - 64) if items[k][2] else items[k][4],
+                                              items[k][5] + 64) + items[k][6:]] + items[k + 1:],
+        "sequence": items[:k] + [(S,) + items[k][1:]] + items[k + 1:],
+        "past max_context": items[:k] + [items[k][:5] + (mx + 1,) + items[k][6:]] + items[k + 1:],
+    }
+    for name, lst in bad.items():
+        assert check_list(lst, S, 2, mx, maxs) == _hip.EINVAL, name
+    assert check_list(items, S, 2, mx, maxs - 1) == _hip.EINVAL  # num_splits below a pair's split count
+
+
 def prefill_params(**over):
     p = _hip.PrefillParams()
     p.struct_size = ctypes.sizeof(_hip.PrefillParams)
     p.num_seqs, p.num_tokens, p.num_q_heads, p.num_kv_heads, p.head_dim, p.block_size = 2, 40, 14, 2, 64, 16
     p.num_blocks, p.max_context, p.max_query_len, p.scale = 8, 64, 32, 0.125
     p.q_stride_t, p.q_stride_h, p.out_stride_t, p.out_stride_h = 14 * 64, 64, 14 * 64, 64
-    p.kv_stride_h, p.kv_stride_n, p.bt_stride_s = 8 * 16 * 64, 16 * 64, 4
+    p.kv_stride_h, p.kv_stride_n, p.bt_stride_s, p.bt_width = 8 * 16 * 64, 16 * 64, 4, 2048
     for ptr in ("q", "k_cache", "v_cache", "block_tables", "context_lens", "query_starts", "query_lens", "out"):
         setattr(p, ptr, 4096)
     for k, v in over.items():
@@ -192,6 +234,8 @@ def prefill_params(**over):
     ({"q": 4100}, _hip.EINVAL),                         # unaligned rows
     ({"out_stride_h": 66}, _hip.EINVAL),
     ({"kv_stride_n": 1020}, _hip.EINVAL),
+    ({"bt_width": 3}, _hip.EINVAL),                     # 3 x 16 tokens < max_context 64
+    ({"bt_width": 0}, _hip.EINVAL),
 ])
 def test_prefill_rejects_bad_arguments_before_launch(over, code):
     lib = _hip.lib()
