@@ -30,6 +30,7 @@ import torch
 from . import _hip
 from .block_manager import BlockManager
 from .device_tables import DeviceBlockTables
+from .hip_decode import decode_workspace_bytes, reserve_workspace
 from .paged_cache import PagedKVCache, PagedMetadata, PerSequence
 
 SCRATCH_SEQ = -(1 << 40)  # the runner's own sequence id in the block manager: the padding rows' block
@@ -89,9 +90,17 @@ class DecodeGraphRunner:
             self._dtail = torch.zeros(n, dtype=torch.int32, device=dev)
             self._plan = (torch.arange(n, dtype=torch.int64, device=dev), self._dplan[:n], self._dplan[n:2 * n],
                           self._dplan[2 * n:], self._dtail)
-        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        # per bucket: the graph, its logits buffer, and the split workspace its decode launches write
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor | None]] = {}
         self._pool = None
         self._stream = torch.cuda.Stream(device=dev)  # capture stream (default priority)
+        # A graph keeps the raw address of the capture stream's split workspace. The buffer is sized here for the
+        # largest bucket's decode launches, so no later capture replaces it while earlier graphs still use it.
+        cfg = cache.cfg
+        mode = {"int8": 1, "int8-kchannel": 2}.get(getattr(cache, "fmt", None), 0)
+        self._ws_bytes = max(decode_workspace_bytes(b, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, max_context,
+                                                    mode) for b in self.buckets)
+        self._workspace = reserve_workspace(torch.device(dev), self._stream.cuda_stream, self._ws_bytes)
         self._prepare([], max_batch)
 
     # ---- persistent metadata ------------------------------------------------------------------------------------
@@ -194,7 +203,11 @@ class DecodeGraphRunner:
         torch.cuda.current_stream().wait_stream(s)
         if self._pool is None:
             self._pool = g.pool()
-        self._graphs[bucket] = (g, logits)
+        plan = getattr(self.cache, "_plan", None)  # the decode plan the captured layers launched
+        ws = getattr(plan, "workspace", None)
+        if ws is not None and ws.data_ptr() != self._workspace.data_ptr():
+            raise RuntimeError("the captured decode used a split workspace the runner did not reserve")
+        self._graphs[bucket] = (g, logits, ws)
 
     def step(self, seq_ids: list[int], input_ids: torch.Tensor, graph: bool = True) -> torch.Tensor:
         """Logits [len(seq_ids), vocab] of one decode step: row i is sequence seq_ids[i]'s newest token
@@ -213,7 +226,7 @@ class DecodeGraphRunner:
         self._d64[:b].copy_(input_ids.to(self._d64.device, torch.int64), non_blocking=True)
         if not graph:
             return self._forward(bucket)[:b]
-        g, logits = self._graphs[bucket]
+        g, logits, _ = self._graphs[bucket]
         g.replay()
         return logits[:b]
 

@@ -93,6 +93,14 @@ def build_work_list(context_lens: list[int], num_kv_heads: int, cu_count: int | 
     return items, int(maxs.value)
 
 
+def check_work_list(items: np.ndarray, num_seqs: int, num_kv_heads: int, max_context: int, num_splits: int) -> None:
+    """Raise ValueError unless a host work list is consistent (sipa_check_work_list): each pair's splits listed
+    once, in order, with one split count; ranges inside [0, max_context)."""
+    items = np.ascontiguousarray(items, dtype=np.int32)
+    _hip.check(_hip.lib().sipa_check_work_list(items.ctypes.data, items.shape[0], num_seqs, num_kv_heads, max_context,
+                                              num_splits), "work list")
+
+
 def is_ragged(context_lens: list[int]) -> bool:
     """Whether a batch gains from a work list: its lengths are far from uniform (total under 80% of
     num_seqs * max_context)."""
@@ -111,13 +119,37 @@ def split_plan(max_context: int, num_splits: int) -> tuple[int, int]:
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (device.index, stream)
+def reserve_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """The split workspace of (device, stream), at least nbytes (and 1 MiB) long. A larger request replaces the
+    stream's buffer with a new zeroed one; the old one lives on only while something holds it, so code that keeps
+    raw addresses beyond a call (captured graphs) must keep the tensor this returned, or reserve the largest size
+    it will need before it records any address."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", index))
         _workspaces[key] = ws
     return ws
+
+
+def grid_splits(num_seqs: int, num_kv_heads: int, max_context: int, quant_mode: int = 0,
+                cu_count: int | None = None) -> int:
+    """The split count a decode plan requests on the (sequence, KV head, split) grid when none is given: the
+    library's policy for the kernel family, and for INT8 pools pieces of at most INT8_MAX_SPLIT tokens."""
+    cu = device_cu_count() if cu_count is None else cu_count
+    req = int(_hip.lib().sipa_choose_splits_for(num_seqs, num_kv_heads, max_context, cu, quant_mode))
+    if quant_mode:
+        req = max(req, math.ceil(max_context / INT8_MAX_SPLIT))
+    return req
+
+
+def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_context: int,
+                           quant_mode: int = 0, num_splits: int | None = None, cu_count: int | None = None) -> int:
+    """Workspace bytes a grid decode of these shapes needs (num_splits None: the policy's split count)."""
+    req = num_splits or grid_splits(num_seqs, num_kv_heads, max_context, quant_mode, cu_count)
+    return int(_hip.lib().sipa_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim, req))
 
 
 class DecodePlan:
@@ -135,9 +167,13 @@ class DecodePlan:
                  host_context_lens: list[int] | None = None, work_list: str = "auto"):
         S, Hq, D = q.shape
         Hkv, N, B, _ = k_cache.shape
-        assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and \
-            block_tables.stride(-1) == 1
-        assert TILE % B == 0, "tiles must be block-aligned"
+        # The reference asserts these (engine/triton_decode.py:201,211): AssertionError, raised explicitly so that
+        # python -O keeps the checks.
+        if not (q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous() and
+                block_tables.stride(-1) == 1):
+            raise AssertionError("q needs a contiguous last dim, the pools must be contiguous")
+        if TILE % B:
+            raise AssertionError(f"block size {B} must divide the {TILE}-token tile")
         _hip.require_gpu(q, k_cache, v_cache, block_tables, context_lens)
         if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
             raise ValueError("block_tables and context_lens must be int32")
@@ -162,20 +198,22 @@ class DecodePlan:
         if use_list and host_context_lens is None:
             raise ValueError("work_list='on' needs host_context_lens")
         self.items = None
+        self.workspace = None
         if use_list:
             if len(host_context_lens) != S or max(host_context_lens, default=0) > max_context:
                 raise ValueError("host_context_lens must hold S lengths, none above max_context")
             items, max_splits = build_work_list(host_context_lens, Hkv, device_cu_count(q.device),
                                                 max_piece=0 if quant is None else INT8_MAX_SPLIT)
+            check_work_list(items, S, Hkv, max_context, max_splits)
             self.items = torch.from_numpy(items).to(q.device)
             self._keep.append(self.items)
             self.requested = self.splits = max_splits
             self.chunk = None
         else:
-            # The library's policy for this kernel family (the INT8 kernels run two workgroups per CU).
-            self.requested = num_splits or int(self.lib.sipa_choose_splits_for(
-                S, Hkv, max_context, device_cu_count(q.device), self.quant_mode))
-            if quant is not None:  # the library splits INT8 work into pieces of at most INT8_MAX_SPLIT tokens
+            # The library's policy for this kernel family (the INT8 kernels run two workgroups per CU), and INT8
+            # work in pieces of at most INT8_MAX_SPLIT tokens.
+            self.requested = num_splits or grid_splits(S, Hkv, max_context, self.quant_mode, device_cu_count(q.device))
+            if quant is not None:
                 self.requested = max(self.requested, math.ceil(max_context / INT8_MAX_SPLIT))
             self.splits, self.chunk = split_plan(max_context, self.requested)
 
@@ -186,7 +224,8 @@ class DecodePlan:
         p.q_dtype = _hip.dtype_code(q.dtype)
         p.impl, p.combine = _hip.IMPL[impl], _hip.COMBINE[combine]
         p.scale = float(scale)
-        p.block_tables, p.bt_stride_s = block_tables.data_ptr(), block_tables.stride(0)
+        p.block_tables, p.bt_stride_s, p.bt_width = block_tables.data_ptr(), block_tables.stride(0), \
+            block_tables.shape[1]
         p.context_lens = self._keep[1].data_ptr()
         p.kv_mode = self.quant_mode
         if self.items is not None:
@@ -204,12 +243,16 @@ class DecodePlan:
                     raise ValueError("mode 2 needs stage and tail_slots")
                 if quant.tail_slots.dtype != torch.int32:
                     raise ValueError("tail_slots must be int32")
+                if quant.tail_slots.numel() < S:
+                    raise ValueError(f"tail_slots holds {quant.tail_slots.numel()} slots for {S} sequences")
                 tails = quant.tail_slots.contiguous()
                 self._keep.append(tails)
                 p.tail_slots = tails.data_ptr()
+                self.num_stage = p.num_stage = quant.stage.shape[1]
         if S > 0 and self.splits > 1:
             nbytes = int(self.lib.sipa_decode_workspace_bytes(S, Hq, Hkv, D, self.requested))
-            ws = _workspace(q.device, self.stream, nbytes)
+            ws = reserve_workspace(q.device, self.stream, nbytes)
+            self.workspace = ws
             self._keep.append(ws)
             p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
         self._bind(q, k_cache, v_cache, quant)
@@ -239,6 +282,8 @@ class DecodePlan:
                 st = quant.stage
                 if st.dtype != torch.bfloat16 or st.stride(-1) != 1:
                     raise ValueError("stage must be bf16 with a contiguous last dim")
+                if st.shape[1] != self.num_stage:
+                    raise ValueError("stage does not match the plan's staging slots")
                 p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = \
                     st.data_ptr(), st.stride(0), st.stride(1), st.stride(2)
 
