@@ -13,7 +13,6 @@ merging, round-trip bounds).
 from __future__ import annotations
 
 import ctypes
-import os
 from pathlib import Path
 
 import numpy as np
@@ -226,10 +225,12 @@ def f32_to_f16_bits_c(values) -> np.ndarray:
 # ---- bf16 helpers --------------------------------------------------------------------------------------------------
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    """Round fp32 values to bf16 (nearest even) and return them as fp32."""
-    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
-    return r.astype(np.uint32).view(np.float32)
+    """Round fp32 values to bf16 (nearest even; past the largest bf16, infinity) and return them as fp32. NaN
+    stays NaN (the integer rounding below would carry a signalling NaN's payload into the exponent)."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16).view(np.float32)
+    return np.where(np.isnan(x), np.float32(np.nan), r).astype(np.float32)
 
 
 # ---- timed CPU baseline (torch on the host cores) -------------------------------------------------------------------
@@ -253,8 +254,3 @@ def decode_torch_cpu(q, k_pool, v_pool, tables, lengths, scale):
         p = torch.softmax(torch.bmm(qg, k.transpose(1, 2)) * scale, dim=-1)
         out[i] = torch.bmm(p, v).reshape(Hq, D)
     return out
-
-
-def cpu_threads() -> int:
-    """Host cores the baseline uses (all of them)."""
-    return os.cpu_count() or 1

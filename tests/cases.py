@@ -61,6 +61,60 @@ def compact_pool(k: torch.Tensor, tables: list[list[int]], lengths: list[int], B
     return small, [[remap[b] for b in t[:-(-n // B)]] for t, n in zip(tables, lengths)]
 
 
+def oracle_cache_decode(cache, layer: int, q: np.ndarray, tables: list[list[int]], lengths: list[int], scale: float,
+                        tails: list[int] | None = None) -> np.ndarray:
+    """The oracle's fp32 decode of one layer of a cache for the given sequences (tables, lengths), q [S, Hq, D]:
+    only the blocks the tables use are copied to the host; INT8 pools are dequantized as the reference's gather
+    path does (per-token scales; format "int8-kchannel" with per-(block, channel) K scales and each partial last
+    block of K from its staging slot, tails[i], -1 when the last block is full)."""
+    B = cache.block_size
+    used = sorted({b for t, n in zip(tables, lengths) for b in t[:-(-n // B)]})
+    remap = {b: i for i, b in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.int64, device=cache.k.device)
+    t2 = [[remap[b] for b in t[:-(-n // B)]] for t, n in zip(tables, lengths)]
+
+    def take(x):
+        return x[layer].index_select(1, idx).float().cpu().numpy()
+
+    fmt = getattr(cache, "fmt", "bf16")
+    if fmt == "bf16":
+        kp, vp = take(cache.k), take(cache.v)
+    else:
+        vp = paged_ref.dequant_tokens(take(cache.v), take(cache.v_scale))
+        kp = paged_ref.dequant_tokens(take(cache.k), take(cache.k_scale)) if fmt == "int8" else None
+    if fmt == "int8-kchannel":
+        kq, ks, stage = take(cache.k), take(cache.k_scale), cache.stage[layer].float().cpu().numpy()
+    out = np.empty(q.shape, dtype=np.float32)
+    for i, n in enumerate(lengths):
+        if fmt == "int8-kchannel":
+            k_i = paged_ref.gather_kchannel(kq, ks, stage, t2[i], n, int(tails[i]))
+        else:
+            k_i = paged_ref.gather(kp, t2[i], n)
+        out[i] = paged_ref.attend_one(q[i], k_i, paged_ref.gather(vp, t2[i], n), scale, np.float32)
+    return out
+
+
+def assert_decode_close(got, ref, what: str = "decode", atol: float = 8e-3) -> float:
+    """The north-star bound on a bf16 attention output against the fp32 oracle: max-abs <= atol (8e-3) wherever
+    |ref| < 2, and relative 2^-7 where |ref| >= 2 (there half a bf16 unit of the output alone reaches 2^-8 |out|,
+    7.8e-3 at |out| = 2). Prints the raw max-abs error and the |out| distribution; returns the raw max-abs."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    err = np.abs(got - ref)
+    mag = np.abs(ref)
+    small = mag < 2.0
+    raw = float(err.max()) if err.size else 0.0
+    e_small = float(err[small].max()) if small.any() else 0.0
+    rel_big = float((err[~small] / mag[~small]).max()) if (~small).any() else 0.0
+    q = np.percentile(mag, [50, 99, 100]) if mag.size else [0, 0, 0]
+    print(f"{what}: max-abs {raw:.2e} (|ref| < 2: {e_small:.2e}; relative above: {rel_big:.2e}); "
+          f"|ref| median {q[0]:.2f}, p99 {q[1]:.2f}, max {q[2]:.2f}, {int((~small).sum())} values >= 2", flush=True)
+    assert e_small <= atol, f"{what}: max-abs {e_small:.3e} where |ref| < 2 exceeds {atol}"
+    assert rel_big <= 2.0 ** -7, f"{what}: relative error {rel_big:.3e} where |ref| >= 2 exceeds 2^-7"
+    return raw
+
+
 def bf16_half_ulp(x: np.ndarray) -> np.ndarray:
     """Half a bf16 unit in the last place at |x| (8 significant bits): the rounding error any bf16 output may
     carry on top of the arithmetic's own error."""

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import HEADS, RAGGED, bf16_error_beyond_rounding, make_case, oracle_decode
+from cases import HEADS, RAGGED, assert_decode_close, make_case, oracle_decode
 from engine.hip_decode import choose_splits, paged_decode_attention, split_plan
 
 pytestmark = pytest.mark.gpu
@@ -244,7 +244,7 @@ def test_int8_bad_ids_are_clamped():
     torch.cuda.synchronize()
     kf, vf = kq.float() * ks.float()[..., None], vq.float() * vs.float()[..., None]
     ref = oracle_decode(q, kf, vf, fixed, lengths, D ** -0.5, np.float32)
-    assert bf16_error_beyond_rounding(out.double().cpu().numpy(), ref) <= 8e-3
+    assert_decode_close(out.double().cpu().numpy(), ref, "int8 clamp")
 
 
 def test_table_narrower_than_max_context_is_refused():

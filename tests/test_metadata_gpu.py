@@ -1,7 +1,8 @@
-"""Per-forward metadata derived on the device (engine/device_tables.py, sipa_paged_metadata) against the host
-builder build_metadata (the reference's contents, engine/paged_cache.py:55-90): every field equal, bit for bit,
-for decode batches, prefill chunks and mixed batches over fragmented pools; and a model forward driven by the
-device metadata gives the same logits as one driven by the host metadata."""
+"""Per-forward metadata derived on the device (engine/device_tables.py, sipa_paged_metadata) against the oracle's
+restatement of the reference's builder (oracle/paged_ref.py metadata, reference engine/paged_cache.py:55-90) and
+against the host builder build_metadata: every field equal, bit for bit, for decode batches, prefill chunks and
+mixed batches over fragmented pools; and a model forward driven by the device metadata gives the same logits as one
+driven by the host metadata."""
 
 import random
 
@@ -13,8 +14,20 @@ from engine.config import ModelConfig
 from engine.device_tables import DeviceBlockTables
 from engine.model import Qwen2Model
 from engine.paged_cache import PagedKVCache, build_metadata
+from oracle import paged_ref
 
 pytestmark = pytest.mark.gpu
+
+
+def assert_matches_oracle(dev, m, batch):
+    """Every field of the device metadata equals the oracle's for the same tables and batch."""
+    ref = paged_ref.metadata({s: m.block_table(s) for s, _, _ in batch}, batch, m.block_size)
+    assert dev.query_starts == ref["query_starts"] and dev.context_lens == ref["context_lens"]
+    for f in ("positions", "slot_mapping", "slot_blocks", "slot_offsets", "block_tables"):
+        assert getattr(dev, f).tolist() == ref[f], f
+    assert dev.context_lens_t.tolist() == ref["context_lens"]
+    assert dev.last_token_indices.tolist() == ref["last_token_indices"]
+    assert list(dev.slots_cpu) == ref["slot_mapping"]
 
 
 def assert_same(dev, host):
@@ -61,6 +74,7 @@ def test_device_metadata_equals_host_metadata(seed):
         dev = dt.build(batch)
         host = build_metadata(m, batch, "cuda")
         torch.cuda.synchronize()
+        assert_matches_oracle(dev, m, batch)
         assert_same(dev, host)
     s0 = min(lens)
     with pytest.raises(ValueError):

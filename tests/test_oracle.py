@@ -8,7 +8,11 @@ Each restatement is checked against something independent of its own formula:
   - gather-then-attend against torch.nn.functional.scaled_dot_product_attention with repeated KV heads, against
     brute-force loops in fp64, and against closed forms (uniform and one-hot softmax);
   - the split merge against the unsplit softmax (the identity Flash-Decoding rests on);
-  - indexing and metadata against the reference tests' known answers (tests/golden/reference_known_answers.json).
+  - indexing and metadata against the reference tests' known answers (tests/golden/reference_known_answers.json);
+  - the bf16 rounding helper against torch's Tensor.bfloat16() over specials, ties and every exponent;
+  - dequantization against the exact products (int8 x fp16 fits fp32) and the quantizer's round-trip bound
+    |x - q s| <= s / 2 (reference tests/test_quant.py:8-26), per token and per channel;
+  - the timed CPU baseline (torch gather-then-attend) against the fp64 oracle decode on a ragged, scattered batch.
 """
 
 import json
@@ -267,6 +271,8 @@ def test_metadata_known_answer():
     for key in ("query_starts", "context_lens", "positions", "slot_mapping", "slot_blocks", "slot_offsets",
                 "block_tables", "last_token_indices"):
         assert meta[key] == ka[key], key
+    padded = paged_ref.padded_tables([tables[0], tables[1]], meta["context_lens"], ka["block_size"])
+    assert padded.dtype == np.int32 and padded.tolist() == ka["block_tables"]
 
 
 def test_slots_known_answer():
@@ -286,3 +292,72 @@ def test_per_channel_beats_per_token_with_outlier_channels():
     err_t = np.linalg.norm(paged_ref.dequant_tokens(qt, st) - x) / np.linalg.norm(x)
     err_c = np.linalg.norm(paged_ref.dequant_channels(qc, sc) - x) / np.linalg.norm(x)
     assert err_c < err_t / 2, (err_c, err_t)
+
+
+# ---- bf16 rounding, dequantization, the CPU baseline ---------------------------------------------------------------
+
+def test_bf16_round_matches_torch():
+    """bf16_round == torch's fp32 -> bf16 -> fp32 bit for bit: specials, subnormals, the largest finite values
+    (round to infinity), exact ties with even and odd lower neighbours, and random values over every exponent."""
+    rng = np.random.default_rng(21)
+    f32 = np.float32
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, 1.0, -1.0, np.finfo(f32).max, -np.finfo(f32).max,
+                         np.finfo(f32).tiny, 1e-45, -1e-45, 3.0e38, 65504.0], dtype=f32)
+    lower = rng.integers(0, 1 << 15, 4000, dtype=np.uint32) << 16 | (rng.integers(0, 256, 4000, dtype=np.uint32) << 23)
+    ties = (lower.astype(np.uint32) | 0x8000).view(f32)  # exactly halfway between two bf16 neighbours
+    near = np.concatenate([(lower | 0x7FFF).view(f32), (lower | 0x8001).view(f32)])
+    with np.errstate(over="ignore"):  # the largest draws overflow to infinity: a case of their own
+        wide = (rng.standard_normal(20000) * 2.0 ** rng.integers(-149, 128, 20000)).astype(f32)
+    x = np.concatenate([specials, ties, near, wide])
+    x = x[np.isfinite(x) | np.isinf(x)]
+    want = torch.from_numpy(x.copy()).bfloat16().float().numpy()
+    got = paged_ref.bf16_round(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(paged_ref.bf16_round(np.array([np.nan, np.float32(np.nan) * -1], dtype=f32))).all()
+    snan = np.array([0x7F800001, 0xFF800123], dtype=np.uint32).view(f32)
+    assert np.isnan(paged_ref.bf16_round(snan)).all()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_dequantize_is_exact_and_inverts_the_quantizer(seed):
+    """dequant_tokens / dequant_channels equal the exact products q * s (an int8 code times an fp16 scale is
+    exact in fp32) with each scale on its own axis, and undo the quantizer to within half a step:
+    |x - q s| <= s / 2 for every element (the reference's round-trip invariant, tests/test_quant.py:8-26)."""
+    rng = np.random.default_rng(30 + seed)
+    x = (rng.standard_normal((2, 9, 16, 64)) * rng.random((2, 9, 16, 1)) * 4).astype(np.float32)
+    x[..., :3] *= 30.0  # outlier channels
+    x[1, 4, 7] = 0.0    # a zero vector (scale 0, codes 0)
+    qt, st = paged_ref.quantize_per_token(x)
+    dt = paged_ref.dequant_tokens(qt, st)
+    assert dt.dtype == np.float32 and dt.shape == x.shape
+    assert np.array_equal(dt.astype(np.float64), qt.astype(np.float64) * st.astype(np.float64)[..., None])
+    assert (np.abs(x.astype(np.float64) - dt) <= st.astype(np.float64)[..., None] / 2).all()
+    assert not dt[1, 4, 7].any()
+    qc, sc = paged_ref.quantize_per_channel(x, axis=2)  # [H, N, D] scales over each block's 16 tokens
+    dc = paged_ref.dequant_channels(qc, sc)
+    assert dc.dtype == np.float32 and dc.shape == x.shape
+    assert np.array_equal(dc.astype(np.float64), qc.astype(np.float64) * sc.astype(np.float64)[:, :, None, :])
+    assert (np.abs(x.astype(np.float64) - dc) <= sc.astype(np.float64)[:, :, None, :] / 2).all()
+
+
+def test_cpu_baseline_matches_oracle_decode():
+    """decode_torch_cpu (the timed CPU baseline: torch gather-then-attend in fp32) equals the fp64 oracle decode on
+    a ragged batch over a scattered pool with partial last blocks and GQA groups of 7."""
+    rng = np.random.default_rng(40)
+    Hq, Hkv, D, B = 14, 2, 64, 16
+    lengths = [1, 15, 16, 17, 33, 100, 1000, 257]
+    nbs = [-(-n // B) for n in lengths]
+    perm = rng.permutation(3 * sum(nbs)).tolist()
+    tables, at = [], 0
+    for nb in nbs:
+        tables.append(perm[at:at + nb])
+        at += nb
+    N = len(perm)
+    k = rng.standard_normal((Hkv, N, B, D)).astype(np.float32)
+    v = rng.standard_normal((Hkv, N, B, D)).astype(np.float32)
+    q = rng.standard_normal((len(lengths), Hq, D)).astype(np.float32)
+    bt = torch.from_numpy(paged_ref.padded_tables(tables, lengths, B).astype(np.int64))
+    got = paged_ref.decode_torch_cpu(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), bt, lengths,
+                                     D ** -0.5).numpy()
+    want = paged_ref.decode(q, k, v, tables, lengths, D ** -0.5, np.float64)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-6)
