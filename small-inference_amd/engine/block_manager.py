@@ -17,14 +17,14 @@ import numpy as np
 
 
 class OutOfBlocks(RuntimeError):
-    """Not enough free blocks for the request; nothing was changed."""
+    """A request needed more free blocks than the pool had; the manager is left as it was before the call."""
 
 
 class BlockManager:
     def __init__(self, num_blocks: int, block_size: int = 16):
         """A pool of num_blocks blocks of block_size tokens, all free."""
         if num_blocks < 1 or block_size < 1:
-            raise ValueError("need at least one block of at least one token")
+            raise ValueError(f"a pool needs num_blocks >= 1 and block_size >= 1, got {num_blocks} and {block_size}")
         self.num_blocks, self.block_size = num_blocks, block_size
         # The top of the stack is the end of the list: block 0 is handed out first.
         self._free: list[int] = list(reversed(range(num_blocks)))
@@ -97,7 +97,7 @@ class BlockManager:
         """Slots of positions [start, end) of the sequence."""
         n = self._lengths[seq_id]
         if not (0 <= start <= end <= n):
-            raise ValueError(f"positions [{start}, {end}) outside sequence {seq_id} of length {n}")
+            raise ValueError(f"sequence {seq_id} holds {n} tokens; slots of positions {start}..{end - 1} asked for")
         table, B = self._tables[seq_id], self.block_size
         return [table[p // B] * B + p % B for p in range(start, end)]
 
@@ -118,23 +118,24 @@ class BlockManager:
         self._table_listeners.remove(fn)
 
     def _pop_blocks(self, count: int) -> list[int]:
-        taken = []
-        for _ in range(count):
-            b = self._free.pop()
-            assert self._ref[b] == 0, f"block {b} on the free list with ref count {self._ref[b]}"
+        taken = self._free[len(self._free) - count:][::-1]  # top of the stack first
+        del self._free[len(self._free) - count:]
+        for b in taken:
+            if self._ref[b]:
+                raise AssertionError(f"block {b} came off the free stack while {self._ref[b]} sequence(s) hold it")
             self._ref[b] = 1
-            taken.append(b)
         return taken
 
     def allocate(self, seq_id: int, n_tokens: int) -> list[int]:
         """Create seq_id holding n_tokens (>= 0) and return their slots."""
         if seq_id in self._tables:
-            raise ValueError(f"sequence {seq_id} already allocated")
+            raise ValueError(f"sequence {seq_id} is already live")
         if n_tokens < 0:
-            raise ValueError("n_tokens must be >= 0")
+            raise ValueError(f"a sequence cannot hold {n_tokens} tokens")
         need = self.blocks_for(n_tokens)
         if need > len(self._free):
-            raise OutOfBlocks(f"{need} blocks needed, {len(self._free)} free")
+            raise OutOfBlocks(f"a new sequence of {n_tokens} tokens takes {need} blocks; the pool has "
+                              f"{len(self._free)} free")
         self._tables[seq_id] = self._pop_blocks(need)
         self._lengths[seq_id] = n_tokens
         self._mirror_extend(seq_id, self._tables[seq_id])
@@ -144,7 +145,8 @@ class BlockManager:
         """Extend seq_id by n tokens and return their slots."""
         need = self.new_blocks_needed(seq_id, n)
         if need > len(self._free):
-            raise OutOfBlocks(f"sequence {seq_id}: {need} blocks needed, {len(self._free)} free")
+            raise OutOfBlocks(f"{n} more tokens for sequence {seq_id} take {need} blocks; the pool has "
+                              f"{len(self._free)} free")
         new = self._pop_blocks(need)
         self._tables[seq_id].extend(new)
         if new:
@@ -165,7 +167,8 @@ class BlockManager:
         released = []
         for b in table[::-1]:  # last block first, so the stack hands the blocks out again in table order
             self._ref[b] -= 1
-            assert self._ref[b] >= 0, f"block {b} freed twice"
+            if self._ref[b] < 0:
+                raise AssertionError(f"block {b} released more often than it was taken")
             if self._ref[b] == 0:
                 self._free.append(b)
                 released.append(b)
@@ -177,16 +180,25 @@ class BlockManager:
     # ---- checking ------------------------------------------------------------------------------------------------
 
     def check_invariants(self) -> None:
-        """Assert consistency: every block free xor owned, reference counts equal owners, table sizes match
-        lengths. Raises AssertionError otherwise."""
+        """Raise AssertionError unless the bookkeeping is consistent: each block is on the free stack exactly when
+        no table holds it, reference counts equal the number of holding tables, every table has the blocks its
+        length needs, and the int32 mirrors match the tables."""
+        def fail(msg: str) -> None:
+            raise AssertionError(msg)
+
         free = set(self._free)
-        assert len(free) == len(self._free), "duplicate block on the free list"
-        owners = [0] * self.num_blocks
+        if len(free) != len(self._free):
+            fail("the free stack holds some block more than once")
+        owners = np.zeros(self.num_blocks, dtype=np.int64)
         for seq_id, table in self._tables.items():
-            assert len(table) == self.blocks_for(self._lengths[seq_id]), f"sequence {seq_id}: table size wrong"
-            assert self._arrays[seq_id][:len(table)].tolist() == table, f"sequence {seq_id}: array mirror differs"
-            for b in table:
-                owners[b] += 1
-        for b, n in enumerate(owners):
-            assert n == self._ref[b], f"block {b}: ref {self._ref[b]} but {n} owners"
-            assert (b in free) == (n == 0), f"block {b}: free={b in free} with {n} owners"
+            if len(table) != self.blocks_for(self._lengths[seq_id]):
+                fail(f"sequence {seq_id} holds {len(table)} blocks for {self._lengths[seq_id]} tokens")
+            if self._arrays[seq_id][:len(table)].tolist() != table:
+                fail(f"the int32 mirror of sequence {seq_id} is out of date")
+            np.add.at(owners, np.asarray(table, dtype=np.int64), 1)
+        for b in range(self.num_blocks):
+            n = int(owners[b])
+            if n != self._ref[b]:
+                fail(f"block {b} has reference count {self._ref[b]} but {n} holding tables")
+            if (b in free) == (n > 0):
+                fail(f"block {b} is {'both free and held' if n else 'neither free nor held'}")

@@ -41,8 +41,3 @@ def quantize_per_channel(x: torch.Tensor, dim: int) -> tuple[torch.Tensor, torch
 def dequantize(q: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """q * scale in `dtype`; scale must broadcast against q."""
     return (q.float() * scale.float()).to(dtype)
-
-
-def relative_error(x: torch.Tensor, x_hat: torch.Tensor) -> float:
-    """||x - x_hat|| / ||x||."""
-    return ((x.float() - x_hat.float()).norm() / x.float().norm()).item()

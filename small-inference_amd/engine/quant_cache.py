@@ -19,6 +19,9 @@ through the HIP decode kernel with dequantization fused into the loads (QuantKV 
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
+import numpy as np
 import torch
 
 from .block_manager import BlockManager
@@ -29,18 +32,109 @@ from .quant import dequantize, quantize_per_channel, quantize_per_token
 
 FORMATS = ("bf16", "int8", "int8-kchannel")
 
+# Pool bytes per (token, KV head, layer) as a function of (head_dim d, block size B); K and V together.
+_BYTES_PER_HEAD_TOKEN = {
+    "bf16": lambda d, B: 4 * d,                      # K and V in bf16
+    "int8": lambda d, B: 2 * (d + 2),                # int8 K and V, an fp16 scale each
+    "int8-kchannel": lambda d, B: (d + 2) + d + 2 * d / B,  # V as "int8"; K codes and d fp16 scales per block
+}
+
 
 def kv_bytes_per_token(cfg: ModelConfig, fmt: str, block_size: int = 16) -> float:
     """Pool bytes per token: 12,288 / 6,336 / 6,624 for 0.5B (bf16 / int8 / int8-kchannel, 16-token blocks)."""
-    d = cfg.head_dim
-    per_head_layer = {"bf16": 4 * d, "int8": 2 * (d + 2), "int8-kchannel": (d + 2) + d + 2 * d / block_size}[fmt]
-    return cfg.num_layers * cfg.num_kv_heads * per_head_layer
+    return cfg.num_layers * cfg.num_kv_heads * _BYTES_PER_HEAD_TOKEN[fmt](cfg.head_dim, block_size)
 
 
 def blocks_for_budget(cfg: ModelConfig, fmt: str, budget_bytes: int, block_size: int, n_stage: int = 0) -> int:
     """Blocks that fit in budget_bytes after n_stage bf16 staging slots (format B)."""
-    stage_bytes = n_stage * cfg.num_layers * cfg.num_kv_heads * block_size * cfg.head_dim * 2
-    return int((budget_bytes - stage_bytes) // (block_size * kv_bytes_per_token(cfg, fmt, block_size)))
+    staging = 2 * n_stage * cfg.num_layers * cfg.num_kv_heads * block_size * cfg.head_dim
+    return int((budget_bytes - staging) // (block_size * kv_bytes_per_token(cfg, fmt, block_size)))
+
+
+class StagingBook:
+    """Host bookkeeping of format B's staging slots: which slot holds which partial block.
+
+    slot_of maps block id -> slot; free is the stack of idle slots, top at the end of the list, so a fresh book
+    hands out slot 0 first and a returned slot is the next one handed out. Both are mutated in place (the cache
+    exposes them as _stage_of and _free_stage)."""
+
+    def __init__(self, n_stage: int):
+        self.n_stage = n_stage
+        self.slot_of: dict[int, int] = {}
+        self.free: list[int] = list(range(n_stage))[::-1]
+
+    def assign(self, blocks) -> None:
+        """Give each of blocks (none of them holding a slot) the next idle slot, in order."""
+        blocks = list(blocks)
+        if len(blocks) > len(self.free):
+            raise RuntimeError(f"the forward needs {len(blocks)} more INT8 staging slots than the {len(self.free)} "
+                               f"idle of {self.n_stage}; construct the cache with a larger n_stage")
+        for b in blocks:
+            self.slot_of[b] = self.free.pop()
+
+    def slot(self, block: int) -> int:
+        """The block's slot, assigned on first use."""
+        if block not in self.slot_of:
+            self.assign([block])
+        return self.slot_of[block]
+
+    def release(self, blocks) -> None:
+        """Blocks that left staging (quantized into the pool, or freed by the block manager) return their slots,
+        in the order given; blocks without a slot are ignored."""
+        for b in blocks:
+            s = self.slot_of.pop(b, None)
+            if s is not None:
+                self.free.append(s)
+
+
+@dataclass
+class _StagingPlan:
+    """Format B's writes for one forward, as host arrays (uploaded together). Row indices refer to the forward's
+    tokens; blocks and slots to the pool and the staging pool."""
+    staged_rows: np.ndarray   # tokens whose K goes to a staging slot ...
+    staged_slots: np.ndarray  # ... this slot ...
+    staged_offs: np.ndarray   # ... at this offset
+    done_blocks: np.ndarray   # blocks whose last token this forward writes: quantized from ...
+    done_slots: np.ndarray    # ... their staging slot
+    whole_blocks: np.ndarray  # blocks this forward writes entirely, never staged: quantized from ...
+    whole_rows: np.ndarray    # ... these rows, B per block
+    tails: np.ndarray         # per sequence: slot of its partial last block, -1 when that block is full
+
+
+def plan_staging(book: StagingBook, slots_cpu: list[int], query_starts: list[int], context_lens: list[int],
+                 B: int) -> _StagingPlan:
+    """Classify the blocks a forward writes (reference engine/quant_cache.py:84-122, same outcome): in order of
+    their first token, a block that is written entirely by this forward and holds no slot is quantized directly;
+    every other block goes through staging (a slot assigned on its first staged token) and is quantized from its
+    slot, which is then released, when this forward writes its last offset. Slots are assigned before any is
+    released, so no slot serves two blocks within one forward."""
+    slots = np.asarray(slots_cpu, dtype=np.int64)
+    blk, off = slots // B, slots % B
+    uniq, first, inv, count = np.unique(blk, return_index=True, return_inverse=True, return_counts=True)
+    order = np.argsort(first, kind="stable")          # unique blocks by first token
+    rank = np.empty_like(order)
+    rank[order] = np.arange(order.size)
+    rows = np.argsort(rank[inv], kind="stable")       # token rows grouped by block, token order inside a group
+    sizes = count[order]
+    ends = np.cumsum(sizes)
+    blocks = uniq[order]
+    first_off, last_off = off[rows[ends - sizes]], off[rows[ends - 1]]
+    held = np.fromiter((b in book.slot_of for b in blocks.tolist()), dtype=bool, count=blocks.size)
+    whole = (first_off == 0) & (sizes == B) & ~held
+    book.assign(blocks[~whole & ~held].tolist())
+    slot_of_block = np.fromiter((book.slot_of.get(b, -1) for b in blocks.tolist()), dtype=np.int64,
+                                count=blocks.size)
+    group = np.repeat(np.arange(blocks.size), sizes)  # position of each grouped row's block
+    staged = ~whole[group]
+    done = ~whole & (last_off == B - 1)
+    plan = _StagingPlan(rows[staged], slot_of_block[group][staged], off[rows[staged]], blocks[done],
+                        slot_of_block[done], blocks[whole], rows[whole[group]], np.empty(0, dtype=np.int64))
+    book.release(plan.done_blocks.tolist())
+    last_block = blk[np.asarray(query_starts[1:], dtype=np.int64) - 1]
+    ctx = np.asarray(context_lens, dtype=np.int64)
+    plan.tails = np.array([book.slot_of[b] if c % B else -1 for b, c in zip(last_block.tolist(), ctx.tolist())],
+                          dtype=np.int64)
+    return plan
 
 
 class QuantPagedKVCache(PagedKVCache):
@@ -59,28 +153,20 @@ class QuantPagedKVCache(PagedKVCache):
         if fmt == "int8-kchannel":
             if manager is None:
                 raise ValueError("int8-kchannel needs the BlockManager to track partial blocks")
-            self._stage_of: dict[int, int] = {}  # block id -> staging slot
-            self._free_stage = list(reversed(range(n_stage)))  # LIFO, slot 0 handed out first
-            manager.add_free_listener(self._release_blocks)
+            self._book = StagingBook(n_stage)
+            self._stage_of, self._free_stage = self._book.slot_of, self._book.free
+            manager.add_free_listener(self._book.release)
 
     def _allocate(self, shape: tuple, device: str | torch.device, dtype: torch.dtype) -> None:
         """int8 K/V, fp16 scales, and (format B) the bf16 staging slots; all zero-initialised."""
         L, H, N, B, D = shape
-        self.k = torch.zeros(shape, device=device, dtype=torch.int8)
-        self.v = torch.zeros(shape, device=device, dtype=torch.int8)
-        self.v_scale = torch.zeros(L, H, N, B, device=device, dtype=torch.float16)
-        if self.fmt == "int8":
-            self.k_scale = torch.zeros(L, H, N, B, device=device, dtype=torch.float16)
-        else:
-            self.k_scale = torch.zeros(L, H, N, D, device=device, dtype=torch.float16)
-            self.stage = torch.zeros(L, H, self.n_stage, B, D, device=device, dtype=torch.bfloat16)
-
-    def _release_blocks(self, blocks: list[int]) -> None:
-        """BlockManager listener: freed blocks give back their staging slots."""
-        for b in blocks:
-            slot = self._stage_of.pop(b, None)
-            if slot is not None:
-                self._free_stage.append(slot)
+        per_token = (L, H, N, B)
+        buffers = {"k": (shape, torch.int8), "v": (shape, torch.int8), "v_scale": (per_token, torch.float16),
+                   "k_scale": (per_token if self.fmt == "int8" else (L, H, N, D), torch.float16)}
+        if self.fmt == "int8-kchannel":
+            buffers["stage"] = ((L, H, self.n_stage, B, D), torch.bfloat16)
+        for name, (shp, dt) in buffers.items():
+            setattr(self, name, torch.zeros(shp, device=device, dtype=dt))
 
     def use_static_plan(self, buffers: tuple | None) -> None:
         """For decode steps replayed from graphs (engine/graph_runner.py): begin() binds format B's staging plan to
@@ -96,26 +182,13 @@ class QuantPagedKVCache(PagedKVCache):
         block quantization (the row writing a block's last token quantizes it from its slot into the block and
         gives the slot back; every other row's quantization goes to scratch_block, which only padding rows read),
         and its tail slot (-1 once the block is full). Same slots and values as begin() plans for the same rows."""
-        B = self.block_size
-        slots, src, dst, tails, done = [], [], [], [], []
-        for b, off in zip(blocks, offsets):
-            slot = self._stage_of.get(b)
-            if slot is None:
-                if not self._free_stage:
-                    raise RuntimeError("out of INT8 staging slots; raise n_stage")
-                slot = self._stage_of[b] = self._free_stage.pop()
-            slots.append(slot)
-            src.append(slot)
-            if off == B - 1:
-                dst.append(b)
-                tails.append(-1)
-                done.append(b)
-            else:
-                dst.append(scratch_block)
-                tails.append(slot)
-        for b in done:
-            self._free_stage.append(self._stage_of.pop(b))
-        return slots, src, dst, tails
+        last = self.block_size - 1
+        slots = [self._book.slot(b) for b in blocks]
+        completes = [off == last for off in offsets]
+        dst = [b if c else scratch_block for b, c in zip(blocks, completes)]
+        tails = [-1 if c else s for s, c in zip(slots, completes)]
+        self._book.release([b for b, c in zip(blocks, completes) if c])
+        return slots, list(slots), dst, tails
 
     def begin(self, n_tokens: int, meta: PagedMetadata | None) -> None:
         """Base bookkeeping, then (format B) the staging plan of every block this forward writes."""
@@ -130,85 +203,72 @@ class QuantPagedKVCache(PagedKVCache):
             self._direct = None
             self._tails = self._tails_dec = self._tails_pf = tails[:T]
             return
-        B, dev = self.block_size, meta.positions.device
-        rows_of: dict[int, list[tuple[int, int]]] = {}  # block -> [(token row, offset)] in token order
-        for row, slot in enumerate(meta.slots_cpu):
-            rows_of.setdefault(slot // B, []).append((row, slot % B))
-        staged_rows, staged_slots, staged_offs, done, direct, direct_rows = [], [], [], [], [], []
-        for b, items in rows_of.items():
-            whole = items[0][1] == 0 and len(items) == B
-            if whole and b not in self._stage_of:
-                direct.append(b)  # written whole by this forward: quantized straight from k, never staged
-                direct_rows.extend(r for r, _ in items)
-                continue
-            if b not in self._stage_of:
-                if not self._free_stage:
-                    raise RuntimeError("out of INT8 staging slots; raise n_stage")
-                self._stage_of[b] = self._free_stage.pop()
-            slot = self._stage_of[b]
-            staged_rows.extend(r for r, _ in items)
-            staged_slots.extend([slot] * len(items))
-            staged_offs.extend(o for _, o in items)
-            if items[-1][1] == B - 1:
-                done.append(b)
-
-        done_slots = [self._stage_of[b] for b in done]
-        for b in done:  # free now: nothing reassigns a slot before the next forward's begin()
-            self._free_stage.append(self._stage_of.pop(b))
-        # Per sequence: the staging slot of its partial last block, -1 if the last block is full (the last block
-        # is the one holding the sequence's last new token).
-        last_slots = [meta.slots_cpu[e - 1] for e in meta.query_starts[1:]]
-        tails = [self._stage_of[last_slots[i] // B] if ctx % B else -1 for i, ctx in enumerate(meta.context_lens)]
+        plan = plan_staging(self._book, meta.slots_cpu, meta.query_starts, meta.context_lens, self.block_size)
         # The whole plan in one host array and one asynchronous copy from pinned memory (separate uploads from
         # pageable lists would each hold the host until the device has caught up).
-        parts = (staged_rows, staged_slots, staged_offs, done, done_slots, direct, direct_rows, tails)
-        flat = torch.tensor([x for part in parts for x in part], dtype=torch.int64)
+        parts = (plan.staged_rows, plan.staged_slots, plan.staged_offs, plan.done_blocks, plan.done_slots,
+                 plan.whole_blocks, plan.whole_rows, plan.tails)
+        flat = torch.from_numpy(np.concatenate(parts))
+        dev = meta.positions.device
         if dev.type == "cuda":
             flat = flat.pin_memory().to(dev, non_blocking=True)
-        views = torch.split(flat, [len(part) for part in parts])
-        self._staged = views[0:3] if staged_rows else None
-        self._done = views[3:5] if done else None
-        self._direct = views[5:7] if direct else None
+        views = torch.split(flat, [p.size for p in parts])
+        self._staged = views[0:3] if plan.staged_rows.size else None
+        self._done = views[3:5] if plan.done_blocks.size else None
+        self._direct = views[5:7] if plan.whole_blocks.size else None
         self._tails = views[7].to(torch.int32)
-        if self._decode is not None and len(self._decode_seqs) != meta.num_seqs:
-            self._tails_dec = self._tails[torch.tensor(self._decode_seqs, device=dev)]
-        else:
-            self._tails_dec = self._tails
-        if self._prefill_launch is not None and len(self._prefill_seqs) != meta.num_seqs:
-            self._tails_pf = self._tails[torch.tensor(self._prefill_seqs, device=dev)]
-        else:
-            self._tails_pf = self._tails
+        self._tails_dec = self._rows_of(self._tails, getattr(self, "_decode_seqs", None), self._decode, dev)
+        self._tails_pf = self._rows_of(self._tails, getattr(self, "_prefill_seqs", None), self._prefill_launch, dev)
+
+    def _rows_of(self, per_seq: torch.Tensor, seqs: list[int] | None, used, dev) -> torch.Tensor:
+        """per_seq restricted to the sequences a kernel launch of this forward covers (all of them: itself)."""
+        if used is None or seqs is None or len(seqs) == per_seq.numel():
+            return per_seq
+        return per_seq[torch.tensor(seqs, device=dev)]
+
+    # ---- writes ------------------------------------------------------------------------------------------------
 
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """Quantize and store this forward's k, v [T, H_kv, d]."""
         if self.fused_writes:
             self._write_fused(layer, k, v)
-            return
-        m = self.meta
-        vq, vs = quantize_per_token(v)
-        self.v[layer][:, m.slot_blocks, m.slot_offsets] = vq.transpose(0, 1)
-        self.v_scale[layer][:, m.slot_blocks, m.slot_offsets] = vs.t()
-        if self.fmt == "int8":
-            kq, ks = quantize_per_token(k)
-            self.k[layer][:, m.slot_blocks, m.slot_offsets] = kq.transpose(0, 1)
-            self.k_scale[layer][:, m.slot_blocks, m.slot_offsets] = ks.t()
-            return
-        # Every path quantizes the bf16-rounded K, so a block's int8 contents do not depend on its chunking.
-        if self._staged is not None:
-            rows, slots, offs = self._staged
-            self.stage[layer][:, slots, offs] = k[rows].transpose(0, 1).to(torch.bfloat16)
+        else:
+            self._write_torch(layer, k, v)
+
+    def _token_store(self, codes_pool: torch.Tensor, scale_pool: torch.Tensor, x: torch.Tensor) -> None:
+        """Per-token quantization of x [T, H, d] into one layer's pools at this forward's slots."""
+        codes, scales = quantize_per_token(x)
+        where = (slice(None), self.meta.slot_blocks, self.meta.slot_offsets)
+        codes_pool[where] = codes.transpose(0, 1)
+        scale_pool[where] = scales.transpose(0, 1)
+
+    def _k_block_sources(self, layer: int, k16: torch.Tensor):
+        """(destination blocks, their [H, n, B, d] bf16 tiles) for the K blocks format B quantizes this forward:
+        completed blocks from their staging slots, whole blocks from the forward's rows."""
         if self._done is not None:
             blocks, slots = self._done
-            kq, ks = quantize_per_channel(self.stage[layer][:, slots], dim=2)  # [H, n, B, d] over the B tokens
-            self.k[layer][:, blocks] = kq
-            self.k_scale[layer][:, blocks] = ks
+            yield blocks, self.stage[layer][:, slots]
         if self._direct is not None:
             blocks, rows = self._direct
-            H, d = k.shape[1], k.shape[2]
-            whole = k[rows].view(-1, self.block_size, H, d).permute(2, 0, 1, 3).to(torch.bfloat16)  # [H, n, B, d]
-            kq, ks = quantize_per_channel(whole, dim=2)
-            self.k[layer][:, blocks] = kq
-            self.k_scale[layer][:, blocks] = ks
+            H, d = k16.shape[1], k16.shape[2]
+            yield blocks, k16[rows].view(-1, self.block_size, H, d).permute(2, 0, 1, 3)
+
+    def _write_torch(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """write() with the torch quantizer (CPU pools, or fused_writes = False)."""
+        self._token_store(self.v[layer], self.v_scale[layer], v)
+        if self.fmt == "int8":
+            self._token_store(self.k[layer], self.k_scale[layer], k)
+            return
+        # Staging holds bf16, and whole blocks are rounded to bf16 too: a block's codes do not depend on whether
+        # it was staged token by token or written in one forward.
+        k16 = k.to(torch.bfloat16)
+        if self._staged is not None:
+            rows, slots, offs = self._staged
+            self.stage[layer][:, slots, offs] = k16[rows].transpose(0, 1)
+        for blocks, tiles in self._k_block_sources(layer, k16):
+            codes, scales = quantize_per_channel(tiles, dim=2)  # one scale per (head, block, channel)
+            self.k[layer][:, blocks] = codes
+            self.k_scale[layer][:, blocks] = scales
 
     def _write_fused(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """write() through the HIP kernels: one launch per step below."""
@@ -230,18 +290,21 @@ class QuantPagedKVCache(PagedKVCache):
             blocks, rows = self._direct
             quantize_store_block_rows(k, rows, blocks, self.k[layer], self.k_scale[layer])
 
+    # ---- reads -------------------------------------------------------------------------------------------------
+
     def gather(self, layer: int, seq: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Sequence seq's dequantized K, V as [H_kv, context_len, d] in the model dtype."""
-        m, (H, d), B = self.meta, (self.cfg.num_kv_heads, self.cfg.head_dim), self.block_size
-        ctx, blocks = m.context_lens[seq], m.block_ids[seq]
-        v = dequantize(self.v[layer][:, blocks], self.v_scale[layer][:, blocks][..., None], self.dtype)
-        if self.fmt == "int8":
-            k = dequantize(self.k[layer][:, blocks], self.k_scale[layer][:, blocks][..., None], self.dtype)
-        else:
-            k = dequantize(self.k[layer][:, blocks], self.k_scale[layer][:, blocks][:, :, None], self.dtype)
-            if ctx % B:
-                k[:, -1] = self.stage[layer][:, self._stage_of[m.block_ids_cpu[seq][-1]]].to(self.dtype)
-        return k.view(H, -1, d)[:, :ctx], v.view(H, -1, d)[:, :ctx]
+        meta, B = self.meta, self.block_size
+        n, ids = meta.context_lens[seq], meta.block_ids[seq]
+        H, d = self.cfg.num_kv_heads, self.cfg.head_dim
+        # Scales broadcast over the channels (per token) or over the tokens of a block (per channel).
+        v = dequantize(self.v[layer][:, ids], self.v_scale[layer][:, ids].unsqueeze(-1), self.dtype)
+        k_axis = -1 if self.fmt == "int8" else 2
+        k = dequantize(self.k[layer][:, ids], self.k_scale[layer][:, ids].unsqueeze(k_axis), self.dtype)
+        if self.fmt == "int8-kchannel" and n % B:  # the partial last block is in its staging slot
+            slot = self._stage_of[meta.block_ids_cpu[seq][-1]]
+            k[:, -1] = self.stage[layer][:, slot].to(self.dtype)
+        return k.reshape(H, -1, d)[:, :n], v.reshape(H, -1, d)[:, :n]
 
     def _prefill_quant(self, layer: int) -> QuantKV:
         """Scales (and format B's staging, with the tail slots of the forward's multi-token rows) for the prefill
