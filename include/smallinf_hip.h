@@ -155,6 +155,19 @@ int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32
 int32_t sipa_decode(const sipa_decode_params* p, void* stream);
 
 /*
+ * sipa_decode without a caller-supplied workspace, for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference. The same
+ * kernels and launches as sipa_decode (identical results for identical parameters); p->workspace and
+ * p->workspace_bytes are ignored. The split partials and merge counters live in a 16 MiB device array inside the
+ * library (one per GPU, held until the process ends; the first call on a GPU also launches one small kernel that
+ * zeroes its counters). A call whose splits need more than that (sipa_decode_workspace_bytes() > 16 MiB) fails with
+ * SIPA_EWORKSPACE before launching anything. Allocates nothing: no hipMalloc, hipFree or allocating library call.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (different streams, or
+ * threads) race and give wrong results; order them on one stream.
+ */
+int32_t sipa_decode_noalloc(const sipa_decode_params* p, void* stream);
+
+/*
  * Paged attention for multi-token rows (prefill chunks): replaces the reference's gather path for rows with
  * several new tokens (reference engine/paged_cache.py:149-155,174-175 with engine/attention.py:6-28). For each
  * sequence s, rows query_starts[s] .. query_starts[s] + query_lens[s] - 1 of q are its new tokens at positions

@@ -40,6 +40,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <cstddef>
+#include <mutex>
 #include <vector>
 
 #include "decode_common.h"
@@ -662,7 +663,53 @@ extern "C" int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_h
   return workspace_layout(num_seqs, num_q_heads, num_kv_heads, head_dim, num_splits).total;
 }
 
-extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
+// ---- the allocation-free entry point's split workspace -----------------------------------------------------------
+
+// sipa_decode_noalloc keeps its split partials and merge counters here: a file-scope device array, one copy per GPU
+// the library runs on, held until the process ends. In host code the name is only a handle for
+// hipGetSymbolAddress; every host use goes through the per-device address scratch_on_current_device() returns.
+constexpr int64_t kScratchBytes = 16ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+__global__ void __launch_bounds__(256) zero_words(int32_t* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
+static std::mutex g_scratch_lock;
+static void* g_scratch_ptr[64];  // per device: the array's address, NULL until that device's first call
+
+// The scratch array of the current device. Its first call on a device looks up the array's address and zeroes the
+// merge-counter region with a fill kernel on `st` (a kernel, not a memset, so that a first call under stream capture
+// records a kernel node); later calls reuse both.
+static int scratch_on_current_device(hipStream_t st, char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SIPA_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  SIPA_CHECK(dev >= 0 && dev < 64, SIPA_EUNSUPPORTED, "device %d: the allocation-free entry serves devices 0..63", dev);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(SIPA_EHIP, "address of the scratch array on device %d: %s", dev, hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, (int32_t*)ptr, kMaxCounters);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(SIPA_EHIP, "clearing the scratch counters: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = (char*)g_scratch_ptr[dev];
+  return SIPA_OK;
+}
+
+static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scratch);
+
+extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) { return decode_impl(p, stream, false); }
+
+extern "C" int32_t sipa_decode_noalloc(const sipa_decode_params* p, void* stream) {
+  return decode_impl(p, stream, true);
+}
+
+static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scratch) {
   SIPA_CHECK(p != nullptr, SIPA_EINVAL, "params is NULL");
   SIPA_CHECK(p->struct_size == (int32_t)sizeof(sipa_decode_params), SIPA_EINVAL,
              "struct_size %d does not match this library's sipa_decode_params (%d bytes, ABI %d)", p->struct_size,
@@ -760,16 +807,27 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
   a.fused = n_items > 0 || p->combine == SIPA_COMBINE_FUSED;  // a work list always merges in place
   a.scale_log2 = p->scale * 1.4426950408889634f;
 
+  hipStream_t st = (hipStream_t)stream;
   if (splits > 1) {
     SIPA_CHECK((int64_t)S * Hkv <= kMaxCounters, SIPA_EINVAL,
                "%lld (sequence, KV head) pairs exceed the %d merge counters of a split launch", (long long)S * Hkv,
                kMaxCounters);
     const WorkspaceLayout w = workspace_layout(S, Hq, Hkv, D, splits);
-    SIPA_CHECK(p->workspace != nullptr && p->workspace_bytes >= w.total, SIPA_EWORKSPACE,
-               "workspace of %lld bytes needed for %d splits (got %lld)", (long long)w.total, splits,
-               (long long)p->workspace_bytes);
-    SIPA_CHECK(((uintptr_t)p->workspace & 255) == 0, SIPA_EWORKSPACE, "workspace must be 256-byte aligned");
-    char* base = (char*)p->workspace;
+    char* base = nullptr;
+    if (use_scratch) {
+      SIPA_CHECK(w.total <= kScratchBytes, SIPA_EWORKSPACE,
+                 "%d splits of %d sequences x %d query heads need a %lld-byte workspace; the allocation-free entry "
+                 "holds %lld (use sipa_decode with a workspace, or fewer splits)", splits, S, Hq, (long long)w.total,
+                 (long long)kScratchBytes);
+      const int rc = scratch_on_current_device(st, &base);
+      if (rc != SIPA_OK) return rc;
+    } else {
+      SIPA_CHECK(p->workspace != nullptr && p->workspace_bytes >= w.total, SIPA_EWORKSPACE,
+                 "workspace of %lld bytes needed for %d splits (got %lld)", (long long)w.total, splits,
+                 (long long)p->workspace_bytes);
+      SIPA_CHECK(((uintptr_t)p->workspace & 255) == 0, SIPA_EWORKSPACE, "workspace must be 256-byte aligned");
+      base = (char*)p->workspace;
+    }
     a.counters = (int32_t*)(base + w.counters);
     a.pm = (float*)(base + w.pm);
     a.pl = (float*)(base + w.pl);
@@ -803,7 +861,6 @@ extern "C" int32_t sipa_decode(const sipa_decode_params* p, void* stream) {
              "(or fp32 channel scales with a zero block stride)");
   const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
 
-  hipStream_t st = (hipStream_t)stream;
   const int64_t wgs = n_items > 0 ? (int64_t)n_items : (int64_t)S * Hkv * splits;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   const dim3 grid((unsigned)wgs);

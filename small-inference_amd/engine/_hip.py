@@ -77,6 +77,7 @@ SIGNATURES = {
     "sipa_split_chunk": (i32, [i32, i32]),
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
+    "sipa_decode_noalloc": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp]),
     "sipa_check_work_list": (i32, [vp, i32, i32, i32, i32, i32]),
     "sipa_prefill": (i32, [_c.POINTER(PrefillParams), vp]),
