@@ -4,7 +4,9 @@
 Metric: paged-decode HBM GB/s and fraction of the 8 TB/s peak, and µs per call. Workload (config
 C2): one layer of Qwen2.5-0.5B attention (14 query heads, 2 KV heads, head_dim 64), 16-token blocks, batch 32 x
 8192 context, bf16 N(0, 1) Q/K/V from a fixed seed, block tables a random permutation of a 32768-block pool. A step
-is one paged_decode_attention call over the whole batch (the CU-count split policy with the fused split merge).
+is one pass over the pool's rotated layers: one paged_decode_attention call per layer (8 calls by default, as a
+decode step makes one call per layer), each over the whole batch with the CU-count split policy and the fused split
+merge. `value` (GB/s) and `config.us_per_call` are per call; `ms_per_step` covers the step's calls.
 
 Bytes per call are algorithmic: K and V actually read from the pool plus Q and O (512 B per token + 3,584 B per
 sequence for 0.5B); block tables and split partials are not counted. Calls rotate over 8 layers of a
@@ -724,8 +726,8 @@ def calibrate_copy(mib: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100, help="timed steps (each one call per rotated layer)")
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=8, help="pool layers the calls rotate over (defeats the MALL)")
     ap.add_argument("--splits", type=int, default=None, help="force a split count (default: CU-count policy)")
     ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "valu"])
@@ -789,10 +791,12 @@ def main() -> int:
 
     wl = bf16_decode("c2", [8192] * 32, 32768, layers=args.layers, splits=args.splits, impl=args.impl,
                      combine=args.combine)
-    # The timed region: K back-to-back launches on the launch stream, HIP events at both ends. Each call is one
-    # kernel (the split merge is fused), so region / K is the kernel's average duration plus the dispatch gap
-    # between consecutive kernels; rocprofv3's kernel trace of the same command agrees to about 1%.
-    ms, _ = time_calls(wl.call, args.steps, args.warmup, per_launch=False)
+    # The timed region: K steps of `layers` back-to-back launches each on the launch stream, HIP events at both
+    # ends. Each call is one kernel (the split merge is fused), so region / (K x layers) is the kernel's average
+    # duration plus the dispatch gap between consecutive kernels; rocprofv3's kernel trace of the same command
+    # agrees to about 1%.
+    calls = args.steps * args.layers
+    ms, _ = time_calls(wl.call, calls, args.warmup * args.layers, per_launch=False)  # ms per call
     kern_us = ms * 1e3
     _, pair_us = time_calls(wl.call, min(args.steps, 200), 0, per_launch=True)
     value = wl.bytes / (ms * 1e-3) / 1e9
@@ -811,7 +815,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(ms * args.layers, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -822,7 +826,8 @@ def main() -> int:
                    "batch": 32, "context": 8192, "block_size": 16, "q_heads": 14, "kv_heads": 2, "head_dim": 64,
                    "splits": wl.plan.splits, "split_tokens": wl.plan.chunk, "impl": args.impl,
                    "combine": args.combine, "layers_rotated": args.layers, "cu_count": cu,
-                   "bytes_per_call": wl.bytes, "us_per_call": round(ms * 1e3, 2),
+                   "bytes_per_call": wl.bytes, "us_per_call": round(ms * 1e3, 2), "calls_per_step": args.layers,
+                   "timed_calls": calls,
                    "max_abs_vs_fp32_oracle": round(err, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
