@@ -730,7 +730,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=8, help="pool layers the calls rotate over (defeats the MALL)")
     ap.add_argument("--splits", type=int, default=None, help="force a split count (default: CU-count policy)")
-    ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "valu"])
+    ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "valu", "valu_stream", "valu_dot2"])
     ap.add_argument("--combine", default="fused", choices=["fused", "kernel"])
     ap.add_argument("--details", dest="details", action="store_true", default=True)
     ap.add_argument("--no-details", dest="details", action="store_false")
@@ -771,7 +771,9 @@ def main() -> int:
     if args.c4:
         res = {}
         for fmt, key in (("int8", "c4b_int8_per_token"), ("int8-kchannel", "c4a_int8_kchannel")):
-            wl = int8_decode(key, fmt, [4096] * 64, 32768)
+            if args.impl not in ("auto", "mfma") and fmt != "int8":
+                continue  # the VALU streaming kernels cover the per-token format only
+            wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl)
             res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
             del wl
             torch.cuda.empty_cache()

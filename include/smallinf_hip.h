@@ -44,8 +44,11 @@ enum {
                              block of K in a bf16 staging slot; int8 V with one scale per token */
 };
 
-/* impl of sipa_decode_params */
-enum { SIPA_IMPL_AUTO = 0, SIPA_IMPL_VALU = 1, SIPA_IMPL_MFMA = 2 };
+/* impl of sipa_decode_params: AUTO picks MFMA where it applies, else the VALU fallback (any supported shape).
+   VALU_STREAM / VALU_DOT2: the MFMA kernels' streaming structure with the dot products on the vector ALUs, fp32
+   FMAs or v_dot2 pair products (bf16 q, block 16, head_dim 64/128, group 6-8, bf16 or int8 per-token pools); they
+   exist to measure the matrix cores against the VALU and are never picked by AUTO. */
+enum { SIPA_IMPL_AUTO = 0, SIPA_IMPL_VALU = 1, SIPA_IMPL_MFMA = 2, SIPA_IMPL_VALU_STREAM = 3, SIPA_IMPL_VALU_DOT2 = 4 };
 
 /* combine of sipa_decode_params */
 enum { SIPA_COMBINE_FUSED = 0, SIPA_COMBINE_KERNEL = 1 };

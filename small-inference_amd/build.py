@@ -17,7 +17,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "build"
 LIB = OUT_DIR / "libsmallinf_hip.so"
-SOURCES = ["capi.hip", "decode.hip", "decode_int8.hip", "metadata.hip", "prefill.hip", "quant_store.hip"]
+SOURCES = ["capi.hip", "decode.hip", "decode_int8.hip", "decode_valu_stream.hip", "metadata.hip", "prefill.hip",
+           "quant_store.hip"]
 PROBE_LIB = OUT_DIR / "libsmallinf_probe.so"  # measurement kernels for bench.py, outside the product ABI
 PROBE_SOURCES = ["probe.hip"]
 ARCH = "gfx950"

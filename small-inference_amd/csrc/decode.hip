@@ -856,16 +856,27 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
                 p->ks_stride_n % 8 == 0;
     }
   }
+  const bool valu_stream = p->impl == SIPA_IMPL_VALU_STREAM || p->impl == SIPA_IMPL_VALU_DOT2;
+  if (valu_stream) {
+    const bool tok_scales = mode == SIPA_KV_PLAIN ||
+                            (mode == SIPA_KV_INT8_TOKEN && p->k_scale_dtype == SIPA_F16 && p->v_scale_dtype == SIPA_F16);
+    SIPA_CHECK(p->q_dtype == SIPA_BF16 && B == 16 && q_aligned && tok_scales &&
+                   valu_stream_supported(D, G, mode, p->impl == SIPA_IMPL_VALU_DOT2),
+               SIPA_EUNSUPPORTED, "the VALU streaming kernels need a bf16 query, block 16, head_dim 64/128, a group "
+               "of 6-8, a bf16 pool or an int8 per-token pool with fp16 scales, and 16-byte aligned rows");
+  }
   SIPA_CHECK(p->impl != SIPA_IMPL_MFMA || mfma_ok, SIPA_EUNSUPPORTED,
              "the MFMA kernels need a bf16 query, block 16, head_dim 64/128, 16-byte aligned rows and fp16 scales "
              "(or fp32 channel scales with a zero block stride)");
-  const bool use_mfma = mfma_ok && p->impl != SIPA_IMPL_VALU;
+  const bool use_mfma = mfma_ok && (p->impl == SIPA_IMPL_AUTO || p->impl == SIPA_IMPL_MFMA);
 
   const int64_t wgs = n_items > 0 ? (int64_t)n_items : (int64_t)S * Hkv * splits;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   const dim3 grid((unsigned)wgs);
   int rc;
-  if (use_mfma && mode == SIPA_KV_PLAIN)
+  if (valu_stream)
+    rc = launch_valu_stream(D, G, mode, p->impl == SIPA_IMPL_VALU_DOT2, grid, a, st);
+  else if (use_mfma && mode == SIPA_KV_PLAIN)
     rc = launch_mfma(D, prefetch_tiles(D), grid, a, st);
   else if (use_mfma)
     rc = launch_mfma_int8(D, int8_variant, prefetch_tiles(D), grid, a, st);

@@ -404,6 +404,11 @@ __device__ __forceinline__ void mfma_epilogue(const DecodeArgs& a, int s, int h,
   publish_and_merge<D, OUT_F32>(a, s, h, nvalid, last_flag);
 }
 
+// VALU streaming kernels (decode_valu_stream.hip): bf16 q, 16-token blocks, head_dim 64/128, groups of 6-8, pools
+// in bf16 (mode 0) or int8 per token (mode 1); dot = 0: fp32 FMAs, 1: v_dot2 pair products.
+bool valu_stream_supported(int D, int G, int mode, int dot);
+int launch_valu_stream(int D, int G, int mode, int dot, dim3 grid, const DecodeArgs& a, hipStream_t st);
+
 // INT8 MFMA kernels (decode_int8.hip). mode: 1 per-token K scales, 2 per-(block, channel) K scales,
 // 3 per-(head, channel) K scales (mode 2 with a zero block stride). nb: tiles in flight per wave.
 int launch_mfma_int8(int D, int mode, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st);

@@ -25,7 +25,7 @@ F32, BF16, F16, I8 = 0, 1, 2, 3
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, -1, -2, -3, -4
 # kv modes, implementations, combine strategies
 KV_PLAIN, KV_INT8_TOKEN, KV_INT8_KCHAN = 0, 1, 2
-IMPL = {"auto": 0, "valu": 1, "mfma": 2}
+IMPL = {"auto": 0, "valu": 1, "mfma": 2, "valu_stream": 3, "valu_dot2": 4}
 COMBINE = {"fused": 0, "kernel": 1}
 
 _c = ctypes

@@ -256,3 +256,12 @@ def test_table_narrower_than_max_context_is_refused():
         paged_decode_attention(q, k, v, bt[:, :10], ctx, D ** -0.5, 300)
     with pytest.raises(ValueError):
         paged_decode_attention(q, k, v, bt, ctx[:1], D ** -0.5, 300)
+
+
+@pytest.mark.parametrize("heads", list(HEADS))
+@pytest.mark.parametrize("impl", ["valu_stream", "valu_dot2"])
+@pytest.mark.parametrize("splits", [1, 3, None], ids=["single", "split3", "auto"])
+def test_valu_streaming_kernels_match_oracle(heads, impl, splits):
+    """The VALU streaming kernels (the matrix-core A/B competitors: fp32 FMAs, v_dot2 pairs) on bf16 pools, ragged
+    lengths with partial blocks and tiles, against the oracle to the north-star bound."""
+    run(RAGGED + [2100, 64], heads, 16, torch.bfloat16, splits, impl=impl)

@@ -350,6 +350,23 @@ def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
         assert err32 <= 8e-3, f"fp32 max-abs {err32:.3e}"
 
 
+@pytest.mark.parametrize("heads", list(HEADS))
+@pytest.mark.parametrize("impl", ["valu_stream", "valu_dot2"])
+@pytest.mark.parametrize("splits", [1, None], ids=["single", "auto"])
+def test_int8_valu_streaming_kernels_match_oracle(heads, impl, splits):
+    """The VALU streaming kernels on per-token INT8 pools (codes used with a +128 bias that the score and the
+    output remove again), against the oracle's dequantize-then-attend with outlier K channels."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [1, 15, 16, 17, 33, 100, 700, 2100]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, "int8", seed=15)
+    print(f"case int8 {heads} {impl} splits={splits}", flush=True)
+    out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                 max(lengths), num_splits=splits, quant=quant, impl=impl)
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    assert_decode_close(out.double().cpu().numpy(), ref, f"int8 {heads} {impl} splits={splits}")
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_int8_context_longer_than_one_split_holds(fmt):
     """The INT8 kernels stage the token scales of at most 4,096 tokens per split: a 9,000-token sequence asked
