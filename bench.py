@@ -258,7 +258,7 @@ def cpu_path(wl, budget_s: float = 2.0) -> dict:
 # ---- detail workloads ----------------------------------------------------------------------------------------------
 
 def int8_decode(name, fmt, lengths, N, Hq=12, Hkv=2, D=128, B=16, layers=4, seed=0, impl="auto",
-                f32_channel_scales=False, work_list="auto"):
+                f32_channel_scales=False, work_list="auto", splits=None):
     """1.5B-shaped INT8 pools built by the HIP quantize-and-store kernels from bf16 K ~ N(0, 1) with 4 of 128
     channels per head scaled by U[20, 68] and V ~ N(0, 1) (config C4)."""
     from engine.hip_decode import QuantKV
@@ -309,7 +309,7 @@ def int8_decode(name, fmt, lengths, N, Hq=12, Hkv=2, D=128, B=16, layers=4, seed
         quant = [QuantKV(2, kscale[i], vs[i], stage, tails) for i in range(layers)]
         per_token = Hkv * (D + 2) + Hkv * (D + 2 * D / B)
     nbytes = int(per_token * sum(lengths)) + 2 * Hq * D * 2 * len(lengths)
-    wl = Decode(name, q, kq, vq, bt, ctx_t, lengths, D ** -0.5, nbytes, None, quant, impl=impl, work_list=work_list,
+    wl = Decode(name, q, kq, vq, bt, ctx_t, lengths, D ** -0.5, nbytes, splits, quant, impl=impl, work_list=work_list,
                 meta={"batch": len(lengths), "context": max(lengths), "format": fmt,
                       "k_scales": "fp32 per (head, channel)" if f32_channel_scales else "fp16 per (block, channel)"
                       if fmt != "int8" else "fp16 per token"})

@@ -32,6 +32,10 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}", "-mc
          # MFMA accumulators in VGPRs: the default AGPR form makes the compiler copy every accumulator between
          # AGPRs and VGPRs around the softmax rescale of each key tile.
          "-mllvm", "-amdgpu-mfma-vgpr-form",
+         # Leading scalar kernel arguments are preloaded into SGPRs at wave launch (the bf16 decode kernel passes
+         # the fields of its first memory round trip that way); kernels whose leading argument is a struct are
+         # unaffected.
+         "-mllvm", "-amdgpu-kernarg-preload-count=16",
          "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas"]
 
 

@@ -48,7 +48,11 @@
 namespace sipa {
 
 template <int D, int NB>  // NB: tiles in flight per wave (the register prefetch ring)
-__global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __restrict__ hbt,
+                                                             const int32_t* __restrict__ hctx,
+                                                             const int32_t* __restrict__ hitems, int32_t hbt_ss,
+                                                             int32_t hSH, int32_t hS, int32_t hchunk,
+                                                             int32_t hmax_ctx, int32_t hbt_w, const DecodeArgs a) {
   constexpr int KS = D / 32;  // QK k-steps per block
   constexpr int DT = D / 16;  // PV d-tiles
   constexpr int VC = D / 32;  // 16-byte V chunks per lane per block
@@ -58,7 +62,8 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   __shared__ int bids[kMaxSplitBlocks];  // this split's block ids
   __shared__ int last_flag;
 
-  const WorkItem w = work_item(a);
+  const HotArgs hp{hbt, hctx, hitems, hbt_ss, hSH, hS, hchunk, hmax_ctx, hbt_w};
+  const WorkItem w = work_item(hp, a);
   const int sp = w.sp, h = w.h, s = w.s;
   const int start = w.start;
   const int G = a.G;
@@ -66,7 +71,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
   int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(a, s, start, w.end, ids);
+  const int nb_spec = fetch_split_ids(hp.bt, hp.bt_ss, hp.bt_w, s, start, w.end, ids);
   bf16x8 qop[KS];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
@@ -77,10 +82,10 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const DecodeArgs a)
       qop[j] = __builtin_bit_cast(bf16x8, u);
     }
   }
-  const int ctx = context_len(a, s);
+  const int ctx = min(hp.ctx[s], hp.max_ctx);  // as context_len()
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
-  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
+  const int nvalid = w.nvalid < 0 ? (ctx + hp.chunk - 1) / hp.chunk : w.nvalid;
   commit_split_ids(nb_spec, ids, bids, a.nb);
   __syncthreads();  // block ids staged
 
@@ -521,19 +526,29 @@ static int prefetch_tiles(int D) {
   return env > 0 ? env : 2;
 }
 
+// The bf16 kernel takes its prologue's fields as leading scalars (preloaded into SGPRs), then the whole block.
+template <int D, int NB>
+static int launch_bf16(dim3 grid, const DecodeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((decode_mfma_bf16<D, NB>), grid, dim3(kThreads), 0, st, a.bt, a.ctx, a.items, (int32_t)a.bt_ss,
+                     a.S * a.Hkv, a.S, a.chunk, a.max_ctx, a.bt_w, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIPA_EHIP, "decode launch failed: %s", hipGetErrorString(e));
+  return SIPA_OK;
+}
+
 static int launch_mfma(int D, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
   if (D == 64) {
     switch (nb) {
-      case 1: return launch(decode_mfma_bf16<64, 1>, grid, a, st);
-      case 2: return launch(decode_mfma_bf16<64, 2>, grid, a, st);
-      case 3: return launch(decode_mfma_bf16<64, 3>, grid, a, st);
-      default: return launch(decode_mfma_bf16<64, 4>, grid, a, st);
+      case 1: return launch_bf16<64, 1>(grid, a, st);
+      case 2: return launch_bf16<64, 2>(grid, a, st);
+      case 3: return launch_bf16<64, 3>(grid, a, st);
+      default: return launch_bf16<64, 4>(grid, a, st);
     }
   }
   switch (nb) {
-    case 1: return launch(decode_mfma_bf16<128, 1>, grid, a, st);
-    case 2: return launch(decode_mfma_bf16<128, 2>, grid, a, st);
-    default: return launch(decode_mfma_bf16<128, 3>, grid, a, st);
+    case 1: return launch_bf16<128, 1>(grid, a, st);
+    case 2: return launch_bf16<128, 2>(grid, a, st);
+    default: return launch_bf16<128, 3>(grid, a, st);
   }
 }
 
@@ -725,6 +740,8 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
   SIPA_CHECK(B > 0 && 64 % B == 0, SIPA_EINVAL, "block_size %d must divide 64 (block-aligned 64-token tiles)", B);
   SIPA_CHECK(p->max_context > 0, SIPA_EINVAL, "max_context %d must be >= 1", p->max_context);
   SIPA_CHECK(p->num_blocks > 0, SIPA_EINVAL, "num_blocks %d must be >= 1", p->num_blocks);
+  SIPA_CHECK(p->bt_stride_s >= 0 && p->bt_stride_s <= INT32_MAX, SIPA_EINVAL,
+             "block_tables row stride %lld outside [0, 2^31)", (long long)p->bt_stride_s);
   SIPA_CHECK(p->bt_width > 0 && (int64_t)p->bt_width * B >= p->max_context, SIPA_EINVAL,
              "block_tables rows of %d entries cannot cover max_context %d (block size %d)", p->bt_width,
              p->max_context, B);

@@ -91,6 +91,37 @@ __device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
   return WorkItem{sh % a.S, sh / a.S, sp, sp * a.chunk, min(sp * a.chunk + a.chunk, a.max_ctx), -1};
 }
 
+// The fields a bf16 decode workgroup needs before its first K/V load, passed as leading scalar kernel arguments
+// that gfx950 preloads into SGPRs at wave launch (-amdgpu-kernarg-preload-count): the block-table and context-length
+// loads then start without waiting for the kernel-argument fetch (a memory round trip of about 0.5 us).
+struct HotArgs {
+  const int32_t* bt;     // block tables
+  const int32_t* ctx;    // context lengths
+  const int32_t* items;  // work list or NULL
+  int32_t bt_ss;         // block-table row stride (elements)
+  int32_t SH;            // sequences x KV heads
+  int32_t S, chunk, max_ctx, bt_w;
+};
+
+__device__ __forceinline__ WorkItem work_item(const HotArgs& hp, const DecodeArgs& a) {
+  const int L = blockIdx.x;
+  if (hp.items != nullptr) {
+    const int4* it = (const int4*)(hp.items + 8 * (int64_t)L);
+    const int4 x = it[0], y = it[1];
+    WorkItem w;
+    w.s = min(max(x.x, 0), hp.S - 1);
+    w.h = min(max(x.y, 0), hp.SH / hp.S - 1);
+    w.sp = min(max(x.z, 0), a.splits - 1);
+    w.nvalid = min(max(x.w, 1), a.splits);
+    w.start = min(max(y.x, 0), hp.max_ctx);
+    w.end = min(max(y.y, w.start), min(hp.max_ctx, w.start + kMaxSplitBlocks * 16));
+    return w;
+  }
+  const int sh = L % hp.SH;
+  const int sp = L / hp.SH;
+  return WorkItem{sh % hp.S, sh / hp.S, sp, sp * hp.chunk, min(sp * hp.chunk + hp.chunk, hp.max_ctx), -1};
+}
+
 template <bool OUT_F32>
 __device__ __forceinline__ void store_out(const DecodeArgs& a, int s, int hq, int d, float v) {
   const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d;
@@ -304,10 +335,10 @@ struct KVTile {
 // before ctx[s] is known, so that the first K/V loads wait for one memory round trip instead of two.
 constexpr int kIdsPerThread = kMaxSplitBlocks / kThreads;
 
-__device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int end_spec,
-                                               int (&ids)[kIdsPerThread]) {
-  const int nb_spec = min((end_spec - start + 15) >> 4, a.bt_w - (start >> 4));  // never past the row's width
-  const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (start >> 4);
+__device__ __forceinline__ int fetch_split_ids(const int32_t* bt, int64_t bt_ss, int bt_w, int s, int start,
+                                               int end_spec, int (&ids)[kIdsPerThread]) {
+  const int nb_spec = min((end_spec - start + 15) >> 4, bt_w - (start >> 4));  // never past the row's width
+  const int32_t* btr = bt + (int64_t)s * bt_ss + (start >> 4);
 #pragma unroll
   for (int i = 0; i < kIdsPerThread; ++i) {
     const int j = threadIdx.x + kThreads * i;
@@ -317,6 +348,11 @@ __device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int s
 }
 
 // Ids outside the pool are clamped into it: a bad table gives wrong results, never an access out of bounds.
+__device__ __forceinline__ int fetch_split_ids(const DecodeArgs& a, int s, int start, int end_spec,
+                                               int (&ids)[kIdsPerThread]) {
+  return fetch_split_ids(a.bt, a.bt_ss, a.bt_w, s, start, end_spec, ids);
+}
+
 __device__ __forceinline__ void commit_split_ids(int nb_spec, const int (&ids)[kIdsPerThread], int* bids,
                                                  int nblocks) {
 #pragma unroll
