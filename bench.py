@@ -453,6 +453,43 @@ def prefill_bench(steps: int, warmup: int) -> dict:
     return res
 
 
+def paged_read_floor(wl, steps: int, warmup: int) -> dict:
+    """The same call's HBM reads without the decode arithmetic or the split merge (csrc/probe.hip
+    sipa_probe_paged_read: same grid, block-table staging, two 32-token tiles in flight per wave, and the INT8
+    kernels' token-scale reads): the floor a decode kernel of this layout reaches on this access pattern."""
+    lib = ctypes.CDLL(str(ROOT / "small-inference_amd" / "build" / "libsmallinf_probe.so"))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.sipa_probe_paged_read.argtypes = [vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, i64, i64, i64, i64, i32, vp,
+                                          vp]
+    lib.sipa_probe_paged_read.restype = i32
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    k0, esz = wl.k[0], wl.k.element_size()
+    Hkv, N, B, D = k0.shape
+    ctx = max(wl.lengths)
+    assert min(wl.lengths) == ctx, "the floor probe takes a uniform batch"
+    sc = None if wl.quant is None or wl.quant[0].mode != 1 else wl.quant  # per-token scales (format "int8")
+
+    def call(i):
+        layer = i % wl.layers
+        ks = vs = None
+        if sc is not None:
+            ks, vs = sc[layer].k_scale.data_ptr(), sc[layer].v_scale.data_ptr()
+        rc = lib.sipa_probe_paged_read(wl.k[layer].data_ptr(), wl.v[layer].data_ptr(), ks, vs, wl.bt.data_ptr(),
+                                       wl.bt.stride(0), len(wl.lengths), Hkv, ctx, wl.plan.chunk,
+                                       k0.stride(0) * esz, k0.stride(1) * esz, N * B * 2, B * 2, D * esz,
+                                       sink.data_ptr(), stream)
+        if rc:
+            raise RuntimeError(f"sipa_probe_paged_read: {rc}")
+
+    ms, _ = time_calls(call, steps, warmup, per_launch=False)
+    r = {"us_per_call": round(ms * 1e3, 2), "gb_s": round(wl.bytes / (ms * 1e-3) / 1e9, 1),
+         "frac_of_peak": round(wl.bytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "splits": wl.plan.splits,
+         "token_scales": sc is not None}
+    log(f"[bench] {wl.name} paged-read floor: {json.dumps(r)}")
+    return r
+
+
 def stream_ceiling(steps: int) -> dict:
     """Read-only streaming ceiling of this GPU from the probe library (1 GiB buffers, 4 rotating)."""
     lib = ctypes.CDLL(str(ROOT / "small-inference_amd" / "build" / "libsmallinf_probe.so"))
@@ -522,6 +559,8 @@ def details(steps: int, warmup: int) -> dict:
         out[key] = measure(wl, steps, warmup)
         if not f32s:
             out[key].update(cpu_path(wl))
+        if fmt == "int8":
+            out[key]["paged_read_floor"] = paged_read_floor(wl, steps, warmup)
         del wl
         torch.cuda.empty_cache()
     out.update(store_bench(steps))
@@ -775,6 +814,8 @@ def main() -> int:
                 continue  # the VALU streaming kernels cover the per-token format only
             wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl)
             res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
+            if fmt == "int8":
+                res[key]["paged_read_floor"] = paged_read_floor(wl, args.steps, args.warmup)
             del wl
             torch.cuda.empty_cache()
         print(json.dumps(res), flush=True)
@@ -835,7 +876,8 @@ def main() -> int:
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                      "kernel_us": round(kern_us, 2), "event_pair_us": round(pair_us, 2),
                      "kernel": "sipa::decode_mfma_bf16<64, 2>" if args.impl != "valu"
-                     else "sipa::decode_valu<1, 0, 64>"},
+                     else "sipa::decode_valu<1, 0, 64>",
+                     "paged_read_floor": paged_read_floor(wl, calls, args.warmup * args.layers)},
     }
     if args.cpu:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
