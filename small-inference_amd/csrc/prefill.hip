@@ -55,7 +55,7 @@ struct PrefillArgs {
   int* counters;           // [units] split arrivals, zero between launches
   float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
   float* pl;               // same shape: softmax denominators
-  float* part;             // [units][nsplit][8 columns][16 tokens][D] unnormalised outputs
+  float* part;             // [units][nsplit][8 columns][16 tokens][D] each split's output O / l, as fp16
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -74,39 +74,6 @@ static inline int prefill_subtiles(int G, int D) {
 }
 constexpr int kPrefillMaxSplits = 32;
 
-// Merge one round of up to KB splits j0 .. of one (head, token) row: every load issued before the first is used;
-// entries past nvalid re-read the last split and get weight 0. Split 0 always holds the row's first key, so M is
-// finite from the first round on.
-template <int KB, int SLOTS>
-__device__ __forceinline__ void prefill_merge_round(const PrefillArgs& a, __amdgpu_buffer_rsrc_t rows,
-                                                    int64_t mrow, int off, int split_bytes, int j0, int nvalid,
-                                                    float& M, float& den, f32x4& num) {
-  float mj[KB], lj[KB];
-  f32x4 pj[KB];
-#pragma unroll
-  for (int u = 0; u < KB; ++u) {
-    const int j = min(j0 + u, nvalid - 1);
-    mj[u] = load_coherent(a.pm + mrow + (int64_t)j * SLOTS);
-    lj[u] = load_coherent(a.pl + mrow + (int64_t)j * SLOTS);
-    pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, off + j * split_bytes, 0, kAuxSc1);
-  }
-#pragma unroll
-  for (int u = 0; u < KB; ++u)
-    if (j0 + u >= nvalid) mj[u] = kNegInf;
-  float mb = M;
-#pragma unroll
-  for (int u = 0; u < KB; ++u) mb = fmaxf(mb, mj[u]);
-  const float rescale = fast_exp2(M - mb);  // 0 on the first round (M = -inf, mb finite)
-  den *= rescale;
-  num *= rescale;
-#pragma unroll
-  for (int u = 0; u < KB; ++u) {
-    const float w = fast_exp2(mj[u] - mb);  // 0 for padding entries and for splits the token sees nothing of
-    den += w * lj[u];
-    num += w * pj[u];
-  }
-  M = mb;
-}
 
 template <int D>
 struct PrefillSmem {  // one 32-key row group; a KT-key tile is KT / 32 of them
@@ -408,19 +375,26 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) lsum[ci] = l_run[ci][0];
   if (nvalid > 1) {
-    // This split's state for column c, token r: m, l at slot 16 c + r, O at channels 16 dt + 4 q4 .. of that row.
+    // This split's state for column c, token r: m, l at slot 16 c + r, and the split's own output O / l (the
+    // weighted mean of its V rows, so fp16 holds it to 2^-11 relative) at channels 16 dt + 4 q4 .. of that row:
+    // half the bytes of unnormalised fp32 partials, which the merge reads back in one or two memory round trips.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kSlots;
-    const int split_bytes = kSlots * D * 4;
+    const int split_bytes = kSlots * D * 2;
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
-        a.part + (int64_t)u * a.nsplit * kSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
+        (uint16_t*)a.part + (int64_t)u * a.nsplit * kSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
       if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
       const int slot = 16 * (wave + kWaves * ci) + r;
+      const float inv = lsum[ci] > 0.f ? 1.f / lsum[ci] : 0.f;  // l = 0: the token sees no key of this split
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        __builtin_amdgcn_raw_buffer_store_b128(acc[ci][dt], rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 4,
-                                               0, kAuxSc1);
+      for (int dt = 0; dt < DT; ++dt) {
+        const f32x4 o = acc[ci][dt] * inv;
+        const u32x2 h = {f32_to_f16_bits(o[0]) | ((uint32_t)f32_to_f16_bits(o[1]) << 16),
+                         f32_to_f16_bits(o[2]) | ((uint32_t)f32_to_f16_bits(o[3]) << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(h, rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 2, 0,
+                                              kAuxSc1);
+      }
       if (q4 == 0) {
         store_coherent(a.pm + base + slot, m_run[ci]);
         store_coherent(a.pl + base + slot, lsum[ci]);
@@ -434,28 +408,72 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     }
     __syncthreads();
     if (!last_flag) return;
-    // The last split to arrive: one thread per (column, token, channel quad) merges every split's state.
-    constexpr int Q = D / 4;
-    for (int idx = threadIdx.x; idx < kSlots * Q; idx += kThreads) {
-      const int slot = idx / Q, cq = idx % Q;
+    // The last split to arrive merges every split's state: thread t takes row t / 2 (column c, token rr) and
+    // half of its channels, in batches of 32 channels; per round of KB splits it reads the row's m and l and
+    // keeps all of the round's channel loads in flight together. KB and the batch width hold the merge's
+    // registers under what the key loop needs, so the merge costs no occupancy.
+    {
+      constexpr int HALF = D / 2, CB = 32, KB = 4;
+      const int slot = threadIdx.x >> 1;
       const int c = slot >> 4, rr = slot & 15;
       const int g = c % G, tok = 16 * (c / G) + rr;
-      if (c / G >= TT || tok >= ntok) continue;
-      const int64_t mrow = (int64_t)u * a.nsplit * kSlots + slot;
-      const int off = (slot * D + 4 * cq) * 4;
-      float M = kNegInf, den = 0.f;
-      f32x4 num = {0.f, 0.f, 0.f, 0.f};
-      if (nvalid <= 4) {
-        prefill_merge_round<4, kSlots>(a, rows, mrow, off, split_bytes, 0, nvalid, M, den, num);
-      } else {
-        for (int j0 = 0; j0 < nvalid; j0 += 8)
-          prefill_merge_round<8, kSlots>(a, rows, mrow, off, split_bytes, j0, nvalid, M, den, num);
+      if (c / G < TT && tok < ntok) {
+        const int64_t mrow = (int64_t)u * a.nsplit * kSlots + slot;
+        uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
+        for (int c0 = HALF * (threadIdx.x & 1); c0 < HALF * ((threadIdx.x & 1) + 1); c0 += CB) {
+          float M = kNegInf, den = 0.f;
+          f32x4 num[CB / 4];
+#pragma unroll
+          for (int qd = 0; qd < CB / 4; ++qd) num[qd] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int j0 = 0; j0 < nvalid; j0 += KB) {
+            float mj[KB], lj[KB];
+            u32x2 oj[KB][CB / 4];
+#pragma unroll
+            for (int uu = 0; uu < KB; ++uu) {
+              const int j = min(j0 + uu, nvalid - 1);  // entries past nvalid re-read the last split, weight 0
+              mj[uu] = load_coherent(a.pm + mrow + (int64_t)j * kSlots);
+              lj[uu] = load_coherent(a.pl + mrow + (int64_t)j * kSlots);
+#pragma unroll
+              for (int qd = 0; qd < CB / 4; ++qd)
+                oj[uu][qd] = __builtin_amdgcn_raw_buffer_load_b64(
+                    rows, j * split_bytes + (slot * D + c0 + 4 * qd) * 2, 0, kAuxSc1);
+            }
+#pragma unroll
+            for (int uu = 0; uu < KB; ++uu)
+              if (j0 + uu >= nvalid) mj[uu] = kNegInf;
+            float mb = M;
+#pragma unroll
+            for (int uu = 0; uu < KB; ++uu) mb = fmaxf(mb, mj[uu]);
+            const float rescale = fast_exp2(M - mb);  // 0 on the first round (split 0 holds the row's first key)
+            den *= rescale;
+#pragma unroll
+            for (int qd = 0; qd < CB / 4; ++qd) num[qd] *= rescale;
+#pragma unroll
+            for (int uu = 0; uu < KB; ++uu) {
+              const float w = fast_exp2(mj[uu] - mb) * lj[uu];  // 0 for padding entries and keyless splits
+              den += w;
+#pragma unroll
+              for (int qd = 0; qd < CB / 4; ++qd) {
+                const u32x2 hw = oj[uu][qd];
+                const f32x4 o = {f16_bits_to_f32(hw[0] & 0xffffu), f16_bits_to_f32(hw[0] >> 16),
+                                 f16_bits_to_f32(hw[1] & 0xffffu), f16_bits_to_f32(hw[1] >> 16)};
+                num[qd] += w * o;
+              }
+            }
+            M = mb;
+          }
+          const float inv = 1.f / den;
+#pragma unroll
+          for (int qd = 0; qd < CB / 4; qd += 2) {
+            const f32x4 x = num[qd] * inv, y = num[qd + 1] * inv;
+            *(u32x4*)(orow + c0 + 4 * qd) =
+                u32x4{f32_to_bf16_bits(x[0]) | ((uint32_t)f32_to_bf16_bits(x[1]) << 16),
+                      f32_to_bf16_bits(x[2]) | ((uint32_t)f32_to_bf16_bits(x[3]) << 16),
+                      f32_to_bf16_bits(y[0]) | ((uint32_t)f32_to_bf16_bits(y[1]) << 16),
+                      f32_to_bf16_bits(y[2]) | ((uint32_t)f32_to_bf16_bits(y[3]) << 16)};
+          }
+        }
       }
-      const f32x4 o = num / den;
-      uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
-      const uint32_t lo = f32_to_bf16_bits(o[0]) | ((uint32_t)f32_to_bf16_bits(o[1]) << 16);
-      const uint32_t hi2 = f32_to_bf16_bits(o[2]) | ((uint32_t)f32_to_bf16_bits(o[3]) << 16);
-      *(u32x2*)(orow + 4 * cq) = u32x2{lo, hi2};
     }
     if (threadIdx.x == 0)
       __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -515,7 +533,7 @@ static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
   l.pm = kCounterBytes;
   l.pl = l.pm + up(rows * 4);
   l.part = l.pl + up(rows * 4);
-  l.total = l.part + up(rows * D * 4);
+  l.total = l.part + up(rows * D * 2);  // fp16 partial outputs
   return l;
 }
 

@@ -253,7 +253,8 @@ def test_prefill_layout_and_empty_calls():
 
 def test_prefill_split_policy_and_workspace():
     """About two workgroups per CU over (KV head, 16-token query tile) units, no split under 256 keys, at most
-    32; the workspace holds (m, l, O) for 8 heads x 16 tokens per unit and split, and nothing for one split."""
+    32; the workspace holds (m, l) fp32 and O / l fp16 for 8 heads x 16 tokens per unit and split, and nothing
+    for one split."""
     lib = _hip.lib()
     assert lib.sipa_prefill_splits(12, 2, 128, 32, 8192, 256) == 8    # 1.5B, 512-token chunk at 8K: 64 units
     assert lib.sipa_prefill_splits(14, 2, 64, 32, 8192, 256) == 8     # 0.5B likewise
@@ -264,9 +265,9 @@ def test_prefill_split_policy_and_workspace():
     assert lib.sipa_prefill_workspace_bytes(1, 12, 2, 128, 512, 8192, 1) == 0
     rows = 2 * 32 * 8 * 128           # units x splits x 8 columns x 16 tokens, after the 256 KiB of counters
     got = lib.sipa_prefill_workspace_bytes(1, 12, 2, 128, 512, 8192, 8)
-    assert (1 << 18) + rows * (128 + 2) * 4 <= got <= (1 << 18) + rows * (128 + 2) * 4 + 3 * 256
+    assert (1 << 18) + rows * (2 * 128 + 8) <= got <= (1 << 18) + rows * (2 * 128 + 8) + 3 * 256
     d64 = lib.sipa_prefill_workspace_bytes(1, 14, 2, 64, 512, 8192, 8)
-    assert (1 << 18) + rows * (64 + 2) * 4 <= d64 <= (1 << 18) + rows * (64 + 2) * 4 + 3 * 256
+    assert (1 << 18) + rows * (2 * 64 + 8) <= d64 <= (1 << 18) + rows * (2 * 64 + 8) + 3 * 256
     assert lib.sipa_prefill_workspace_bytes(1, 4, 2, 64, 512, 8192, 8) < d64  # G = 2: 64-token units
     rc = lib.sipa_prefill(ctypes.byref(prefill_params(max_context=8192, num_splits=8)), None)
     assert rc == _hip.EWORKSPACE, lib.sipa_last_error()
