@@ -114,15 +114,3 @@ def assert_decode_close(got, ref, what: str = "decode", atol: float = 8e-3) -> f
     assert rel_big <= 2.0 ** -7, f"{what}: relative error {rel_big:.3e} where |ref| >= 2 exceeds 2^-7"
     return raw
 
-
-def bf16_half_ulp(x: np.ndarray) -> np.ndarray:
-    """Half a bf16 unit in the last place at |x| (8 significant bits): the rounding error any bf16 output may
-    carry on top of the arithmetic's own error."""
-    ax = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -126)
-    return 2.0 ** (np.floor(np.log2(ax)) - 8)
-
-
-def bf16_error_beyond_rounding(got: np.ndarray, ref: np.ndarray) -> float:
-    """max |got - ref| - half_ulp_bf16(got): how far a bf16 output lies from the reference beyond its own output
-    rounding (<= the error of the fp32 result before rounding)."""
-    return float((np.abs(got - ref) - bf16_half_ulp(got)).max())

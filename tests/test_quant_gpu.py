@@ -327,7 +327,8 @@ def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False):
 @pytest.mark.parametrize("splits", [1, 3, None, "list"], ids=["single", "split3", "auto", "worklist"])
 def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     """Both INT8 kernels against the oracle's fp32 dequantize-then-attend, outlier K channels (4 per head scaled
-    by U[20, 68], as config C4), ragged lengths with partial last blocks, max-abs 8e-3."""
+    by U[20, 68], as config C4), ragged lengths with partial last blocks: max-abs 8e-3 where |ref| < 2, relative
+    2^-7 above; the fp32-output VALU kernel at 8e-3 everywhere."""
     Hq, Hkv, D = HEADS[heads]
     lengths = [1, 15, 16, 17, 33, 100, 700, 2100]
     q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=5)
