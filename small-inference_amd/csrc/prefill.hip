@@ -46,6 +46,7 @@ struct PrefillArgs {
   const void* ks;
   const void* vs;
   bool ks_f32, vs_f32;
+  bool ks_vec;  // MODE 2: each block's channel-scale row is 16-byte aligned (vector loads of 16 scales)
   int64_t ks_sh, ks_sn, vs_sh, vs_sn;
   const uint16_t* stage;
   int64_t st_sh, st_sn, st_sb;
@@ -81,10 +82,11 @@ struct PrefillSmem {  // one 32-key row group; a KT-key tile is KT / 32 of them
   static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
 };
 
-// A cooperative-load chunk (8 channels of one key) as it arrives from memory, per pool format: MODE 0 bf16 K/V;
-// MODE 1 int8 codes with per-token K and V scales; MODE 2 int8 codes with the block's 8 K channel scales, the
-// token's V scale, and the bf16 staged K of the sequence's partial last block (used when `staged`). Scales are
-// kept as raw fp16 or fp32 bits until the LDS store, so that their loads are waited for only there.
+// A cooperative-load chunk as it arrives from memory, per pool format: MODE 0 bf16 K/V, 8 channels of one key
+// (16 bytes each); MODE 1 int8 codes, 16 channels of one key (16 bytes each), with per-token K and V scales;
+// MODE 2 the same codes with the block's 16 K channel scales (fp16: two 16-byte words, fp32: four), the token's
+// V scale, and the bf16 staged K of the sequence's partial last block (used when `staged`). Scales are kept as
+// raw fp16 or fp32 bits until the LDS store, so that their loads are waited for only there.
 template <int MODE>
 struct KvRaw;
 template <>
@@ -93,16 +95,24 @@ struct KvRaw<0> {
 };
 template <>
 struct KvRaw<1> {
-  u32x2 k, v;
+  u32x4 k, v;
   uint32_t ks, vs;
 };
 template <>
 struct KvRaw<2> {
-  u32x2 k, v;
-  uint32_t ks[8], vs;
-  u32x4 st;
+  u32x4 k, v;
+  u32x4 ks[4];
+  uint32_t vs;
+  u32x4 st[2];
   bool staged;
 };
+
+// Channel scale j (0 .. 15) of a chunk from its raw words: fp16 bits packed two per dword, or fp32 bits.
+__device__ __forceinline__ float chan_scale(const u32x4 (&w)[4], bool f32, int j) {
+  if (f32) return __uint_as_float(w[j >> 2][j & 3]);
+  const uint32_t d = w[j >> 3][(j >> 1) & 3];
+  return f16_bits_to_f32((j & 1) ? d >> 16 : d & 0xffffu);
+}
 
 __device__ __forceinline__ uint32_t scale_bits(const void* base, bool f32, int64_t i) {
   return f32 ? ((const uint32_t*)base)[i] : (uint32_t)((const uint16_t*)base)[i];
@@ -136,7 +146,8 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   constexpr int CW = prefill_cols_per_wave(D);
   constexpr int kSlots = CW * kWaves * 16;  // (column, token) rows of a split state
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = HT * PrefillSmem<D>::kTile;
-  constexpr int CPK = D / 8;                // 16-byte chunks per key row
+  constexpr int CH = MODE == 0 ? 8 : 16;   // channels per cooperative-load chunk: 16 bytes of bf16 or of codes
+  constexpr int CPK = D / CH;               // chunks per key row
   constexpr int LPT = KT * CPK / kThreads;  // chunks per thread per K (or V) tile
   static_assert(LPT * kThreads == KT * CPK, "tile chunks must divide over the workgroup");
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
@@ -209,8 +220,8 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   __syncthreads();  // block ids staged
 
   const int ntiles = (kv_end - k_lo + KT - 1) / KT;
-  // Cooperative tile load: chunk c = threadIdx.x + 256 i of the 32 x D tile is key c / CPK, channels
-  // 8 (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
+  // Cooperative tile load: chunk c = threadIdx.x + 256 i of the KT x D tile is key c / CPK, channels
+  // CH (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
   // (temporal) loads: every query tile of the sequence reads the same keys, so L2 keeps serving them.
   // INT8 pools: the chunk's 8 codes of K and of V with their scales; the LDS store dequantizes them to bf16,
   // q * s in fp32 rounded to bf16, the values the reference's gather path attends over. Format B's keys at or
@@ -231,21 +242,42 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
         x.k = *(const u32x4*)((const uint16_t*)a.k + e);
         x.v = *(const u32x4*)((const uint16_t*)a.v + e);
       } else {
-        const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + 8 * cg;
-        x.k = *(const u32x2*)((const int8_t*)a.k + e);
-        x.v = *(const u32x2*)((const int8_t*)a.v + e);
+        const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + CH * cg;
+        x.k = *(const u32x4*)((const int8_t*)a.k + e);
+        x.v = *(const u32x4*)((const int8_t*)a.v + e);
         x.vs = scale_bits(a.vs, a.vs_f32, (int64_t)h * a.vs_sh + blk * a.vs_sn + off);
         if constexpr (MODE == 1) {
           x.ks = scale_bits(a.ks, a.ks_f32, (int64_t)h * a.ks_sh + blk * a.ks_sn + off);
         } else {
+          const int64_t sb = (int64_t)h * a.ks_sh + blk * a.ks_sn + CH * cg;  // the chunk's 16 channel scales
+          if (a.ks_vec) {  // 16-byte aligned rows (host-checked): 32 or 64 contiguous bytes
+            const u32x4* src = (const u32x4*)((const uint8_t*)a.ks + sb * (a.ks_f32 ? 4 : 2));
+            x.ks[0] = src[0];
+            x.ks[1] = src[1];
+            if (a.ks_f32) {
+              x.ks[2] = src[2];
+              x.ks[3] = src[3];
+            }
+          } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            x.ks[j] = scale_bits(a.ks, a.ks_f32, (int64_t)h * a.ks_sh + blk * a.ks_sn + 8 * cg + j);
+            for (int j = 0; j < 16; j += 2) {
+              const uint32_t b0 = scale_bits(a.ks, a.ks_f32, sb + j), b1 = scale_bits(a.ks, a.ks_f32, sb + j + 1);
+              if (a.ks_f32) {
+                x.ks[j >> 2][j & 3] = b0;
+                x.ks[j >> 2][(j & 3) + 1] = b1;
+              } else {
+                x.ks[j >> 3][(j >> 1) & 3] = b0 | (b1 << 16);
+              }
+            }
+          }
           const int pos = k_lo + rel;
           x.staged = tail >= 0 && pos >= nq;
-          if (x.staged)
-            x.st = *(const u32x4*)(a.stage + (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn +
-                                   (int64_t)(pos & 15) * a.st_sb + 8 * cg);
+          if (x.staged) {
+            const u32x4* st = (const u32x4*)(a.stage + (int64_t)h * a.st_sh + (int64_t)tail * a.st_sn +
+                                             (int64_t)(pos & 15) * a.st_sb + CH * cg);
+            x.st[0] = st[0];
+            x.st[1] = st[1];
+          }
         }
       }
     }
@@ -254,20 +286,26 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int c = threadIdx.x + kThreads * i;
-      const int e = (c / CPK) * P + 8 * (c % CPK);
+      const int e = (c / CPK) * P + CH * (c % CPK);
       const KvRaw<MODE>& x = raw[set][i];
       if constexpr (MODE == 0) {
         *(u32x4*)(&sm[buf][0][e]) = x.k;
         *(u32x4*)(&sm[buf][1][e]) = x.v;
       } else {
+        const u32x2 klo = {x.k[0], x.k[1]}, khi = {x.k[2], x.k[3]};
+        const u32x2 vlo = {x.v[0], x.v[1]}, vhi = {x.v[2], x.v[3]};
         const float vsf = scale_value(x.vs, a.vs_f32);
-        *(u32x4*)(&sm[buf][1][e]) = dequant8(x.v, [&](int) { return vsf; });
+        *(u32x4*)(&sm[buf][1][e]) = dequant8(vlo, [&](int) { return vsf; });
+        *(u32x4*)(&sm[buf][1][e + 8]) = dequant8(vhi, [&](int) { return vsf; });
         if constexpr (MODE == 1) {
           const float ksf = scale_value(x.ks, a.ks_f32);
-          *(u32x4*)(&sm[buf][0][e]) = dequant8(x.k, [&](int) { return ksf; });
+          *(u32x4*)(&sm[buf][0][e]) = dequant8(klo, [&](int) { return ksf; });
+          *(u32x4*)(&sm[buf][0][e + 8]) = dequant8(khi, [&](int) { return ksf; });
         } else {
           *(u32x4*)(&sm[buf][0][e]) =
-              x.staged ? x.st : dequant8(x.k, [&](int j) { return scale_value(x.ks[j], a.ks_f32); });
+              x.staged ? x.st[0] : dequant8(klo, [&](int j) { return chan_scale(x.ks, a.ks_f32, j); });
+          *(u32x4*)(&sm[buf][0][e + 8]) =
+              x.staged ? x.st[1] : dequant8(khi, [&](int j) { return chan_scale(x.ks, a.ks_f32, 8 + j); });
         }
       }
     }
@@ -653,6 +691,10 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.vs = p->v_scale;
   a.ks_f32 = p->k_scale_dtype == SIPA_F32;
   a.vs_f32 = p->v_scale_dtype == SIPA_F32;
+  {
+    const int per16 = a.ks_f32 ? 4 : 8;  // scales per 16 bytes
+    a.ks_vec = aligned16p(p->k_scale) && p->ks_stride_h % per16 == 0 && p->ks_stride_n % per16 == 0;
+  }
   a.ks_sh = p->ks_stride_h;
   a.ks_sn = p->ks_stride_n;
   a.vs_sh = p->vs_stride_h;
@@ -680,7 +722,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   } else {
     if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 0, 32>), grid, block, 0, st, a);
     else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 1, 32>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 1, 2, 32>), grid, block, 0, st, a);  // registers: one tile ahead
+    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 2, 32>), grid, block, 0, st, a);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));

@@ -267,3 +267,41 @@ def test_int8_pools(fmt, shape, splits):
     err = np.abs(got.double().cpu().numpy()[rows] - ref32[rows])
     bound = np.where(np.abs(ref32[rows]) < 2, 8e-3, 2 ** -7 * np.abs(ref32[rows])) + 2 ** -9 * pv_abs
     assert (err <= bound).all(), f"max excess {(err - bound).max():.3e}"
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+def test_kchannel_scale_layouts(shape):
+    """Format B's channel scales in every layout the parameter block allows give the same output bits: fp16 rows
+    (16-byte vector loads), fp32 rows (the same values), and fp16 / fp32 views whose rows are not 16-byte aligned
+    (the kernel's per-scale loads); per-(head, channel) scales broadcast over blocks (block stride 0, fp32) equal
+    the same scales written out per block."""
+    from engine.hip_decode import QuantKV
+
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [300, 1000, 33, 517], [64, 7, 33, 200]
+    print(f"case kchannel scale layouts shape={shape}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=23)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    quant, kq, vq, _, _ = int8_pools(k, v, "int8-kchannel", ctx, tables, g)
+    N = kq.shape[1]
+    scale = D ** -0.5
+
+    def run(ks):
+        return paged_prefill_attention(q, kq, vq, bt, c, st, ln, scale, max(ctx), max(qlen),
+                                       quant=QuantKV(2, ks, quant.v_scale, quant.stage, quant.tail_slots))
+
+    def misaligned(x):  # the same values in a view whose rows start 1 element past a 16-byte boundary
+        wide = torch.zeros(Hkv, N, D + 1, dtype=x.dtype, device=x.device)
+        wide[:, :, 1:] = x
+        return wide[:, :, 1:]
+
+    ks16 = quant.k_scale
+    base = run(ks16)
+    for name, ks in (("fp32", ks16.float()), ("fp16 misaligned", misaligned(ks16)),
+                     ("fp32 misaligned", misaligned(ks16.float()))):
+        assert torch.equal(run(ks), base), name
+    per_ch = torch.rand(Hkv, 1, D, generator=g, device="cuda") * 0.05 + 0.01  # fp32 per (head, channel)
+    wide = run(per_ch.expand(Hkv, N, D))
+    assert per_ch.expand(Hkv, N, D).stride(1) == 0
+    assert torch.equal(wide, run(per_ch.expand(Hkv, N, D).contiguous()))
+    assert torch.equal(wide, run(misaligned(per_ch.expand(Hkv, N, D).contiguous())))
