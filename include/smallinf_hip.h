@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 3
+#define SIPA_ABI_VERSION 4
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -221,7 +221,13 @@ typedef struct sipa_prefill_params {
   void* workspace;
   int64_t workspace_bytes;
   int32_t bt_width;             /* entries per block_tables row; must be >= ceil(max_context / 16) */
+  /* Split merge (ABI 4): SIPA_MERGE_AUTO reads a unit's partials from the L2 of the XCD its splits ran on when
+     they all shared one (the kernel places them so), through memory otherwise; SIPA_MERGE_MEMORY always reads
+     them through memory (agent-coherent loads). Both give the same bits. */
+  int32_t merge_path;
 } sipa_prefill_params;
+
+enum { SIPA_MERGE_AUTO = 0, SIPA_MERGE_MEMORY = 1 };
 
 int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
 

@@ -155,6 +155,9 @@ __device__ __forceinline__ void store_out4(const DecodeArgs& a, int s, int hq, i
 // resource (gfx9 descriptor word 3). Loads and stores through it with the sc1 cache-policy bit (aux 16) are
 // agent-coherent, like the relaxed agent-scope atomics above, but move 16 bytes per lane in one instruction.
 constexpr int kAuxSc1 = 16;
+// The sc0 bit alone (aux 1): loads that bypass the CU's L1 and are served by the XCD's L2, coherent with every
+// store made on the same XCD.
+constexpr int kAuxSc0 = 1;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rows(const DecodeArgs& a, int s, int h, int D) {
   float* base = a.part + ((int64_t)s * a.Hq + (int64_t)h * a.G) * a.splits * D;

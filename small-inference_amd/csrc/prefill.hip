@@ -18,6 +18,7 @@
 //   causal mask: key position > token position -> -inf; online softmax per token (exp2 domain, lazy rescale)
 //   O^T[16 d x 16 tokens] += V^T . P^T   (V^T by transposing LDS reads, P^T from the S^T registers)
 #include <algorithm>
+#include <type_traits>
 
 #include "decode_common.h"
 
@@ -53,6 +54,7 @@ struct PrefillArgs {
   int32_t n_stage;
   const int32_t* tails;
   float scale_log2;
+  bool mem_merge;          // merge every unit through memory (SIPA_MERGE_MEMORY)
   int* counters;           // [units] split arrivals, zero between launches
   float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
   float* pl;               // same shape: softmax denominators
@@ -154,12 +156,15 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
 
-  // Splits fastest: consecutive workgroups (which the dispatcher deals round-robin to the 8 XCDs) take the
-  // splits of one unit. Units go out last query tile first, over all (sequence, KV head) pairs: under the causal
-  // mask a unit's keys grow with its tile index, so the longest units start first and the short ones fill in.
+  // Units by XCD: the dispatcher deals workgroups round-robin to the 8 XCDs (workgroup L on XCD L mod 8), and
+  // unit u's splits take workgroups L = u mod 8 + 8 (nsplit (u / 8) + split), so they share one L2, which then
+  // serves the merge its partials. Each workgroup checks its XCD (XCC_ID); a unit any of whose splits ran
+  // elsewhere is merged through memory instead. Units go out last query tile first, over all (sequence, KV
+  // head) pairs: under the causal mask a unit's keys grow with its tile index, so the longest units start first.
   const int L = blockIdx.x;
-  const int sp = L % a.nsplit;
-  const int u = L / a.nsplit;
+  const int sp = (L >> 3) % a.nsplit;
+  const int u = (L & 7) + 8 * ((L >> 3) / a.nsplit);
+  if (u >= a.npair * a.qtiles) return;  // the grid is padded to whole groups of 8 units
   const int pair = u % a.npair;
   const int j = a.qtiles - 1 - u / a.npair;
   const int s = pair % a.S, h = pair / a.S;
@@ -441,22 +446,34 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-      const int prev = __hip_atomic_fetch_add(a.counters + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = (prev == nvalid - 1);
+      // Arrival: +1, and +2^16 from a workgroup that is not on its unit's XCD. The last to arrive merges from
+      // its L2 (L1 bypassed) when every split of the unit, itself included, ran on that XCD: their write-through
+      // stores updated that L2. Otherwise from memory, as agent-coherent loads.
+      uint32_t xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      const int away = a.mem_merge || (int)(xcc & 0xf) != (L & 7);
+      const int prev = __hip_atomic_fetch_add(a.counters + u, 1 + (away << 16), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = (prev & 0xffff) == nvalid - 1 ? 1 + ((prev >> 16) + away == 0) : 0;
     }
     __syncthreads();
     if (!last_flag) return;
+    const bool from_l2 = last_flag == 2;
     // The last split to arrive merges every split's state: thread t takes row t / 2 (column c, token rr) and
     // half of its channels, in batches of 32 channels; per round of KB splits it reads the row's m and l and
     // keeps all of the round's channel loads in flight together. KB and the batch width hold the merge's
-    // registers under what the key loop needs, so the merge costs no occupancy.
-    {
+    // registers under what the key loop needs, so the merge costs no occupancy. AUX: the loads' cache policy.
+    const __amdgpu_buffer_rsrc_t mrows = __builtin_amdgcn_make_buffer_rsrc(
+        a.pm + (int64_t)u * a.nsplit * kSlots, (short)0, a.nsplit * kSlots * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t lrows = __builtin_amdgcn_make_buffer_rsrc(
+        a.pl + (int64_t)u * a.nsplit * kSlots, (short)0, a.nsplit * kSlots * 4, 0x00020000);
+    auto merge = [&](auto aux_tag) {
+      constexpr int AUX = decltype(aux_tag)::value;
       constexpr int HALF = D / 2, CB = 32, KB = 4;
       const int slot = threadIdx.x >> 1;
       const int c = slot >> 4, rr = slot & 15;
       const int g = c % G, tok = 16 * (c / G) + rr;
       if (c / G < TT && tok < ntok) {
-        const int64_t mrow = (int64_t)u * a.nsplit * kSlots + slot;
         uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
         for (int c0 = HALF * (threadIdx.x & 1); c0 < HALF * ((threadIdx.x & 1) + 1); c0 += CB) {
           float M = kNegInf, den = 0.f;
@@ -469,12 +486,14 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu) {
               const int j = min(j0 + uu, nvalid - 1);  // entries past nvalid re-read the last split, weight 0
-              mj[uu] = load_coherent(a.pm + mrow + (int64_t)j * kSlots);
-              lj[uu] = load_coherent(a.pl + mrow + (int64_t)j * kSlots);
+              mj[uu] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                     mrows, (j * kSlots + slot) * 4, 0, AUX));
+              lj[uu] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                     lrows, (j * kSlots + slot) * 4, 0, AUX));
 #pragma unroll
               for (int qd = 0; qd < CB / 4; ++qd)
                 oj[uu][qd] = __builtin_amdgcn_raw_buffer_load_b64(
-                    rows, j * split_bytes + (slot * D + c0 + 4 * qd) * 2, 0, kAuxSc1);
+                    rows, j * split_bytes + (slot * D + c0 + 4 * qd) * 2, 0, AUX);
             }
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu)
@@ -512,7 +531,11 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
           }
         }
       }
-    }
+    };
+    if (from_l2)
+      merge(std::integral_constant<int, kAuxSc0>());
+    else
+      merge(std::integral_constant<int, kAuxSc1>());
     if (threadIdx.x == 0)
       __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -645,7 +668,8 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   if (splits <= 0) splits = prefill_splits_host(units, p->max_context, sipa_device_cu_count(-1));
   const int chunk = prefill_chunk(p->max_context, splits);
   const int nsplit = (p->max_context + chunk - 1) / chunk;
-  const int64_t wgs = units * nsplit;
+  // split launches: whole groups of 8 units, one XCD each (the kernel's workgroup-to-unit mapping)
+  const int64_t wgs = (nsplit > 1 ? (units + 7) / 8 * 8 : units) * nsplit;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   PrefillLayout lay{};
   if (nsplit > 1) {
@@ -705,6 +729,9 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.st_sb = p->st_stride_b;
   a.n_stage = p->num_stage;
   a.tails = p->tail_slots;
+  SIPA_CHECK(p->merge_path == SIPA_MERGE_AUTO || p->merge_path == SIPA_MERGE_MEMORY, SIPA_EINVAL,
+             "merge_path %d is neither SIPA_MERGE_AUTO nor SIPA_MERGE_MEMORY", p->merge_path);
+  a.mem_merge = p->merge_path == SIPA_MERGE_MEMORY;
   char* ws = (char*)p->workspace;
   a.counters = nsplit > 1 ? (int*)(ws + lay.counters) : nullptr;
   a.pm = nsplit > 1 ? (float*)(ws + lay.pm) : nullptr;

@@ -40,7 +40,8 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                             context_lens: torch.Tensor, query_starts: torch.Tensor, query_lens: torch.Tensor,
                             scale: float, max_context: int, max_query_len: int,
                             out: torch.Tensor | None = None, *, num_splits: int | None = None,
-                            host_query_lens: list[int] | None = None, quant=None) -> torch.Tensor:
+                            host_query_lens: list[int] | None = None, quant=None,
+                            merge_path: str = "auto") -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16 (int8 with
@@ -54,6 +55,8 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     INT8 pools take quant (engine.hip_decode.QuantKV: mode 1 per-token scales, mode 2 per-channel K scales with
     format B's staging and tail slots, which must then cover these S sequences); K/V are dequantized as the
     reference's gather path does, q * s in fp32 rounded to bf16.
+    merge_path: "auto" merges a query tile's key splits from the L2 of the XCD they ran on when they shared one
+    (the kernel places them so), through memory otherwise; "memory" always through memory. Same bits either way.
     """
     S = block_tables.shape[0]
     T, Hq, D = q.shape
@@ -107,6 +110,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
         lens = host_query_lens if host_query_lens is not None else [max_query_len] * S
         num_splits = prefill_splits(Hq, Hkv, D, lens, max_context)
     p.num_splits = num_splits
+    if merge_path not in ("auto", "memory"):
+        raise ValueError(f"merge_path {merge_path!r} is neither 'auto' nor 'memory'")
+    p.merge_path = 1 if merge_path == "memory" else 0
     stream = _hip.stream_of(q)
     nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)
     if nbytes > 0:

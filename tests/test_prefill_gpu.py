@@ -152,8 +152,10 @@ def test_chunk_at_8k_splits_against_torch(shape):
     scale = D ** -0.5
     run = lambda n: paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=n)  # noqa: E731
     a, b, a2 = run(8), run(3), run(8)
+    mem = paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=8, merge_path="memory")
     torch.cuda.synchronize()
     assert torch.equal(a, a2)
+    assert torch.equal(a, mem)  # the L2 merge and the merge through memory give the same bits
     G = Hq // Hkv
     idx = torch.tensor(tables[0], device="cuda", dtype=torch.int64)
     kk = k.index_select(1, idx).reshape(Hkv, -1, D)[:, :8192].float().repeat_interleave(G, 0)
@@ -305,3 +307,27 @@ def test_kchannel_scale_layouts(shape):
     assert per_ch.expand(Hkv, N, D).stride(1) == 0
     assert torch.equal(wide, run(per_ch.expand(Hkv, N, D).contiguous()))
     assert torch.equal(wide, run(misaligned(per_ch.expand(Hkv, N, D).contiguous())))
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g4", "g1"])
+@pytest.mark.parametrize("splits", [2, 5, 32])
+def test_merge_paths_agree(shape, splits):
+    """The split merge from the XCD's L2 (units whose splits shared an XCD) and through memory (agent-coherent
+    loads, every unit) give the same bits, and the memory path meets the oracle bound on its own; unit counts
+    that are not multiples of 8 exercise the padded grid."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [3000, 700, 129], [700, 300, 17]
+    print(f"case merge paths shape={shape} splits={splits}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=31)
+    scale = D ** -0.5
+    run = lambda path: paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen),  # noqa: E731
+                                               num_splits=splits, merge_path=path)
+    auto, mem, auto2 = run("auto"), run("memory"), run("auto")
+    torch.cuda.synchronize()
+    assert torch.equal(auto, mem) and torch.equal(auto, auto2)
+    args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
+    ref32 = paged_ref.prefill(*args, dtype=np.float32)
+    rows = np.concatenate([np.arange(s0, s0 + n) for s0, n in zip(starts, qlen)])
+    assert_bf16_close(mem.double().cpu().numpy()[rows], ref32[rows], "merge through memory")
+    with pytest.raises(ValueError):
+        run("l2")
