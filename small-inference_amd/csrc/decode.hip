@@ -425,7 +425,7 @@ __global__ void __launch_bounds__(kThreads) combine_splits(const DecodeArgs a) {
   const int h = blockIdx.x, s = blockIdx.y;
   const int nvalid = (context_len(a, s) + a.chunk - 1) / a.chunk;
   if (nvalid <= 1) return;  // the single split wrote the output itself
-  combine_group<D, OUT_F32, false>(a, s, h, nvalid);
+  combine_group<D, OUT_F32, kMergePlain>(a, s, h, nvalid);
 }
 
 // ---- host side --------------------------------------------------------------------------------------------------

@@ -164,23 +164,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rows(const DecodeArgs&
   return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, a.G * a.splits * D * 4, 0x00020000);
 }
 
-// One round of the merge: up to KB splits j0 .. j0 + KB - 1 of row0, every load issued before the first is used.
-// Entries past nvalid re-read the last split and get weight 0 (branch-free).
-template <int KB, int D, bool COHERENT>
-__device__ __forceinline__ void combine_round(const DecodeArgs& a, __amdgpu_buffer_rsrc_t rows, int64_t row0,
-                                              int g, int c, int j0, int nvalid, float& M, float& den, f32x4& num) {
-  auto ld = [](float* p) { return COHERENT ? load_coherent(p) : *p; };
+// Where a merge reads the split partials from: plainly (the separate combine kernel, a later launch), from the
+// merging workgroup's XCD's L2 (every split of the pair ran on that XCD: their write-through stores updated it),
+// or through memory with agent-coherent loads (splits on several XCDs).
+enum MergeLoads { kMergePlain = 0, kMergeL2 = 1, kMergeMemory = 2 };
+
+// One round of the merge: up to KB splits j0 .. j0 + KB - 1 of row0 (query head g of the pair), every load
+// issued before the first is used. Entries past nvalid re-read the last split and get weight 0 (branch-free).
+template <int KB, int D, int POL>
+__device__ __forceinline__ void combine_round(const DecodeArgs& a, __amdgpu_buffer_rsrc_t rows,
+                                              __amdgpu_buffer_rsrc_t mrows, __amdgpu_buffer_rsrc_t lrows,
+                                              int64_t row0, int g, int c, int j0, int nvalid, float& M, float& den,
+                                              f32x4& num) {
+  constexpr int AUX = POL == kMergeL2 ? kAuxSc0 : kAuxSc1;
   float mj[KB], lj[KB];
   f32x4 pj[KB];
 #pragma unroll
   for (int u = 0; u < KB; ++u) {
     const int j = min(j0 + u, nvalid - 1);
-    mj[u] = ld(a.pm + row0 + j);
-    lj[u] = ld(a.pl + row0 + j);
-    if (COHERENT)
-      pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, ((g * a.splits + j) * D + 4 * c) * 4, 0, kAuxSc1);
-    else
+    if constexpr (POL == kMergePlain) {
+      mj[u] = a.pm[row0 + j];
+      lj[u] = a.pl[row0 + j];
       pj[u] = *(const f32x4*)(a.part + (row0 + j) * D + 4 * c);
+    } else {
+      const int e = g * a.splits + j;
+      mj[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mrows, e * 4, 0, AUX));
+      lj[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrows, e * 4, 0, AUX));
+      pj[u] = __builtin_amdgcn_raw_buffer_load_b128(rows, (e * D + 4 * c) * 4, 0, AUX);
+    }
   }
 #pragma unroll
   for (int u = 0; u < KB; ++u)
@@ -202,25 +213,30 @@ __device__ __forceinline__ void combine_round(const DecodeArgs& a, __amdgpu_buff
 
 // Merge the split partials of (s, h) for every query head of the group: rows [h*G, h*G + G). One thread per
 // (query head, 4-channel quad), so all loads of a round are in flight together; 4 (nvalid <= 4), 8 (<= 8) or 16
-// splits per round, merged online, so up to 8 splits cost one memory round trip and 32 cost two. COHERENT: the partials were written
-// by other workgroups of this launch (the fused merge).
-template <int D, bool OUT_F32, bool COHERENT>
+// splits per round, merged online, so up to 8 splits cost one memory round trip and 32 cost two. POL: where the
+// partials are read from (MergeLoads).
+template <int D, bool OUT_F32, int POL>
 __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
   constexpr int Q = D / 4;
   const int G = a.G;
   const __amdgpu_buffer_rsrc_t rows = partial_rows(a, s, h, D);
+  const int64_t pair0 = ((int64_t)s * a.Hq + (int64_t)h * G) * a.splits;
+  const __amdgpu_buffer_rsrc_t mrows = __builtin_amdgcn_make_buffer_rsrc(a.pm + pair0, (short)0, G * a.splits * 4,
+                                                                         0x00020000);
+  const __amdgpu_buffer_rsrc_t lrows = __builtin_amdgcn_make_buffer_rsrc(a.pl + pair0, (short)0, G * a.splits * 4,
+                                                                         0x00020000);
   for (int idx = threadIdx.x; idx < G * Q; idx += kThreads) {
     const int g = idx / Q, c = idx % Q;
-    const int64_t row0 = ((int64_t)s * a.Hq + h * G + g) * a.splits;
+    const int64_t row0 = pair0 + (int64_t)g * a.splits;
     float M = kNegInf, den = 0.f;
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     if (nvalid <= 4) {
-      combine_round<4, D, COHERENT>(a, rows, row0, g, c, 0, nvalid, M, den, num);
+      combine_round<4, D, POL>(a, rows, mrows, lrows, row0, g, c, 0, nvalid, M, den, num);
     } else if (nvalid <= 8) {
-      combine_round<8, D, COHERENT>(a, rows, row0, g, c, 0, nvalid, M, den, num);
+      combine_round<8, D, POL>(a, rows, mrows, lrows, row0, g, c, 0, nvalid, M, den, num);
     } else {
       for (int j0 = 0; j0 < nvalid; j0 += 16)
-        combine_round<16, D, COHERENT>(a, rows, row0, g, c, j0, nvalid, M, den, num);
+        combine_round<16, D, POL>(a, rows, mrows, lrows, row0, g, c, j0, nvalid, M, den, num);
     }
     store_out4<OUT_F32>(a, s, h * G + g, 4 * c, num / den);
   }
@@ -228,19 +244,29 @@ __device__ void combine_group(const DecodeArgs& a, int s, int h, int nvalid) {
 
 // After this workgroup's partial stores are issued: once they have completed (reached the point of coherence),
 // count the partial; the workgroup that brings the count of (s, h) to nvalid merges every partial and resets the
-// counter for the next launch.
+// counter for the next launch. On the (sequence, KV head, split) grid with S Hkv a multiple of 8, every split of
+// (s, h) has the same workgroup id mod 8, the XCD the dispatcher deals it to; each workgroup checks that it ran
+// there (XCC_ID) and counts +2^16 if not (and always on a work list, whose items go anywhere). The merger reads
+// from its L2 when no split of the pair counted away, through memory otherwise.
 template <int D, bool OUT_F32>
 __device__ void publish_and_merge(const DecodeArgs& a, int s, int h, int nvalid, int* last_flag) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    *last_flag = (prev == nvalid - 1);
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const bool may_share = a.items == nullptr && (a.S * a.Hkv) % 8 == 0;
+    const int away = !may_share || (int)(xcc & 0xf) != (int)(blockIdx.x & 7);
+    const int prev = __hip_atomic_fetch_add(a.counters + (int64_t)s * a.Hkv + h, 1 + (away << 16),
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = (prev & 0xffff) == nvalid - 1 ? 1 + ((prev >> 16) + away == 0) : 0;
   }
   __syncthreads();
   if (!*last_flag) return;
-  combine_group<D, OUT_F32, true>(a, s, h, nvalid);
+  if (*last_flag == 2)
+    combine_group<D, OUT_F32, kMergeL2>(a, s, h, nvalid);
+  else
+    combine_group<D, OUT_F32, kMergeMemory>(a, s, h, nvalid);
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
