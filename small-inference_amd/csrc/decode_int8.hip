@@ -98,19 +98,37 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   for (int j = 0; j < KS; ++j) qb[j] = load_qb(j);
   constexpr bool kconst = MODE == 3;  // one channel scale per (head, channel) for every block
   // qh: the query in fp16 (modes 1, 2), or the high part of Q' = q * s (mode 3) with ql its low part,
-  // fp16(Q' - qh), so that qh + ql carries Q' to about 2^-22.
+  // fp16(Q' - qh), so that qh + ql carries Q' to about 2^-22. A head whose largest |q| (|Q'| in mode 3) lies
+  // outside [2^-6, 2^8) is first scaled by 2^-shift to bring it into [2^6, 2^7): fp16 then holds it without
+  // overflow (|q| > 65504) or subnormal loss, and mode 2's q * s products keep headroom. The factor is exact and
+  // the softmax scale of that head (lane column r) takes its inverse, so the scores equal unscaled ones bit for
+  // bit wherever those are representable.
+  float qf[KS][8];
+  float qmax = 0.f;
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qf[j][i] = (float)qb[j][i];
+      if (kconst) {
+        const int64_t ci = (int64_t)h * a.ks_sh + kchan(j) + i;
+        qf[j][i] *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
+      }
+      qmax = fmaxf(qmax, fabsf(qf[j][i]));
+    }
+  }
+  qmax = max_over_rows(qmax);  // head r over the four lane groups
+  const int qexp = qmax > 0.f ? (int)((__float_as_uint(qmax) >> 23) & 0xff) - 127 : 0;  // floor(log2) of a normal
+  const int qshift = (qexp >= 8 || qexp < -6) ? qexp - 6 : 0;
+  const float sl2 = ldexpf(a.scale_log2, qshift);  // this lane's head: the softmax scale times 2^shift
   f16x8 qh[KS], ql[KS];
 #pragma unroll
   for (int j = 0; j < KS; ++j) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float qf = (float)qb[j][i];
-      if (kconst) {
-        const int64_t ci = (int64_t)h * a.ks_sh + kchan(j) + i;
-        qf *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
-      }
-      qh[j][i] = (_Float16)qf;
-      ql[j][i] = (_Float16)(qf - (float)qh[j][i]);
+      const float x = ldexpf(qf[j][i], -qshift);
+      qh[j][i] = (_Float16)x;
+      ql[j][i] = (_Float16)(x - (float)qh[j][i]);
     }
   }
   const int ctx = context_len(a, s);
@@ -202,6 +220,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
         for (int j = 0; j < KS; ++j)
           sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, *(const u32x4*)(st + kchan(j))),
                                                            load_qb(j), sc[mt], 0, 0, 0);  // reloaded: rare
+        if (qshift != 0) sc[mt] *= ldexpf(1.f, -qshift);  // the unscaled bf16 query: onto the head's scale
         continue;
       }
 #pragma unroll
@@ -244,7 +263,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                      fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
     mx = max_over_rows(mx);
-    mx *= a.scale_log2;
+    mx *= sl2;
     if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
@@ -259,7 +278,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int mt = i >> 2, e = i & 3;
-      const float p = fast_exp2(fmaf(sc[mt][e], a.scale_log2, -m_run));
+      const float p = fast_exp2(fmaf(sc[mt][e], sl2, -m_run));
       psum += p;
       const uint32_t vsw = (e < 2) ? vsc[mt].x : vsc[mt].y;
       pop[i] = (_Float16)(p * h2f(vsw >> (16 * (e & 1))));

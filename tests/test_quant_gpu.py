@@ -436,3 +436,26 @@ def test_kchannel_tail_slots_are_clamped_and_counted(impl):
         paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
                                max(lengths), quant=QuantKV(2, quant.k_scale, quant.v_scale, quant.stage,
                                                            bad_tails[:2]))
+
+
+@pytest.mark.parametrize("fmt,const", [("int8", False), ("int8-kchannel", False), ("int8-kchannel", True)],
+                         ids=["per_token", "kchannel", "kchannel_const"])
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_int8_mfma_query_magnitudes(fmt, const, heads):
+    """The INT8 MFMA kernels hold the query in fp16: heads whose |q| reaches 3e5 (past fp16's 65504) or stays
+    under 1e-6 (fp16 subnormals) are scaled by a power of two first, so they meet the same bound against the
+    oracle's fp32 attention as ordinary heads; every other head of the same call keeps its plain scale."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [1, 17, 300, 1000]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=8, const_channels=const)
+    mag = torch.ones(Hq, 1, device="cuda")
+    mag[0], mag[1], mag[-1] = 3e5 / 4, 1e-7, 300.0  # |q| about 4 sigma: 3e5, 4e-7, 1.2e3
+    q = (q.float() * mag).bfloat16()
+    print(f"case int8 query magnitudes {fmt} const={const} {heads}", flush=True)
+    out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                 max(lengths), quant=quant, impl="mfma")
+    got = out.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    assert_decode_close(got, ref, f"int8 query magnitudes {fmt} const={const} {heads}")
