@@ -18,10 +18,16 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The larger of two scores as gfx950's v_maximum(3)_f32. fmaxf lowers, in the IEEE mode kernels run in, to
+// v_max_f32 with every operand first quieted by a v_max_f32 x, x of its own; maximum needs no quieting and fuses
+// three operands. It differs from fmaxf only where a score max never goes: a NaN operand (propagated rather than
+// dropped) and -0 against +0 (+0 wins).
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes of an MFMA accumulator column).
 __device__ __forceinline__ float max_over_rows(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  x = vmax(x, __shfl_xor(x, 16));
+  return vmax(x, __shfl_xor(x, 32));
 }
 
 __device__ __forceinline__ float sum_over_rows(float x) {
@@ -36,9 +42,9 @@ __device__ __forceinline__ float sum_over_rows(float x) {
 // (the ragged split-grid case 52 -> 65 us), so only the prefill kernel uses these.
 __device__ __forceinline__ float max_over_rows_swap(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float sum_over_rows_swap(float x) {

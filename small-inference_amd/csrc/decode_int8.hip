@@ -260,8 +260,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
         for (int i = 0; i < 4; ++i)
           if (t0 + 16 * mt + 4 * q4 + i >= end) sc[mt][i] = kNegInf;
     }
-    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    float mx = vmax(vmax(vmax(sc[0][0], sc[0][1]), vmax(sc[0][2], sc[0][3])),
+                    vmax(vmax(sc[1][0], sc[1][1]), vmax(sc[1][2], sc[1][3])));
     mx = max_over_rows(mx);
     mx *= sl2;
     if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleSlack)) {

@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
       }
       float mx = kNegInf;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) mx = fmaxf(mx, fmaxf(fmaxf(sc[mt][0], sc[mt][1]), fmaxf(sc[mt][2], sc[mt][3])));
+      for (int mt = 0; mt < MT; ++mt) mx = vmax(mx, vmax(vmax(sc[mt][0], sc[mt][1]), vmax(sc[mt][2], sc[mt][3])));
       mx = max_over_rows_swap(mx) * a.scale_log2;
       // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
       // below are taken as 0 then, so that -inf - -inf never forms.
