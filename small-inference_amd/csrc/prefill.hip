@@ -332,10 +332,18 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int jj = 0; jj < KS; ++jj) kop[mt][jj] = *(const bf16x8*)(ks + (16 * mt + r) * P + 32 * jj + 8 * q4);
+    // An unused column tile (G < 8) skips its scores and softmax (the VALU work, which bounds the kernel when
+    // three workgroups share a CU) and takes zero probabilities, so that the P.V MFMAs below run for every
+    // column without a branch between them and the V reads run ahead of them (per-column branches there cost
+    // 2.2 us of a 512-token chunk at 8K context).
     bf16x8 pop[CW][HT];
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
-      if (!cvalid[ci]) continue;  // wave-uniform
+      if (!cvalid[ci]) {  // wave-uniform
+#pragma unroll
+        for (int hf = 0; hf < HT; ++hf) pop[ci][hf] = bf16x8{};
+        continue;
+      }
       f32x4 sc[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -388,8 +396,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
         const bf16x8 vop = read_v_operand<bf16x8>(vs + 32 * P * hf, tr_off, P, 16 * dt);
 #pragma unroll
         for (int ci = 0; ci < CW; ++ci)
-          if (cvalid[ci])
-            acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci][hf], acc[ci][dt], 0, 0, 0);
+          acc[ci][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[ci][hf], acc[ci][dt], 0, 0, 0);
       }
   };
 
