@@ -265,3 +265,24 @@ def test_valu_streaming_kernels_match_oracle(heads, impl, splits):
     """The VALU streaming kernels (the matrix-core A/B competitors: fp32 FMAs, v_dot2 pairs) on bf16 pools, ragged
     lengths with partial blocks and tiles, against the oracle to the north-star bound."""
     run(RAGGED + [2100, 64], heads, 16, torch.bfloat16, splits, impl=impl)
+
+
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_l2_merge_reads_this_calls_partials(heads):
+    """On the split grid with S * Hkv a multiple of 8 the fused merge reads the partials from the XCD's L2. Calls
+    that alternate between two batches of the same shape (the same workspace addresses) each match the oracle on
+    their own inputs, so no partial of an earlier call is read back; a batch whose S * Hkv is not a multiple of 8
+    (merged through memory) in between changes nothing."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [700, 2100, 33, 4096, 1000, 1, 3000, 129]  # S = 8: S * Hkv = 16
+    cases = [make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=s) for s in (41, 42)]
+    odd = make_case(lengths[:3], Hq, Hkv, D, 16, torch.bfloat16, seed=43)  # S * Hkv = 6
+    refs = [oracle_decode(q, k, v, t, lengths, D ** -0.5, np.float32) for q, k, v, _, _, t in cases]
+    print(f"case l2 merge alternation {heads}", flush=True)
+    for rep in range(3):
+        for i, (q, k, v, bt, ctx, _) in enumerate(cases):
+            out = paged_decode_attention(q, k, v, bt, ctx, D ** -0.5, max(lengths), num_splits=4)
+            torch.cuda.synchronize()
+            assert_decode_close(out.double().cpu().numpy(), refs[i], f"l2 merge rep {rep} batch {i}")
+        q, k, v, bt, ctx, _ = odd
+        paged_decode_attention(q, k, v, bt, ctx, D ** -0.5, max(lengths[:3]), num_splits=4)

@@ -331,3 +331,27 @@ def test_merge_paths_agree(shape, splits):
     assert_bf16_close(mem.double().cpu().numpy()[rows], ref32[rows], "merge through memory")
     with pytest.raises(ValueError):
         run("l2")
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+def test_l2_merge_reads_this_calls_partials(shape):
+    """The prefill merge from the XCD's L2: calls alternating between two inputs of one shape (the same workspace
+    addresses) each give the memory-path bits of their own inputs, so no partial of an earlier call is read
+    back."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [3000, 700], [700, 300]
+    cases = [make_prefill(ctx, qlen, Hq, Hkv, D, seed=s) for s in (51, 52)]
+    scale = D ** -0.5
+    print(f"case prefill l2 merge alternation {shape}", flush=True)
+
+    def run(i, path):
+        q, k, v, bt, c, st, ln = cases[i][:7]
+        return paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), num_splits=6,
+                                       merge_path=path)
+
+    want = [run(i, "memory").clone() for i in (0, 1)]
+    for rep in range(3):
+        for i in (0, 1):
+            got = run(i, "auto")
+            torch.cuda.synchronize()
+            assert torch.equal(got, want[i]), f"rep {rep} input {i}"
