@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 4
+#define SIPA_ABI_VERSION 5
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -225,6 +225,10 @@ typedef struct sipa_prefill_params {
      they all shared one (the kernel places them so), through memory otherwise; SIPA_MERGE_MEMORY always reads
      them through memory (agent-coherent loads). Both give the same bits. */
   int32_t merge_path;
+  /* Column tiles (a query head and 16 of the unit's tokens) per wave (ABI 5): 0 lets the library choose (one per
+     wave in 8-wave workgroups when the grid has at most two workgroups per CU and the pool is bf16 or per-token
+     INT8, two per wave in 4-wave workgroups otherwise); 1 or 2 forces it. Both give the same bits. */
+  int32_t cols_per_wave;
 } sipa_prefill_params;
 
 enum { SIPA_MERGE_AUTO = 0, SIPA_MERGE_MEMORY = 1 };

@@ -141,17 +141,22 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
 
 // NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
 // issued NPRE tiles before its LDS store.
-template <int D, int NPRE, int MODE, int KT>
-__global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs a) {
+// CW: column tiles per wave; the workgroup has 8 / CW waves, so that its 8 column tiles are always covered.
+template <int D, int NPRE, int MODE, int KT, int CW>
+__global__ void __launch_bounds__(64 * 8 / CW) prefill_mfma_bf16(const PrefillArgs a) {
   static_assert(KT == 32 || KT == 64, "key tiles of 32 or 64 keys");
+  static_assert(CW == 1 || CW == 2, "one or two column tiles per wave");
+  constexpr int PW = 8 / CW, PT = 64 * PW;   // waves and threads of the workgroup
   constexpr int MT = KT / 16, HT = KT / 32;  // 16-key row tiles, 32-key halves
-  constexpr int CW = prefill_cols_per_wave(D);
-  constexpr int kSlots = CW * kWaves * 16;  // (column, token) rows of a split state
+  constexpr int kSlots = CW * PW * 16;       // (column, token) rows of a split state
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = HT * PrefillSmem<D>::kTile;
   constexpr int CH = MODE == 0 ? 8 : 16;   // channels per cooperative-load chunk: 16 bytes of bf16 or of codes
   constexpr int CPK = D / CH;               // chunks per key row
-  constexpr int LPT = KT * CPK / kThreads;  // chunks per thread per K (or V) tile
-  static_assert(LPT * kThreads == KT * CPK, "tile chunks must divide over the workgroup");
+  constexpr int NCH = KT * CPK;                // chunks per K (or V) tile
+  constexpr int LPT = (NCH + PT - 1) / PT;     // chunks per thread per K (or V) tile
+  static_assert(NCH % PT == 0 || (LPT == 1 && NCH % 64 == 0), "tile chunks must divide over whole waves");
+  // threads past the tile's chunks (NCH < PT: whole waves) take no part in the cooperative load
+  const bool loads = NCH >= PT || (int)threadIdx.x < NCH;
   __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
@@ -188,7 +193,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
   const int last_col = a.bt_w - 1 - (k_lo >> 4);  // >= nblk - 1 when the host's width check held
-  for (int i = threadIdx.x; i < nblk; i += kThreads) bids[i] = min(max(btr[min(i, last_col)], 0), a.nb - 1);
+  for (int i = threadIdx.x; i < nblk; i += PT) bids[i] = min(max(btr[min(i, last_col)], 0), a.nb - 1);
 
   // Column tiles c = wave + 4 ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15 with
   // tt = c / G (G * TT <= 8). A column tile's B operand holds token r of head g (zero past the unit's tokens).
@@ -197,7 +202,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   bf16x8 qop[CW][KS];
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) {
-    const int c = wave + kWaves * ci;
+    const int c = wave + PW * ci;
     cg[ci] = c % G;
     ctok[ci] = 16 * (c / G);
     cvalid[ci] = c / G < TT && ctok[ci] < ntok;
@@ -235,9 +240,10 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
   const int tail = MODE == 2 ? min(a.tails[s], a.n_stage - 1) : -1;
   KvRaw<MODE> raw[NPRE][LPT];
   auto gload = [&](int set, int t) {
+    if (!loads) return;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int c = threadIdx.x + kThreads * i, cg = c % CPK;
+      const int c = threadIdx.x + PT * i, cg = c % CPK;
       const int rel = min(KT * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
       const int64_t blk = bids[rel >> 4];
       const int off = rel & 15;
@@ -288,9 +294,10 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     }
   };
   auto sstore = [&](int set, int buf) {
+    if (!loads) return;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int c = threadIdx.x + kThreads * i;
+      const int c = threadIdx.x + PT * i;
       const int e = (c / CPK) * P + CH * (c % CPK);
       const KvRaw<MODE>& x = raw[set][i];
       if constexpr (MODE == 0) {
@@ -435,7 +442,7 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
       if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
-      const int slot = 16 * (wave + kWaves * ci) + r;
+      const int slot = 16 * (wave + PW * ci) + r;
       const float inv = lsum[ci] > 0.f ? 1.f / lsum[ci] : 0.f;  // l = 0: the token sees no key of this split
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -466,8 +473,8 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
     __syncthreads();
     if (!last_flag) return;
     const bool from_l2 = last_flag == 2;
-    // The last split to arrive merges every split's state: thread t takes row t / 2 (column c, token rr) and
-    // half of its channels, in batches of 32 channels; per round of KB splits it reads the row's m and l and
+    // The last split to arrive merges every split's state: thread t takes row t / TPR (column c, token rr) and
+    // 1 / TPR of its channels, in batches of up to 32 channels; per round of KB splits it reads the row's m and l and
     // keeps all of the round's channel loads in flight together. KB and the batch width hold the merge's
     // registers under what the key loop needs, so the merge costs no occupancy. AUX: the loads' cache policy.
     const __amdgpu_buffer_rsrc_t mrows = __builtin_amdgcn_make_buffer_rsrc(
@@ -476,13 +483,13 @@ __global__ void __launch_bounds__(kThreads) prefill_mfma_bf16(const PrefillArgs 
         a.pl + (int64_t)u * a.nsplit * kSlots, (short)0, a.nsplit * kSlots * 4, 0x00020000);
     auto merge = [&](auto aux_tag) {
       constexpr int AUX = decltype(aux_tag)::value;
-      constexpr int HALF = D / 2, CB = 32, KB = 4;
-      const int slot = threadIdx.x >> 1;
+      constexpr int TPR = PT / kSlots, CPT = D / TPR, CB = CPT < 32 ? CPT : 32, KB = 4;  // threads per row
+      const int slot = threadIdx.x / TPR, part = threadIdx.x % TPR;
       const int c = slot >> 4, rr = slot & 15;
       const int g = c % G, tok = 16 * (c / G) + rr;
       if (c / G < TT && tok < ntok) {
         uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + tok) * a.o_st + (int64_t)(h * G + g) * a.o_sh;
-        for (int c0 = HALF * (threadIdx.x & 1); c0 < HALF * ((threadIdx.x & 1) + 1); c0 += CB) {
+        for (int c0 = CPT * part; c0 < CPT * (part + 1); c0 += CB) {
           float M = kNegInf, den = 0.f;
           f32x4 num[CB / 4];
 #pragma unroll
@@ -626,6 +633,16 @@ extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_
   return prefill_layout(units, nsplit, head_dim).total;
 }
 
+template <int D, int NPRE, int KT, int CW>
+static void launch_prefill(int mode, dim3 grid, dim3 block, hipStream_t st, const PrefillArgs& a) {
+  if (mode == SIPA_KV_PLAIN)
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 0, KT, CW>), grid, block, 0, st, a);
+  else if (mode == SIPA_KV_INT8_TOKEN)
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 1, KT, CW>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 2, KT, CW>), grid, block, 0, st, a);
+}
+
 extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   SIPA_CHECK(p != nullptr && p->struct_size == (int32_t)sizeof(sipa_prefill_params), SIPA_EINVAL,
              "struct_size does not match this library's sipa_prefill_params (%d bytes)",
@@ -745,19 +762,28 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.pl = nsplit > 1 ? (float*)(ws + lay.pl) : nullptr;
   a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)wgs), block(kThreads);
+  // Waves per workgroup: a grid of at most two workgroups per CU (a chunk over a long context, split) is
+  // latency-bound, and runs faster with one column tile per wave in 8-wave workgroups (16 waves per CU instead
+  // of 8); a larger grid keeps two column tiles per wave in 4-wave workgroups, whose shared K/V operand reads
+  // and lower VALU overhead win once three workgroups share a CU (512 keys at 8K context: 36.6 -> 35.0 us;
+  // four 2048-token prompts 60.0 -> 63.9 us the other way). Format B's 8-wave kernels hold too many registers
+  // for two workgroups per CU, so it keeps 4-wave workgroups.
+  SIPA_CHECK(p->cols_per_wave >= 0 && p->cols_per_wave <= 2, SIPA_EINVAL, "cols_per_wave %d not in {0, 1, 2}",
+             p->cols_per_wave);
+  const int cw = p->cols_per_wave ? p->cols_per_wave
+                                  : (mode != SIPA_KV_INT8_KCHAN && wgs <= 2LL * sipa_device_cu_count(-1) ? 1 : 2);
+  const dim3 grid((unsigned)wgs), block(64 * 8 / cw);
   // Key tiles: 64 keys at head_dim 64 (one barrier, one max reduction and one rescale test per 64 keys: four
   // 2048-token prompts 94 -> 84 us), 32 at head_dim 128, whose registers would otherwise halve the waves per SIMD
   // (166 -> 221 us). Tiles in flight (NPRE) within the register budget.
-  if (D == 64) {
-    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 0, 64>), grid, block, 0, st, a);
-    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 1, 64>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_mfma_bf16<64, 2, 2, 64>), grid, block, 0, st, a);
-  } else {
-    if (mode == SIPA_KV_PLAIN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 0, 32>), grid, block, 0, st, a);
-    else if (mode == SIPA_KV_INT8_TOKEN) hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 1, 32>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_mfma_bf16<128, 2, 2, 32>), grid, block, 0, st, a);
-  }
+  if (D == 64 && cw == 1)
+    launch_prefill<64, 2, 64, 1>(mode, grid, block, st, a);
+  else if (D == 64)
+    launch_prefill<64, 2, 64, 2>(mode, grid, block, st, a);
+  else if (cw == 1)
+    launch_prefill<128, 2, 32, 1>(mode, grid, block, st, a);
+  else
+    launch_prefill<128, 2, 32, 2>(mode, grid, block, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
   return SIPA_OK;

@@ -41,7 +41,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                             scale: float, max_context: int, max_query_len: int,
                             out: torch.Tensor | None = None, *, num_splits: int | None = None,
                             host_query_lens: list[int] | None = None, quant=None,
-                            merge_path: str = "auto") -> torch.Tensor:
+                            merge_path: str = "auto", cols_per_wave: int = 0) -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16 (int8 with
@@ -57,6 +57,8 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     reference's gather path does, q * s in fp32 rounded to bf16.
     merge_path: "auto" merges a query tile's key splits from the L2 of the XCD they ran on when they shared one
     (the kernel places them so), through memory otherwise; "memory" always through memory. Same bits either way.
+    cols_per_wave: 0 lets the library pick the workgroup layout (one column tile per wave in 8-wave workgroups
+    for grids of at most two workgroups per CU, two per wave in 4-wave workgroups otherwise); 1 or 2 forces it.
     """
     S = block_tables.shape[0]
     T, Hq, D = q.shape
@@ -113,6 +115,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     if merge_path not in ("auto", "memory"):
         raise ValueError(f"merge_path {merge_path!r} is neither 'auto' nor 'memory'")
     p.merge_path = 1 if merge_path == "memory" else 0
+    if cols_per_wave not in (0, 1, 2):
+        raise ValueError(f"cols_per_wave {cols_per_wave} is not 0, 1 or 2")
+    p.cols_per_wave = cols_per_wave
     stream = _hip.stream_of(q)
     nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)
     if nbytes > 0:

@@ -355,3 +355,27 @@ def test_l2_merge_reads_this_calls_partials(shape):
             got = run(i, "auto")
             torch.cuda.synchronize()
             assert torch.equal(got, want[i]), f"rep {rep} input {i}"
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g4", "g1", "g3"])
+@pytest.mark.parametrize("pool", ["bf16", "int8", "int8-kchannel"])
+@pytest.mark.parametrize("splits", [1, None], ids=["one_split", "auto"])
+def test_wave_layouts_agree(shape, pool, splits):
+    """One column tile per wave (8-wave workgroups) and two per wave (4-wave workgroups) compute every column
+    with the same operations in the same order, so the layouts give the same bits, each one's unused column tiles
+    (G < 8) included; the oracle checks of the other tests run whichever the library picks."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [300, 1000, 33, 517], [64, 7, 33, 200]
+    print(f"case wave layouts shape={shape} pool={pool} splits={splits}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=61)
+    quant = None
+    if pool != "bf16":
+        g = torch.Generator(device="cuda").manual_seed(7)
+        quant, k, v, _, _ = int8_pools(k, v, pool, ctx, tables, g)
+    run = lambda cw: paged_prefill_attention(q, k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen),  # noqa: E731
+                                             num_splits=splits, quant=quant, cols_per_wave=cw)
+    one, two, auto = run(1), run(2), run(0)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two) and torch.equal(one, auto)
+    with pytest.raises(ValueError):
+        run(4)
