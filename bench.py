@@ -8,7 +8,8 @@ is one pass over the pool's rotated layers: one paged_decode_attention call per 
 decode step makes one call per layer), each over the whole batch with the CU-count split policy and the fused split
 merge. `value` (GB/s) and `config.us_per_call` are per call; `ms_per_step` covers the step's calls.
 
-Bytes per call are algorithmic: K and V actually read from the pool plus Q and O (512 B per token + 3,584 B per
+Every timed region follows W warm-up calls and at least 0.3 s of back-to-back calls of the same kind, so that the
+GPU runs at the clocks sustained work gets (an idle GPU clocks down). Bytes per call are algorithmic: K and V actually read from the pool plus Q and O (512 B per token + 3,584 B per
 sequence for 0.5B); block tables and split partials are not counted. Calls rotate over 8 layers of a
 [8, 2, 32768, 16, 64] pool so each call streams memory the previous calls did not touch (the 256 MB MALL cannot
 serve it). Inputs are resident in HBM before the timed region.
@@ -84,10 +85,21 @@ class Decode:
             _hip.check(rc, self.name)
 
 
-def time_calls(fn, steps: int, warmup: int, per_launch: bool):
-    """(ms per call over a back-to-back region, mean µs per call from event pairs around each call or None)."""
-    for i in range(warmup):
+# Seconds of back-to-back calls before each timed region, after the `warmup` calls: a GPU left idle lowers its
+# clocks, and a few calls do not raise them again (one 512-token prefill chunk at 8K context took 34.6-35.5 µs a
+# call timed after 1 s idle, 33.1 after 10 warm-up calls, 30.9 after 0.5 s of calls).
+WARM_S = 0.3
+
+
+def time_calls(fn, steps: int, warmup: int, per_launch: bool, warm_s: float = WARM_S):
+    """(ms per call over a back-to-back region, mean µs per call from event pairs around each call or None).
+    Warm-up: `warmup` calls, then more until `warm_s` seconds of calls have run."""
+    t0, i = time.perf_counter(), 0
+    while i < warmup or time.perf_counter() - t0 < warm_s:
         fn(i)
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()  # the host stays within 32 calls of the GPU
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -507,7 +519,7 @@ def stream_ceiling(steps: int) -> dict:
                     if lib.sipa_probe_read(bufs[i % 4].data_ptr(), nbytes, sink.data_ptr(), wgs, unroll, nt,
                                            stream):
                         raise RuntimeError("probe read launch failed")
-                ms, kus = time_calls(rd, max(8, steps // 20), 4, True)
+                ms, kus = time_calls(rd, max(8, steps // 20), 4, True, warm_s=0.0)  # the sweep runs back to back
                 gbs = nbytes / (kus * 1e-6) / 1e9
                 sweep.append((wgs, unroll, nt, round(gbs, 1)))
                 if gbs > best.get("gb_s", 0):

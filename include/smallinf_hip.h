@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 5
+#define SIPA_ABI_VERSION 6
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -225,25 +225,36 @@ typedef struct sipa_prefill_params {
      they all shared one (the kernel places them so), through memory otherwise; SIPA_MERGE_MEMORY always reads
      them through memory (agent-coherent loads). Both give the same bits. */
   int32_t merge_path;
-  /* Column tiles (a query head and 16 of the unit's tokens) per wave (ABI 5): 0 lets the library choose (one per
-     wave in 8-wave workgroups when the grid has at most two workgroups per CU and the pool is bf16 or per-token
-     INT8, two per wave in 4-wave workgroups otherwise); 1 or 2 forces it. Both give the same bits. */
-  int32_t cols_per_wave;
+  /* Workgroup layout (ABI 6), a SIPA_PREFILL_* value. A column tile is a query head and 16 of a unit's tokens.
+     SIPA_PREFILL_AUTO lets the library choose from the grid of 8-column workgroups: SIPA_PREFILL_W4X2 above two
+     per CU (and always for format B pools, SIPA_KV_INT8_KCHAN, which take SIPA_PREFILL_W4X2 or _W8X1 only);
+     SIPA_PREFILL_W16X1 above one and up to two per CU when max_context >= 2 max_query_len and the key splits
+     (if more than one) are at least 1024 keys long; SIPA_PREFILL_W8X1 otherwise. W4X2 and W8X1 give the same bits; W16X1 too with one split (with several, a row may go through the
+     split merge's fp16 partials in one layout and not in the other). */
+  int32_t wg_layout;
 } sipa_prefill_params;
 
 enum { SIPA_MERGE_AUTO = 0, SIPA_MERGE_MEMORY = 1 };
+enum {
+  SIPA_PREFILL_AUTO = 0,
+  SIPA_PREFILL_W4X2 = 1,  /* 4 waves of two column tiles: 8 column tiles per workgroup */
+  SIPA_PREFILL_W8X1 = 2,  /* 8 waves of one column tile: 8 column tiles per workgroup */
+  SIPA_PREFILL_W16X1 = 3  /* 16 waves of one column tile: 16 column tiles (a unit of twice the tokens) */
+};
 
 int32_t sipa_prefill(const sipa_prefill_params* p, void* stream);
 
 /* Key splits for a prefill call (no counterpart in the reference, whose gather path has no grid): about two
- * workgroups per CU over the call's units, at least 256 keys per split, at most 32 splits. A unit is a KV head
- * and 16 tt new tokens of one sequence, tt = 8 / G 16-token subtiles (at least 1) for a group of G = Hq / Hkv
- * query heads (head_dim is part of the policy's signature; both head dims use 8 column tiles today);
- * query_tiles = sum over sequences of ceil(query_len / 16). cu_count <= 0 asks the current device. */
+ * workgroups per CU over the call's 8-column units, at least 256 keys per split, at most 32 splits. An 8-column
+ * unit is a KV head and 16 tt new tokens of one sequence, tt = 8 / G 16-token subtiles (at least 1) for a group
+ * of G = Hq / Hkv query heads (head_dim is part of the policy's signature and does not change it today);
+ * query_tiles = sum over sequences of ceil(query_len / 16). A 16-column layout keeps the split count and runs
+ * half as many units. cu_count <= 0 asks the current device. */
 int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t query_tiles,
                             int32_t max_context, int32_t cu_count);
 
-/* Workspace bytes sipa_prefill needs for these sizes and num_splits (0 when one split runs). */
+/* Workspace bytes sipa_prefill needs for these sizes and num_splits under any workgroup layout (0 when one
+ * split runs). */
 int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                                      int32_t head_dim, int32_t max_query_len, int32_t max_context,
                                      int32_t num_splits);

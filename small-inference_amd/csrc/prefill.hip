@@ -63,18 +63,25 @@ struct PrefillArgs {
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Column tiles (head, 16 tokens) per wave. Two at either head_dim: four at head_dim 64 (more independent softmax
-// chains per wave, each K/V operand read serving four MFMA columns) measured slower, 86.7 -> 112 us on four 2048-token
-// prompts, with the register use halving the waves per SIMD and the 32-token units coarsening the causal tiles.
-constexpr int prefill_cols_per_wave(int /*D*/) { return 2; }
+// Workgroup layouts: NC column tiles (a query head and 16 tokens) per workgroup, CW per wave, NC / CW waves.
+//   SIPA_PREFILL_W4X2 (NC 8, CW 2): 4 waves; each K/V operand read serves two column tiles. Large grids.
+//   SIPA_PREFILL_W8X1 (NC 8, CW 1): 8 waves, twice the waves per CU for grids of at most 2 workgroups per CU.
+//   SIPA_PREFILL_W16X1 (NC 16, CW 1): 16 waves over two query tiles' worth of columns, one workgroup per CU where
+//   two 8-column workgroups would share it (the later-dispatched of two co-resident workgroups ran 30% longer
+//   than the first, its solo tail idling the CU's other SIMD slots); each K/V tile load serves both query tiles.
+// Four column tiles per wave (at head_dim 64) measured slower, 86.7 -> 112 us on four 2048-token prompts, with
+// the register use halving the waves per SIMD and the 32-token units coarsening the causal tiles.
 constexpr int kPrefillMaxGroup = 8;
-
-// 16-token subtiles per unit for a GQA group of G heads: as many as fit the workgroup's 8 column tiles (G = 7: 1,
-// G = 4: 2, G = 1: 8), so every group size keeps the waves busy.
-static inline int prefill_subtiles(int G, int D) {
-  const int cols = prefill_cols_per_wave(D) * kWaves;
-  return G >= cols ? 1 : cols / G;
+struct PfShape {
+  int nc, cw;
+};
+static inline PfShape prefill_shape(int layout) {
+  return layout == SIPA_PREFILL_W8X1 ? PfShape{8, 1} : layout == SIPA_PREFILL_W16X1 ? PfShape{16, 1} : PfShape{8, 2};
 }
+
+// 16-token subtiles per unit for a GQA group of G heads: as many as fit the workgroup's NC column tiles (NC 8:
+// G = 7: 1, G = 4: 2, G = 1: 8), so every group size keeps the waves busy.
+static inline int prefill_subtiles(int G, int nc) { return G >= nc ? 1 : nc / G; }
 constexpr int kPrefillMaxSplits = 32;
 
 
@@ -141,14 +148,15 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
 
 // NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
 // issued NPRE tiles before its LDS store.
-// CW: column tiles per wave; the workgroup has 8 / CW waves, so that its 8 column tiles are always covered.
-template <int D, int NPRE, int MODE, int KT, int CW>
-__global__ void __launch_bounds__(64 * 8 / CW) prefill_mfma_bf16(const PrefillArgs a) {
+// NC: column tiles per workgroup; CW: column tiles per wave (the workgroup has NC / CW waves).
+template <int D, int NPRE, int MODE, int KT, int CW, int NC>
+__global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillArgs a) {
   static_assert(KT == 32 || KT == 64, "key tiles of 32 or 64 keys");
   static_assert(CW == 1 || CW == 2, "one or two column tiles per wave");
-  constexpr int PW = 8 / CW, PT = 64 * PW;   // waves and threads of the workgroup
+  static_assert(NC == 8 || NC == 16, "8 or 16 column tiles per workgroup");
+  constexpr int PW = NC / CW, PT = 64 * PW;  // waves and threads of the workgroup
   constexpr int MT = KT / 16, HT = KT / 32;  // 16-key row tiles, 32-key halves
-  constexpr int kSlots = CW * PW * 16;       // (column, token) rows of a split state
+  constexpr int kSlots = NC * 16;            // (column, token) rows of a split state
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = HT * PrefillSmem<D>::kTile;
   constexpr int CH = MODE == 0 ? 8 : 16;   // channels per cooperative-load chunk: 16 bytes of bf16 or of codes
   constexpr int CPK = D / CH;               // chunks per key row
@@ -600,10 +608,10 @@ struct PrefillLayout {
   int64_t counters, pm, pl, part, total;  // byte offsets into the workspace
 };
 
-static PrefillLayout prefill_layout(int64_t units, int nsplit, int D) {
+static PrefillLayout prefill_layout(int64_t units, int nsplit, int D, int nc) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   PrefillLayout l;
-  const int64_t rows = units * nsplit * prefill_cols_per_wave(D) * kWaves * 16;
+  const int64_t rows = units * nsplit * nc * 16;
   l.counters = 0;
   l.pm = kCounterBytes;
   l.pl = l.pm + up(rows * 4);
@@ -616,7 +624,7 @@ extern "C" int32_t sipa_prefill_splits(int32_t num_q_heads, int32_t num_kv_heads
                                        int64_t query_tiles, int32_t max_context, int32_t cu_count) {
   if (num_kv_heads <= 0 || num_q_heads < num_kv_heads) return 1;
   if (cu_count <= 0) cu_count = sipa_device_cu_count(-1);
-  const int tt = prefill_subtiles(num_q_heads / num_kv_heads, head_dim);
+  const int tt = prefill_subtiles(num_q_heads / num_kv_heads, 8);
   return prefill_splits_host((int64_t)num_kv_heads * ((query_tiles + tt - 1) / tt), max_context, cu_count);
 }
 
@@ -628,19 +636,24 @@ extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_
   const int chunk = prefill_chunk(max_context, num_splits);
   const int nsplit = (max_context + chunk - 1) / chunk;
   if (nsplit <= 1) return 0;
-  const int nt = 16 * prefill_subtiles(num_q_heads / num_kv_heads, head_dim);
-  const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + nt - 1) / nt);
-  return prefill_layout(units, nsplit, head_dim).total;
+  int64_t most = 0;  // the largest over the workgroup layouts sipa_prefill may pick
+  for (const int nc : {8, 16}) {
+    const int nt = 16 * prefill_subtiles(num_q_heads / num_kv_heads, nc);
+    const int64_t units = (int64_t)num_seqs * num_kv_heads * ((max_query_len + nt - 1) / nt);
+    most = std::max(most, prefill_layout(units, nsplit, head_dim, nc).total);
+  }
+  return most;
 }
 
-template <int D, int NPRE, int KT, int CW>
-static void launch_prefill(int mode, dim3 grid, dim3 block, hipStream_t st, const PrefillArgs& a) {
+template <int D, int NPRE, int KT, int CW, int NC>
+static void launch_prefill(int mode, dim3 grid, hipStream_t st, const PrefillArgs& a) {
+  const dim3 block(64 * NC / CW);
   if (mode == SIPA_KV_PLAIN)
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 0, KT, CW>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 0, KT, CW, NC>), grid, block, 0, st, a);
   else if (mode == SIPA_KV_INT8_TOKEN)
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 1, KT, CW>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 2, KT, CW>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 1, KT, CW, NC>), grid, block, 0, st, a);
+  else if constexpr (NC == 8)  // format B at 16 columns is refused by the host (register budget)
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 2, KT, CW, NC>), grid, block, 0, st, a);
 }
 
 extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
@@ -685,27 +698,57 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
                      p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
                  SIPA_EINVAL, "format B needs a 16-byte aligned bf16 staging pool and tail slots");
   }
-  const int tt = prefill_subtiles(G, D);
-  const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
-  const int64_t units = (int64_t)S * Hkv * qtiles;
+  SIPA_CHECK(p->wg_layout >= SIPA_PREFILL_AUTO && p->wg_layout <= SIPA_PREFILL_W16X1, SIPA_EINVAL,
+             "wg_layout %d is not a SIPA_PREFILL_* layout", p->wg_layout);
+  // The split count and the layout choice are made over 8-column units; a 16-column layout then runs half as
+  // many units with the same splits.
+  const int tt8 = prefill_subtiles(G, 8);
+  const int64_t units8 = (int64_t)S * Hkv * ((p->max_query_len + 16 * tt8 - 1) / (16 * tt8));
+  const int cus = sipa_device_cu_count(-1);
   int splits = p->num_splits;
-  if (splits <= 0) splits = prefill_splits_host(units, p->max_context, sipa_device_cu_count(-1));
+  if (splits <= 0) splits = prefill_splits_host(units8, p->max_context, cus);
   const int chunk = prefill_chunk(p->max_context, splits);
   const int nsplit = (p->max_context + chunk - 1) / chunk;
   // split launches: whole groups of 8 units, one XCD each (the kernel's workgroup-to-unit mapping)
-  const int64_t wgs = (nsplit > 1 ? (units + 7) / 8 * 8 : units) * nsplit;
+  auto grid_of = [&](int64_t units) { return (nsplit > 1 ? (units + 7) / 8 * 8 : units) * nsplit; };
+  // Layout (SIPA_PREFILL_AUTO), from the grid of 8-column workgroups:
+  //  - more than two per CU: 4-wave workgroups of two column tiles per wave, whose shared K/V operand reads and
+  //    lower VALU overhead win once three workgroups share a CU;
+  //  - one to two per CU with balanced units (a chunk at least its own length into its context: the causal
+  //    triangle then varies a unit's keys by at most a factor of two) and splits of at least 1024 keys: 16-wave
+  //    workgroups of 16 column tiles, one per CU. The later-dispatched of two co-resident 8-column workgroups
+  //    runs ~30% longer than the first and finishes alone; 512 new tokens at 16K 51.3 -> 49.4 us, two chunks of
+  //    512 at 8K 50.4 -> 47.8, at head_dim 128 51.7 -> 50.3, INT8 per-token at 8K 37.3 -> 33.9 (bf16 at 8K: even);
+  //  - otherwise 8-wave workgroups: at most one per CU; a fresh prompt, whose 32-token units would double the
+  //    longest CU's keys (one 2048-token prompt 26.9 -> 28.3 us, two at head_dim 128 59 -> 71 us); or short
+  //    splits, which leave the one merging workgroup per unit the larger share (512 at 4K: 19.8 -> 21.4 us).
+  // Format B's one-column waves hold too many registers for 16 waves, so it takes the 4-wave layout.
+  int layout = p->wg_layout;
+  if (layout == SIPA_PREFILL_AUTO) {
+    const int64_t g8 = grid_of(units8);
+    if (mode == SIPA_KV_INT8_KCHAN || g8 > 2LL * cus) layout = SIPA_PREFILL_W4X2;
+    else if (g8 > cus && p->max_context >= 2LL * p->max_query_len && (nsplit == 1 || chunk >= 1024))
+      layout = SIPA_PREFILL_W16X1;
+    else layout = SIPA_PREFILL_W8X1;
+  }
+  SIPA_CHECK(mode != SIPA_KV_INT8_KCHAN || layout != SIPA_PREFILL_W16X1, SIPA_EUNSUPPORTED,
+             "SIPA_PREFILL_W16X1 does not take format B pools (its 16-wave workgroups cannot hold their registers)");
+  const PfShape shape = prefill_shape(layout);
+  const int tt = prefill_subtiles(G, shape.nc);
+  const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
+  const int64_t units = (int64_t)S * Hkv * qtiles;
+  const int64_t wgs = grid_of(units);
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   PrefillLayout lay{};
   if (nsplit > 1) {
     SIPA_CHECK(units <= kMaxCounters, SIPA_EINVAL,
                "%lld query tiles x KV heads exceed the %d merge counters of a split launch; use one split",
                (long long)units, kMaxCounters);
-    lay = prefill_layout(units, nsplit, D);
+    lay = prefill_layout(units, nsplit, D, shape.nc);
     SIPA_CHECK(p->workspace != nullptr && ((uintptr_t)p->workspace & 255) == 0 && p->workspace_bytes >= lay.total,
                SIPA_EWORKSPACE, "%d key splits need a 256-byte aligned workspace of %lld bytes (have %lld)", nsplit,
                (long long)lay.total, (long long)p->workspace_bytes);
-    SIPA_CHECK((int64_t)nsplit * prefill_cols_per_wave(D) * kWaves * 16 * D * 4 <= 0x7fffffff, SIPA_EINVAL,
-               "split state too large");
+    SIPA_CHECK((int64_t)nsplit * shape.nc * 16 * D * 4 <= 0x7fffffff, SIPA_EINVAL, "split state too large");
   }
   PrefillArgs a;
   a.q = p->q;
@@ -762,28 +805,19 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   a.pl = nsplit > 1 ? (float*)(ws + lay.pl) : nullptr;
   a.part = nsplit > 1 ? (float*)(ws + lay.part) : nullptr;
   hipStream_t st = (hipStream_t)stream;
-  // Waves per workgroup: a grid of at most two workgroups per CU (a chunk over a long context, split) is
-  // latency-bound, and runs faster with one column tile per wave in 8-wave workgroups (16 waves per CU instead
-  // of 8); a larger grid keeps two column tiles per wave in 4-wave workgroups, whose shared K/V operand reads
-  // and lower VALU overhead win once three workgroups share a CU (512 keys at 8K context: 36.6 -> 35.0 us;
-  // four 2048-token prompts 60.0 -> 63.9 us the other way). Format B's 8-wave kernels hold too many registers
-  // for two workgroups per CU, so it keeps 4-wave workgroups.
-  SIPA_CHECK(p->cols_per_wave >= 0 && p->cols_per_wave <= 2, SIPA_EINVAL, "cols_per_wave %d not in {0, 1, 2}",
-             p->cols_per_wave);
-  const int cw = p->cols_per_wave ? p->cols_per_wave
-                                  : (mode != SIPA_KV_INT8_KCHAN && wgs <= 2LL * sipa_device_cu_count(-1) ? 1 : 2);
-  const dim3 grid((unsigned)wgs), block(64 * 8 / cw);
+  const dim3 grid((unsigned)wgs);
   // Key tiles: 64 keys at head_dim 64 (one barrier, one max reduction and one rescale test per 64 keys: four
   // 2048-token prompts 94 -> 84 us), 32 at head_dim 128, whose registers would otherwise halve the waves per SIMD
   // (166 -> 221 us). Tiles in flight (NPRE) within the register budget.
-  if (D == 64 && cw == 1)
-    launch_prefill<64, 2, 64, 1>(mode, grid, block, st, a);
-  else if (D == 64)
-    launch_prefill<64, 2, 64, 2>(mode, grid, block, st, a);
-  else if (cw == 1)
-    launch_prefill<128, 2, 32, 1>(mode, grid, block, st, a);
-  else
-    launch_prefill<128, 2, 32, 2>(mode, grid, block, st, a);
+  if (D == 64) {
+    if (shape.nc == 16) launch_prefill<64, 2, 64, 1, 16>(mode, grid, st, a);
+    else if (shape.cw == 1) launch_prefill<64, 2, 64, 1, 8>(mode, grid, st, a);
+    else launch_prefill<64, 2, 64, 2, 8>(mode, grid, st, a);
+  } else {
+    if (shape.nc == 16) launch_prefill<128, 2, 32, 1, 16>(mode, grid, st, a);
+    else if (shape.cw == 1) launch_prefill<128, 2, 32, 1, 8>(mode, grid, st, a);
+    else launch_prefill<128, 2, 32, 2, 8>(mode, grid, st, a);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
   return SIPA_OK;

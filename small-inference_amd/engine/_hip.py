@@ -17,7 +17,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library; see th
 
 # SIPA_LIB overrides the location (for copies of these modules placed inside another package).
 LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # element types (SIPA_F32 ...)
 F32, BF16, F16, I8 = 0, 1, 2, 3
@@ -64,7 +64,7 @@ class PrefillParams(ctypes.Structure):
         ("v_scale", vp), ("v_scale_dtype", i32), ("vs_stride_h", i64), ("vs_stride_n", i64),
         ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64), ("num_stage", i32),
         ("tail_slots", vp), ("num_splits", i32), ("workspace", vp), ("workspace_bytes", i64), ("bt_width", i32),
-        ("merge_path", i32), ("cols_per_wave", i32),
+        ("merge_path", i32), ("wg_layout", i32),
     ]
 
 

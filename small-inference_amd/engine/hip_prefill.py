@@ -12,6 +12,9 @@ import torch
 from . import _hip
 from .hip_decode import reserve_workspace  # one split workspace per (device, stream) serves decode and prefill
 
+# wg_layout names, indexed by their SIPA_PREFILL_* values
+WG_LAYOUTS = ("auto", "w4x2", "w8x1", "w16x1")
+
 
 def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
                       max_context: int) -> bool:
@@ -41,7 +44,7 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                             scale: float, max_context: int, max_query_len: int,
                             out: torch.Tensor | None = None, *, num_splits: int | None = None,
                             host_query_lens: list[int] | None = None, quant=None,
-                            merge_path: str = "auto", cols_per_wave: int = 0) -> torch.Tensor:
+                            merge_path: str = "auto", wg_layout: str = "auto") -> torch.Tensor:
     """Causal attention of every sequence's new tokens over its paged context.
 
     q [T, Hq, D] bf16 (rows may be strided, last dim contiguous); k_cache, v_cache [Hkv, N, 16, D] bf16 (int8 with
@@ -57,8 +60,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     reference's gather path does, q * s in fp32 rounded to bf16.
     merge_path: "auto" merges a query tile's key splits from the L2 of the XCD they ran on when they shared one
     (the kernel places them so), through memory otherwise; "memory" always through memory. Same bits either way.
-    cols_per_wave: 0 lets the library pick the workgroup layout (one column tile per wave in 8-wave workgroups
-    for grids of at most two workgroups per CU, two per wave in 4-wave workgroups otherwise); 1 or 2 forces it.
+    wg_layout: the workgroup layout, waves x column tiles (a query head and 16 tokens) per wave: "w4x2", "w8x1",
+    "w16x1" (format B pools take the first two), or "auto", the library's choice by grid size and context
+    (sipa_prefill_params.wg_layout). "w4x2" and "w8x1" give the same bits, "w16x1" too with one split.
     """
     S = block_tables.shape[0]
     T, Hq, D = q.shape
@@ -115,9 +119,9 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     if merge_path not in ("auto", "memory"):
         raise ValueError(f"merge_path {merge_path!r} is neither 'auto' nor 'memory'")
     p.merge_path = 1 if merge_path == "memory" else 0
-    if cols_per_wave not in (0, 1, 2):
-        raise ValueError(f"cols_per_wave {cols_per_wave} is not 0, 1 or 2")
-    p.cols_per_wave = cols_per_wave
+    if wg_layout not in WG_LAYOUTS:
+        raise ValueError(f"wg_layout {wg_layout!r} is not one of {', '.join(WG_LAYOUTS)}")
+    p.wg_layout = WG_LAYOUTS.index(wg_layout)
     stream = _hip.stream_of(q)
     nbytes = lib.sipa_prefill_workspace_bytes(S, Hq, Hkv, D, max_query_len, max_context, num_splits)
     if nbytes > 0:

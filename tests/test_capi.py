@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_and_struct_layout():
-    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 5
+    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 6
     # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives; the
     # work-list fields, then the table width and staging count come last.
     assert _hip.DecodeParams.work_items.offset == _hip.DecodeParams.workspace_bytes.offset + 8
@@ -35,8 +35,8 @@ def test_abi_and_struct_layout():
     pad8 = lambda n: -(-n // 8) * 8  # noqa: E731  (the structs hold 8-byte members: their size rounds up to 8)
     assert ctypes.sizeof(_hip.DecodeParams) == pad8(_hip.DecodeParams.num_stage.offset + 4)
     assert _hip.PrefillParams.merge_path.offset == _hip.PrefillParams.bt_width.offset + 4
-    assert _hip.PrefillParams.cols_per_wave.offset == _hip.PrefillParams.merge_path.offset + 4
-    assert ctypes.sizeof(_hip.PrefillParams) == pad8(_hip.PrefillParams.cols_per_wave.offset + 4)
+    assert _hip.PrefillParams.wg_layout.offset == _hip.PrefillParams.merge_path.offset + 4
+    assert ctypes.sizeof(_hip.PrefillParams) == pad8(_hip.PrefillParams.wg_layout.offset + 4)
 
 
 def bad_params(**over):

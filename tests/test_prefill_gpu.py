@@ -361,9 +361,13 @@ def test_l2_merge_reads_this_calls_partials(shape):
 @pytest.mark.parametrize("pool", ["bf16", "int8", "int8-kchannel"])
 @pytest.mark.parametrize("splits", [1, None], ids=["one_split", "auto"])
 def test_wave_layouts_agree(shape, pool, splits):
-    """One column tile per wave (8-wave workgroups) and two per wave (4-wave workgroups) compute every column
-    with the same operations in the same order, so the layouts give the same bits, each one's unused column tiles
-    (G < 8) included; the oracle checks of the other tests run whichever the library picks."""
+    """The workgroup layouts compute every column tile with the same operations in the same order. 4 waves of two
+    column tiles and 8 waves of one run the same units, so they give the same bits, each one's unused column
+    tiles included. 16 waves of 16 column tiles run units of twice the tokens: with one split they give the same
+    bits too (a unit's earlier tokens also run its later tokens' key tiles, fully masked for them, which must
+    leave their bits alone); with several, a token whose 16-token unit saw one split may sit in a 32-token unit
+    that sees two, and its row then goes through the merge's fp16 partials. There the bar is the oracle's, and
+    the layouts stay within a bf16 rounding and the fp16 partial's of each other."""
     Hq, Hkv, D = SHAPES[shape]
     ctx, qlen = [300, 1000, 33, 517], [64, 7, 33, 200]
     print(f"case wave layouts shape={shape} pool={pool} splits={splits}", flush=True)
@@ -372,10 +376,32 @@ def test_wave_layouts_agree(shape, pool, splits):
     if pool != "bf16":
         g = torch.Generator(device="cuda").manual_seed(7)
         quant, k, v, _, _ = int8_pools(k, v, pool, ctx, tables, g)
-    run = lambda cw: paged_prefill_attention(q, k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen),  # noqa: E731
-                                             num_splits=splits, quant=quant, cols_per_wave=cw)
-    one, two, auto = run(1), run(2), run(0)
+    run = lambda lay: paged_prefill_attention(q, k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen),  # noqa: E731
+                                              num_splits=splits, quant=quant, wg_layout=lay)
+    want = run("w4x2")
+    layouts = ["w8x1", "auto"] + (["w16x1"] if pool != "int8-kchannel" else [])
+    got = {lay: run(lay) for lay in layouts}
     torch.cuda.synchronize()
-    assert torch.equal(one, two) and torch.equal(one, auto)
+    assert torch.equal(got["w8x1"], want)
+    if pool == "int8-kchannel":  # format B's auto layout is always w4x2
+        assert torch.equal(got["auto"], want)
+    else:
+        rows = torch.cat([torch.arange(s, s + n) for s, n in zip(starts, qlen)]).cuda()
+        for lay in ("w16x1", "auto"):  # auto picks w8x1 or w16x1 for these small grids
+            if splits == 1:
+                assert torch.equal(got[lay], want), lay
+            else:
+                a, b = got[lay][rows].float(), want[rows].float()
+                bound = 2 ** -7 * torch.maximum(a.abs(), b.abs()) + 2 ** -9
+                assert ((a - b).abs() <= bound).all(), f"{lay}: {((a - b).abs() - bound).max().item():.3e} over"
+        if quant is None:
+            scale = D ** -0.5
+            args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
+            ref32 = paged_ref.prefill(*args, dtype=np.float32)
+            npr = rows.cpu().numpy()
+            assert_bf16_close(got["w16x1"].double().cpu().numpy()[npr], ref32[npr], "w16x1")
     with pytest.raises(ValueError):
-        run(4)
+        run("w2x4")
+    if pool == "int8-kchannel":
+        with pytest.raises(ValueError, match="format B"):
+            run("w16x1")
