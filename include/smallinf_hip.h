@@ -226,11 +226,12 @@ typedef struct sipa_prefill_params {
      them through memory (agent-coherent loads). Both give the same bits. */
   int32_t merge_path;
   /* Workgroup layout (ABI 6), a SIPA_PREFILL_* value. A column tile is a query head and 16 of a unit's tokens.
-     SIPA_PREFILL_AUTO lets the library choose from the grid of 8-column workgroups: SIPA_PREFILL_W4X2 above two
-     per CU (and always for format B pools, SIPA_KV_INT8_KCHAN, which take SIPA_PREFILL_W4X2 or _W8X1 only);
-     SIPA_PREFILL_W16X1 above one and up to two per CU when max_context >= 2 max_query_len and the key splits
-     (if more than one) are at least 1024 keys long; SIPA_PREFILL_W8X1 otherwise. W4X2 and W8X1 give the same bits; W16X1 too with one split (with several, a row may go through the
-     split merge's fp16 partials in one layout and not in the other). */
+     SIPA_PREFILL_AUTO lets the library choose from g8, the grid of 8-column workgroups: SIPA_PREFILL_W8X1 for
+     g8 <= CUs; for a chunk at least its own length into its context, SIPA_PREFILL_W16X1 when the key splits (if
+     more than one) hold at least 1024 keys, else W8X1; for fresh prompts W8X1 up to 3 workgroups per CU, then
+     W16X1, except SIPA_PREFILL_W4X2 beyond 4 per CU at head_dim 64. Format B pools (SIPA_KV_INT8_KCHAN) take
+     W4X2 (W4X2 or W8X1 when forced). W4X2 and W8X1 give the same bits; W16X1 too with one split (with several,
+     a row may go through the split merge's fp16 partials in one layout and not in the other). */
   int32_t wg_layout;
 } sipa_prefill_params;
 

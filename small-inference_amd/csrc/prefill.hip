@@ -87,7 +87,10 @@ constexpr int kPrefillMaxSplits = 32;
 
 template <int D>
 struct PrefillSmem {  // one 32-key row group; a KT-key tile is KT / 32 of them
-  static constexpr int kPitch = D + 8;       // bf16 per LDS row of a 32-key tile
+  // bf16 per LDS row of a 32-key tile. D + 16 keeps the waves' K (16-byte rows) and transposing V reads free
+  // of bank conflicts; at D + 8 46% of the LDS's active cycles were conflicts, which cost little while two column
+  // tiles per wave shared each read but 1.5 us of a 512-token chunk at 8K (3.5 at head_dim 128) with one.
+  static constexpr int kPitch = D + 16;
   static constexpr int kTile = 32 * kPitch;  // elements of one K or V tile
 };
 
@@ -711,25 +714,31 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   const int nsplit = (p->max_context + chunk - 1) / chunk;
   // split launches: whole groups of 8 units, one XCD each (the kernel's workgroup-to-unit mapping)
   auto grid_of = [&](int64_t units) { return (nsplit > 1 ? (units + 7) / 8 * 8 : units) * nsplit; };
-  // Layout (SIPA_PREFILL_AUTO), from the grid of 8-column workgroups:
-  //  - more than two per CU: 4-wave workgroups of two column tiles per wave, whose shared K/V operand reads and
-  //    lower VALU overhead win once three workgroups share a CU;
-  //  - one to two per CU with balanced units (a chunk at least its own length into its context: the causal
-  //    triangle then varies a unit's keys by at most a factor of two) and splits of at least 1024 keys: 16-wave
-  //    workgroups of 16 column tiles, one per CU. The later-dispatched of two co-resident 8-column workgroups
-  //    runs ~30% longer than the first and finishes alone; 512 new tokens at 16K 51.3 -> 49.4 us, two chunks of
-  //    512 at 8K 50.4 -> 47.8, at head_dim 128 51.7 -> 50.3, INT8 per-token at 8K 37.3 -> 33.9 (bf16 at 8K: even);
-  //  - otherwise 8-wave workgroups: at most one per CU; a fresh prompt, whose 32-token units would double the
-  //    longest CU's keys (one 2048-token prompt 26.9 -> 28.3 us, two at head_dim 128 59 -> 71 us); or short
-  //    splits, which leave the one merging workgroup per unit the larger share (512 at 4K: 19.8 -> 21.4 us).
-  // Format B's one-column waves hold too many registers for 16 waves, so it takes the 4-wave layout.
+  // Layout (SIPA_PREFILL_AUTO), from g8, the grid of 8-column workgroups (warm A/B on one MI355X, 0.5B and 1.5B
+  // shapes, us per call):
+  //  - g8 <= CUs: 8-wave workgroups, one per CU (16-wave ones would leave half the CUs idle).
+  //  - a chunk at least its own length into its context (balanced units: the causal triangle varies a unit's keys
+  //    by at most a factor of two) with splits of at least 1024 keys: 16-wave workgroups of 16 column tiles, one
+  //    per CU at a time. Two co-resident 8-column workgroups do not share a CU evenly (the later-dispatched ran
+  //    ~30% longer and finished alone), and 16 column tiles share each K/V tile load: 512 new tokens at 16K
+  //    48.9 -> 46.3 (8-wave), 16 chunks of 512 at 8K 313.8 -> 290.6 (4-wave). Splits of 512 keys keep 8-wave
+  //    workgroups (512 at 4K: 19.5 against 20.7): the one merging workgroup per unit weighs more.
+  //  - fresh prompts: 8-wave workgroups up to 3 per CU (two 2048-token prompts 31.9 against 40.3 at 16 waves:
+  //    32-token units double the longest CU's keys); above, 16-wave ones (four 2048-token prompts 48.6 against
+  //    50.4 at 4 waves; at head_dim 128 76.0 against 87.9), except at head_dim 64 beyond 4 per CU, where 4-wave
+  //    workgroups of two column tiles per wave share each K/V operand read among more tokens (six prompts 67.3
+  //    against 76.9; at head_dim 128 their 206 registers leave two waves per SIMD, never the best).
+  // Format B's one-column waves hold too many registers for 16 waves; it takes the 4-wave layout.
   int layout = p->wg_layout;
   if (layout == SIPA_PREFILL_AUTO) {
     const int64_t g8 = grid_of(units8);
-    if (mode == SIPA_KV_INT8_KCHAN || g8 > 2LL * cus) layout = SIPA_PREFILL_W4X2;
-    else if (g8 > cus && p->max_context >= 2LL * p->max_query_len && (nsplit == 1 || chunk >= 1024))
-      layout = SIPA_PREFILL_W16X1;
-    else layout = SIPA_PREFILL_W8X1;
+    const bool balanced = p->max_context >= 2LL * p->max_query_len;
+    if (mode == SIPA_KV_INT8_KCHAN) layout = SIPA_PREFILL_W4X2;
+    else if (g8 <= cus) layout = SIPA_PREFILL_W8X1;
+    else if (balanced) layout = nsplit == 1 || chunk >= 1024 ? SIPA_PREFILL_W16X1 : SIPA_PREFILL_W8X1;
+    else if (g8 <= 3LL * cus) layout = SIPA_PREFILL_W8X1;
+    else if (D == 64 && g8 > 4LL * cus) layout = SIPA_PREFILL_W4X2;
+    else layout = SIPA_PREFILL_W16X1;
   }
   SIPA_CHECK(mode != SIPA_KV_INT8_KCHAN || layout != SIPA_PREFILL_W16X1, SIPA_EUNSUPPORTED,
              "SIPA_PREFILL_W16X1 does not take format B pools (its 16-wave workgroups cannot hold their registers)");
