@@ -73,10 +73,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // the register use halving the waves per SIMD and the 32-token units coarsening the causal tiles.
 constexpr int kPrefillMaxGroup = 8;
 struct PfShape {
-  int nc, cw;
+  int nc, cw, kh;
 };
 static inline PfShape prefill_shape(int layout) {
-  return layout == SIPA_PREFILL_W8X1 ? PfShape{8, 1} : layout == SIPA_PREFILL_W16X1 ? PfShape{16, 1} : PfShape{8, 2};
+  switch (layout) {
+    case SIPA_PREFILL_W8X1: return PfShape{8, 1, 1};
+    case SIPA_PREFILL_W16X1: return PfShape{16, 1, 1};
+    case SIPA_PREFILL_W16H2: return PfShape{8, 1, 2};
+    default: return PfShape{8, 2, 1};
+  }
 }
 
 // 16-token subtiles per unit for a GQA group of G heads: as many as fit the workgroup's NC column tiles (NC 8:
@@ -151,24 +156,31 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
 
 // NPRE: key tiles in flight per workgroup (register sets of the cooperative load), so a tile's global loads are
 // issued NPRE tiles before its LDS store.
-// NC: column tiles per workgroup; CW: column tiles per wave (the workgroup has NC / CW waves).
-template <int D, int NPRE, int MODE, int KT, int CW, int NC>
-__global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillArgs a) {
+// NC: column tiles per workgroup; CW: column tiles per wave; KH: key halves (KH = 2: the workgroup takes two
+// consecutive key chunks, each with its own NC / CW waves, and combines them before the split epilogue). The
+// workgroup has KH NC / CW waves.
+template <int D, int NPRE, int MODE, int KT, int CW, int NC, int KH>
+__global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const PrefillArgs a) {
   static_assert(KT == 32 || KT == 64, "key tiles of 32 or 64 keys");
   static_assert(CW == 1 || CW == 2, "one or two column tiles per wave");
   static_assert(NC == 8 || NC == 16, "8 or 16 column tiles per workgroup");
-  constexpr int PW = NC / CW, PT = 64 * PW;  // waves and threads of the workgroup
-  constexpr int MT = KT / 16, HT = KT / 32;  // 16-key row tiles, 32-key halves
-  constexpr int kSlots = NC * 16;            // (column, token) rows of a split state
+  static_assert(KH == 1 || (KH == 2 && CW == 1 && NC == 8), "key halves: 8 column tiles of one per wave");
+  constexpr int CWV = NC / CW;                // waves of one key half
+  constexpr int PW = CWV * KH, PT = 64 * PW;  // waves and threads of the workgroup
+  constexpr int PTH = PT / KH;                // threads of one key half (its tiles' cooperative load)
+  constexpr int MT = KT / 16, HT = KT / 32;   // 16-key row tiles, 32-key halves
+  constexpr int kSlots = NC * 16;             // (column, token) rows of a split state
   constexpr int KS = D / 32, DT = D / 16, P = PrefillSmem<D>::kPitch, TE = HT * PrefillSmem<D>::kTile;
   constexpr int CH = MODE == 0 ? 8 : 16;   // channels per cooperative-load chunk: 16 bytes of bf16 or of codes
   constexpr int CPK = D / CH;               // chunks per key row
   constexpr int NCH = KT * CPK;                // chunks per K (or V) tile
-  constexpr int LPT = (NCH + PT - 1) / PT;     // chunks per thread per K (or V) tile
-  static_assert(NCH % PT == 0 || (LPT == 1 && NCH % 64 == 0), "tile chunks must divide over whole waves");
-  // threads past the tile's chunks (NCH < PT: whole waves) take no part in the cooperative load
-  const bool loads = NCH >= PT || (int)threadIdx.x < NCH;
-  __shared__ __align__(16) uint16_t sm[2][2][TE];  // [buffer][K, V][32 keys][P]
+  constexpr int LPT = (NCH + PTH - 1) / PTH;   // chunks per thread per K (or V) tile
+  static_assert(NCH % PTH == 0 || (LPT == 1 && NCH % 64 == 0), "tile chunks must divide over whole waves");
+  // the key half whose tiles this thread loads, and its index there; threads past the tile's chunks (NCH < PTH:
+  // whole waves) take no part in the cooperative load
+  const int hx = KH == 1 ? 0 : (int)threadIdx.x / PTH, tx = (int)threadIdx.x % PTH;
+  const bool loads = NCH >= PTH || tx < NCH;
+  __shared__ __align__(16) uint16_t sm[2][KH][2][TE];  // [buffer][key half][K, V][32 keys][P]
   __shared__ int bids[kMaxSplitBlocks];
   __shared__ int last_flag;
 
@@ -192,28 +204,33 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
   const int ntok = min(min(NT, n - NT * j), a.T - row0);  // rows past T are not touched
   if (ntok <= 0 || row0 < 0) return;
   const int P0 = ctx - n + NT * j;  // position of the unit's first token
-  // keys [0, kv_vis) are visible to some token of the unit; this split takes [k_lo, kv_end)
+  // keys [0, kv_vis) are visible to some token of the unit; this split takes [k_lo, kv_end), KH chunks of
+  // a.chunk keys, key half x the x-th of them (the last half may be shorter or empty)
   const int kv_vis = max(1, min(ctx, P0 + ntok));
-  const int nvalid = (kv_vis + a.chunk - 1) / a.chunk;
-  const int k_lo = sp * a.chunk;
+  const int nvalid = (kv_vis + KH * a.chunk - 1) / (KH * a.chunk);
+  const int k_lo = sp * KH * a.chunk;
   if (k_lo >= kv_vis) return;
-  const int kv_end = min(k_lo + a.chunk, kv_vis);
+  const int kv_end = min(k_lo + KH * a.chunk, kv_vis);
+  auto half_lo = [&](int x) { return min(k_lo + x * a.chunk, kv_end); };
+  auto half_end = [&](int x) { return min(k_lo + (x + 1) * a.chunk, kv_end); };
   const int nblk = min((kv_end - k_lo + 15) >> 4, kMaxSplitBlocks);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wcol = wave % CWV, whalf = wave / CWV;  // the wave's column-tile slot and key half
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
   const int last_col = a.bt_w - 1 - (k_lo >> 4);  // >= nblk - 1 when the host's width check held
   for (int i = threadIdx.x; i < nblk; i += PT) bids[i] = min(max(btr[min(i, last_col)], 0), a.nb - 1);
 
-  // Column tiles c = wave + 4 ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15 with
-  // tt = c / G (G * TT <= 8). A column tile's B operand holds token r of head g (zero past the unit's tokens).
+  // Column tiles c = wcol + (NC / CW) ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15
+  // with tt = c / G (G * TT <= NC). A column tile's B operand holds token r of head g (zero past the unit's
+  // tokens).
   int cg[CW], ctok[CW];
   bool cvalid[CW];  // wave-uniform
   bf16x8 qop[CW][KS];
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) {
-    const int c = wave + PW * ci;
+    const int c = wcol + CWV * ci;
     cg[ci] = c % G;
     ctok[ci] = 16 * (c / G);
     cvalid[ci] = c / G < TT && ctok[ci] < ntok;
@@ -240,7 +257,10 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
   }
   __syncthreads();  // block ids staged
 
-  const int ntiles = (kv_end - k_lo + KT - 1) / KT;
+  // every wave runs the longest half's tile count (half 0's) for the barriers; each computes its own half's
+  const int ntiles = (half_end(0) - k_lo + KT - 1) / KT;
+  const int h_lo = half_lo(whalf), h_end = half_end(whalf);
+  const int my_tiles = (h_end - h_lo + KT - 1) / KT;
   // Cooperative tile load: chunk c = threadIdx.x + 256 i of the KT x D tile is key c / CPK, channels
   // CH (c % CPK) ..; keys past kv_end re-read the split's last key (finite values that the mask zeroes). Plain
   // (temporal) loads: every query tile of the sequence reads the same keys, so L2 keeps serving them.
@@ -250,12 +270,14 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
   const int nq = MODE == 2 ? ctx / 16 * 16 : 0;
   const int tail = MODE == 2 ? min(a.tails[s], a.n_stage - 1) : -1;
   KvRaw<MODE> raw[NPRE][LPT];
+  // keys past the half's end (an empty half: past the split's) re-read its last key
+  const int rel_lo = half_lo(hx) - k_lo, rel_cap = max(half_end(hx), half_lo(hx) + 1) - 1 - k_lo;
   auto gload = [&](int set, int t) {
     if (!loads) return;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int c = threadIdx.x + PT * i, cg = c % CPK;
-      const int rel = min(KT * t + c / CPK, kv_end - 1 - k_lo);  // key offset within the split
+      const int c = tx + PTH * i, cg = c % CPK;
+      const int rel = min(rel_lo + KT * t + c / CPK, min(rel_cap, kv_end - 1 - k_lo));  // key offset in the split
       const int64_t blk = bids[rel >> 4];
       const int off = rel & 15;
       KvRaw<MODE>& x = raw[set][i];
@@ -308,26 +330,26 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
     if (!loads) return;
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int c = threadIdx.x + PT * i;
+      const int c = tx + PTH * i;
       const int e = (c / CPK) * P + CH * (c % CPK);
       const KvRaw<MODE>& x = raw[set][i];
       if constexpr (MODE == 0) {
-        *(u32x4*)(&sm[buf][0][e]) = x.k;
-        *(u32x4*)(&sm[buf][1][e]) = x.v;
+        *(u32x4*)(&sm[buf][hx][0][e]) = x.k;
+        *(u32x4*)(&sm[buf][hx][1][e]) = x.v;
       } else {
         const u32x2 klo = {x.k[0], x.k[1]}, khi = {x.k[2], x.k[3]};
         const u32x2 vlo = {x.v[0], x.v[1]}, vhi = {x.v[2], x.v[3]};
         const float vsf = scale_value(x.vs, a.vs_f32);
-        *(u32x4*)(&sm[buf][1][e]) = dequant8(vlo, [&](int) { return vsf; });
-        *(u32x4*)(&sm[buf][1][e + 8]) = dequant8(vhi, [&](int) { return vsf; });
+        *(u32x4*)(&sm[buf][hx][1][e]) = dequant8(vlo, [&](int) { return vsf; });
+        *(u32x4*)(&sm[buf][hx][1][e + 8]) = dequant8(vhi, [&](int) { return vsf; });
         if constexpr (MODE == 1) {
           const float ksf = scale_value(x.ks, a.ks_f32);
-          *(u32x4*)(&sm[buf][0][e]) = dequant8(klo, [&](int) { return ksf; });
-          *(u32x4*)(&sm[buf][0][e + 8]) = dequant8(khi, [&](int) { return ksf; });
+          *(u32x4*)(&sm[buf][hx][0][e]) = dequant8(klo, [&](int) { return ksf; });
+          *(u32x4*)(&sm[buf][hx][0][e + 8]) = dequant8(khi, [&](int) { return ksf; });
         } else {
-          *(u32x4*)(&sm[buf][0][e]) =
+          *(u32x4*)(&sm[buf][hx][0][e]) =
               x.staged ? x.st[0] : dequant8(klo, [&](int j) { return chan_scale(x.ks, a.ks_f32, j); });
-          *(u32x4*)(&sm[buf][0][e + 8]) =
+          *(u32x4*)(&sm[buf][hx][0][e + 8]) =
               x.staged ? x.st[1] : dequant8(khi, [&](int j) { return chan_scale(x.ks, a.ks_f32, 8 + j); });
         }
       }
@@ -340,10 +362,10 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
 
   auto tile = [&](int t) {
     const int buf = t & 1;
-    const int t0 = k_lo + KT * t;
-    const bool masked = t0 + KT - 1 > P0 || t0 + KT > kv_end;  // some key of the tile is hidden from some token
-    const uint16_t* ks = sm[buf][0];
-    const uint16_t* vs = sm[buf][1];
+    const int t0 = h_lo + KT * t;
+    const bool masked = t0 + KT - 1 > P0 || t0 + KT > h_end;  // some key of the tile is hidden from some token
+    const uint16_t* ks = sm[buf][whalf][0];
+    const uint16_t* vs = sm[buf][whalf][1];
     // The K operands of the tile serve both column tiles of the wave.
     bf16x8 kop[MT][KS];
 #pragma unroll
@@ -377,7 +399,7 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = t0 + 16 * mt + 4 * q4 + i;  // key position of accumulator row (mt, q4, i)
-            if (kp > tok_pos || kp >= kv_end) sc[mt][i] = kNegInf;
+            if (kp > tok_pos || kp >= h_end) sc[mt][i] = kNegInf;
           }
       }
       float mx = kNegInf;
@@ -432,7 +454,7 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
       const int t = tb + k;
       if (t >= ntiles) break;
       gload(k, t + NPRE);
-      tile(t);
+      if (KH == 1 || t < my_tiles) tile(t);  // wave-uniform
       // buffer (t + 1) & 1 was last read in tile t - 1, before the last barrier
       if (t + 1 < ntiles) sstore((k + 1) % NPRE, (t + 1) & 1);
       __syncthreads();
@@ -442,6 +464,34 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
   float lsum[CW];  // token r's denominators (every row of the l_run accumulator holds the same sum)
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) lsum[ci] = l_run[ci][0];
+  if constexpr (KH == 2) {
+    // Key half 1's waves hand their state to half 0's waves of the same column tile through LDS (the tile
+    // buffers, free after the loop's last barrier), which combine the two like two splits: M = max(m0, m1),
+    // x = 2^(m0 - M) x0 + 2^(m1 - M) x1 for l and O. A half that saw no key of a token has (-inf, 0, 0).
+    constexpr int XS = DT * 4 + 2;  // floats per lane: O, m, l
+    static_assert(CWV * 64 * XS * 4 <= (int)sizeof(sm), "half state fits the tile buffers");
+    float* xs = (float*)&sm[0][0][0][0] + (wcol * 64 + lane) * XS;
+    if (whalf == 1 && cvalid[0]) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *(f32x4*)(xs + 4 * dt) = acc[0][dt];
+      xs[4 * DT] = m_run[0];
+      xs[4 * DT + 1] = lsum[0];
+    }
+    __syncthreads();
+    if (whalf == 0 && cvalid[0]) {
+      const float m1 = xs[4 * DT], l1 = xs[4 * DT + 1];
+      const float M = fmaxf(m_run[0], m1);
+      if (M != kNegInf) {
+        const float f0 = fast_exp2(m_run[0] - M), f1 = fast_exp2(m1 - M);  // 0 for a keyless half
+        lsum[0] = f0 * lsum[0] + f1 * l1;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[0][dt] = f0 * acc[0][dt] + f1 * *(const f32x4*)(xs + 4 * dt);
+        m_run[0] = M;
+      }
+    }
+  }
+  // the column tiles' state is half 0's now: half 1's waves only take part in the barriers and the merge
+  const bool owner = KH == 1 || whalf == 0;
   if (nvalid > 1) {
     // This split's state for column c, token r: m, l at slot 16 c + r, and the split's own output O / l (the
     // weighted mean of its V rows, so fp16 holds it to 2^-11 relative) at channels 16 dt + 4 q4 .. of that row:
@@ -452,8 +502,8 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
         (uint16_t*)a.part + (int64_t)u * a.nsplit * kSlots * D, (short)0, a.nsplit * split_bytes, 0x00020000);
 #pragma unroll
     for (int ci = 0; ci < CW; ++ci) {
-      if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
-      const int slot = 16 * (wave + PW * ci) + r;
+      if (!owner || !cvalid[ci] || ctok[ci] + r >= ntok) continue;
+      const int slot = 16 * (wcol + CWV * ci) + r;
       const float inv = lsum[ci] > 0.f ? 1.f / lsum[ci] : 0.f;  // l = 0: the token sees no key of this split
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -569,7 +619,7 @@ __global__ void __launch_bounds__(64 * NC / CW) prefill_mfma_bf16(const PrefillA
   // One split: token r's output for each column tile is acc / l.
 #pragma unroll
   for (int ci = 0; ci < CW; ++ci) {
-    if (!cvalid[ci] || ctok[ci] + r >= ntok) continue;
+    if (!owner || !cvalid[ci] || ctok[ci] + r >= ntok) continue;
     const float inv = 1.f / lsum[ci];
     uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + ctok[ci] + r) * a.o_st + (int64_t)(h * G + cg[ci]) * a.o_sh;
 #pragma unroll
@@ -648,15 +698,15 @@ extern "C" int64_t sipa_prefill_workspace_bytes(int32_t num_seqs, int32_t num_q_
   return most;
 }
 
-template <int D, int NPRE, int KT, int CW, int NC>
+template <int D, int NPRE, int KT, int CW, int NC, int KH>
 static void launch_prefill(int mode, dim3 grid, hipStream_t st, const PrefillArgs& a) {
-  const dim3 block(64 * NC / CW);
+  const dim3 block(64 * NC / CW * KH);
   if (mode == SIPA_KV_PLAIN)
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 0, KT, CW, NC>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 0, KT, CW, NC, KH>), grid, block, 0, st, a);
   else if (mode == SIPA_KV_INT8_TOKEN)
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 1, KT, CW, NC>), grid, block, 0, st, a);
-  else if constexpr (NC == 8)  // format B at 16 columns is refused by the host (register budget)
-    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 2, KT, CW, NC>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 1, KT, CW, NC, KH>), grid, block, 0, st, a);
+  else if constexpr (NC == 8 && KH == 1)  // format B in 16-wave workgroups is refused by the host (registers)
+    hipLaunchKernelGGL((prefill_mfma_bf16<D, NPRE, 2, KT, CW, NC, KH>), grid, block, 0, st, a);
 }
 
 extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
@@ -701,7 +751,7 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
                      p->st_stride_n % 8 == 0 && p->st_stride_b % 8 == 0,
                  SIPA_EINVAL, "format B needs a 16-byte aligned bf16 staging pool and tail slots");
   }
-  SIPA_CHECK(p->wg_layout >= SIPA_PREFILL_AUTO && p->wg_layout <= SIPA_PREFILL_W16X1, SIPA_EINVAL,
+  SIPA_CHECK(p->wg_layout >= SIPA_PREFILL_AUTO && p->wg_layout <= SIPA_PREFILL_W16H2, SIPA_EINVAL,
              "wg_layout %d is not a SIPA_PREFILL_* layout", p->wg_layout);
   // The split count and the layout choice are made over 8-column units; a 16-column layout then runs half as
   // many units with the same splits.
@@ -711,18 +761,27 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   int splits = p->num_splits;
   if (splits <= 0) splits = prefill_splits_host(units8, p->max_context, cus);
   const int chunk = prefill_chunk(p->max_context, splits);
-  const int nsplit = (p->max_context + chunk - 1) / chunk;
-  // split launches: whole groups of 8 units, one XCD each (the kernel's workgroup-to-unit mapping)
-  auto grid_of = [&](int64_t units) { return (nsplit > 1 ? (units + 7) / 8 * 8 : units) * nsplit; };
+  const int nchunk = (p->max_context + chunk - 1) / chunk;  // key chunks per unit
+  // split launches: whole groups of 8 units, one XCD each (the kernel's workgroup-to-unit mapping); a
+  // workgroup of KH key halves takes KH consecutive chunks
+  auto grid_of = [&](int64_t units, int kh) {
+    const int ns = (nchunk + kh - 1) / kh;
+    return (ns > 1 ? (units + 7) / 8 * 8 : units) * ns;
+  };
   // Layout (SIPA_PREFILL_AUTO), from g8, the grid of 8-column workgroups (warm A/B on one MI355X, 0.5B and 1.5B
   // shapes, us per call):
   //  - g8 <= CUs: 8-wave workgroups, one per CU (16-wave ones would leave half the CUs idle).
   //  - a chunk at least its own length into its context (balanced units: the causal triangle varies a unit's keys
-  //    by at most a factor of two) with splits of at least 1024 keys: 16-wave workgroups of 16 column tiles, one
-  //    per CU at a time. Two co-resident 8-column workgroups do not share a CU evenly (the later-dispatched ran
-  //    ~30% longer and finished alone), and 16 column tiles share each K/V tile load: 512 new tokens at 16K
-  //    48.9 -> 46.3 (8-wave), 16 chunks of 512 at 8K 313.8 -> 290.6 (4-wave). Splits of 512 keys keep 8-wave
-  //    workgroups (512 at 4K: 19.5 against 20.7): the one merging workgroup per unit weighs more.
+  //    by at most a factor of two):
+  //    . 8 or more key chunks of at most 1024 keys: 16 waves over 8 column tiles and two consecutive key chunks,
+  //      combined in the workgroup, so that half as many splits store partials and merge (one merging workgroup
+  //      per unit reads 4 partials, not 8): 512 new tokens at 8K 29.0 -> 28.2, 256 at 8K 23.1 -> 20.5, 128 at 8K
+  //      25.5 -> 18.5, at head_dim 128 512 at 8K 46.5 -> 43.8, 256 at 8K 39.2 -> 30.1 (best of the others ->);
+  //    . otherwise, with one chunk or chunks of at least 1024 keys: 16-wave workgroups of 16 column tiles, one per
+  //      CU at a time. Two co-resident 8-column workgroups do not share a CU evenly (the later-dispatched ran ~30%
+  //      longer and finished alone), and 16 column tiles share each K/V tile load: 512 new tokens at 16K
+  //      48.9 -> 46.3 (8-wave), 16 chunks of 512 at 8K 313.8 -> 290.6 (4-wave), 1024 at 8K 47.2 -> 44.0;
+  //    . else 8-wave workgroups.
   //  - fresh prompts: 8-wave workgroups up to 3 per CU (two 2048-token prompts 31.9 against 40.3 at 16 waves:
   //    32-token units double the longest CU's keys); above, 16-wave ones (four 2048-token prompts 48.6 against
   //    50.4 at 4 waves; at head_dim 128 76.0 against 87.9), except at head_dim 64 beyond 4 per CU, where 4-wave
@@ -731,22 +790,27 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   // Format B's one-column waves hold too many registers for 16 waves; it takes the 4-wave layout.
   int layout = p->wg_layout;
   if (layout == SIPA_PREFILL_AUTO) {
-    const int64_t g8 = grid_of(units8);
+    const int64_t g8 = grid_of(units8, 1);
     const bool balanced = p->max_context >= 2LL * p->max_query_len;
     if (mode == SIPA_KV_INT8_KCHAN) layout = SIPA_PREFILL_W4X2;
     else if (g8 <= cus) layout = SIPA_PREFILL_W8X1;
-    else if (balanced) layout = nsplit == 1 || chunk >= 1024 ? SIPA_PREFILL_W16X1 : SIPA_PREFILL_W8X1;
+    else if (balanced)
+      layout = nchunk >= 8 && chunk <= 1024            ? SIPA_PREFILL_W16H2
+               : nchunk == 1 || chunk >= 1024 ? SIPA_PREFILL_W16X1
+                                                        : SIPA_PREFILL_W8X1;
     else if (g8 <= 3LL * cus) layout = SIPA_PREFILL_W8X1;
     else if (D == 64 && g8 > 4LL * cus) layout = SIPA_PREFILL_W4X2;
     else layout = SIPA_PREFILL_W16X1;
   }
-  SIPA_CHECK(mode != SIPA_KV_INT8_KCHAN || layout != SIPA_PREFILL_W16X1, SIPA_EUNSUPPORTED,
-             "SIPA_PREFILL_W16X1 does not take format B pools (its 16-wave workgroups cannot hold their registers)");
+  SIPA_CHECK(mode != SIPA_KV_INT8_KCHAN || layout == SIPA_PREFILL_W4X2 || layout == SIPA_PREFILL_W8X1,
+             SIPA_EUNSUPPORTED, "format B pools take SIPA_PREFILL_W4X2 or _W8X1 (16-wave workgroups cannot hold "
+             "their registers)");
   const PfShape shape = prefill_shape(layout);
   const int tt = prefill_subtiles(G, shape.nc);
   const int qtiles = (p->max_query_len + 16 * tt - 1) / (16 * tt);
   const int64_t units = (int64_t)S * Hkv * qtiles;
-  const int64_t wgs = grid_of(units);
+  const int nsplit = (nchunk + shape.kh - 1) / shape.kh;  // workgroups per unit
+  const int64_t wgs = grid_of(units, shape.kh);
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   PrefillLayout lay{};
   if (nsplit > 1) {
@@ -819,13 +883,15 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   // 2048-token prompts 94 -> 84 us), 32 at head_dim 128, whose registers would otherwise halve the waves per SIMD
   // (166 -> 221 us). Tiles in flight (NPRE) within the register budget.
   if (D == 64) {
-    if (shape.nc == 16) launch_prefill<64, 2, 64, 1, 16>(mode, grid, st, a);
-    else if (shape.cw == 1) launch_prefill<64, 2, 64, 1, 8>(mode, grid, st, a);
-    else launch_prefill<64, 2, 64, 2, 8>(mode, grid, st, a);
+    if (shape.kh == 2) launch_prefill<64, 2, 64, 1, 8, 2>(mode, grid, st, a);
+    else if (shape.nc == 16) launch_prefill<64, 2, 64, 1, 16, 1>(mode, grid, st, a);
+    else if (shape.cw == 1) launch_prefill<64, 2, 64, 1, 8, 1>(mode, grid, st, a);
+    else launch_prefill<64, 2, 64, 2, 8, 1>(mode, grid, st, a);
   } else {
-    if (shape.nc == 16) launch_prefill<128, 2, 32, 1, 16>(mode, grid, st, a);
-    else if (shape.cw == 1) launch_prefill<128, 2, 32, 1, 8>(mode, grid, st, a);
-    else launch_prefill<128, 2, 32, 2, 8>(mode, grid, st, a);
+    if (shape.kh == 2) launch_prefill<128, 2, 32, 1, 8, 2>(mode, grid, st, a);
+    else if (shape.nc == 16) launch_prefill<128, 2, 32, 1, 16, 1>(mode, grid, st, a);
+    else if (shape.cw == 1) launch_prefill<128, 2, 32, 1, 8, 1>(mode, grid, st, a);
+    else launch_prefill<128, 2, 32, 2, 8, 1>(mode, grid, st, a);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "prefill launch failed: %s", hipGetErrorString(e));

@@ -13,7 +13,7 @@ from . import _hip
 from .hip_decode import reserve_workspace  # one split workspace per (device, stream) serves decode and prefill
 
 # wg_layout names, indexed by their SIPA_PREFILL_* values
-WG_LAYOUTS = ("auto", "w4x2", "w8x1", "w16x1")
+WG_LAYOUTS = ("auto", "w4x2", "w8x1", "w16x1", "w16h2")
 
 
 def prefill_supported(q_dtype: torch.dtype, pool_dtype: torch.dtype, block_size: int, head_dim: int, group: int,
@@ -61,7 +61,8 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     merge_path: "auto" merges a query tile's key splits from the L2 of the XCD they ran on when they shared one
     (the kernel places them so), through memory otherwise; "memory" always through memory. Same bits either way.
     wg_layout: the workgroup layout, waves x column tiles (a query head and 16 tokens) per wave: "w4x2", "w8x1",
-    "w16x1" (format B pools take the first two), or "auto", the library's choice by grid size and context
+    "w16x1", "w16h2" (16 waves over 8 column tiles and two consecutive key splits, combined in the workgroup;
+    format B pools take the first two), or "auto", the library's choice by grid size and context
     (sipa_prefill_params.wg_layout). "w4x2" and "w8x1" give the same bits, "w16x1" too with one split.
     """
     S = block_tables.shape[0]

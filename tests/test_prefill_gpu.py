@@ -153,9 +153,13 @@ def test_chunk_at_8k_splits_against_torch(shape):
     run = lambda n: paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=n)  # noqa: E731
     a, b, a2 = run(8), run(3), run(8)
     mem = paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=8, merge_path="memory")
+    # 16 waves over key halves: each workgroup combines two of the 8 key chunks, then 4 splits merge
+    hx = [paged_prefill_attention(q, k, v, bt, c, st, ln, scale, 8192, 512, num_splits=8, wg_layout="w16h2",
+                                  merge_path=path) for path in ("auto", "memory")]
     torch.cuda.synchronize()
     assert torch.equal(a, a2)
     assert torch.equal(a, mem)  # the L2 merge and the merge through memory give the same bits
+    assert torch.equal(hx[0], hx[1])
     G = Hq // Hkv
     idx = torch.tensor(tables[0], device="cuda", dtype=torch.int64)
     kk = k.index_select(1, idx).reshape(Hkv, -1, D)[:, :8192].float().repeat_interleave(G, 0)
@@ -165,7 +169,7 @@ def test_chunk_at_8k_splits_against_torch(shape):
     pos = torch.arange(8192 - 512, 8192, device="cuda")[:, None]
     sc = sc.masked_fill(torch.arange(8192, device="cuda")[None, :] > pos, float("-inf"))
     want = torch.matmul(torch.softmax(sc, -1), vv).permute(1, 0, 2).double().cpu().numpy()
-    for got in (a, b):
+    for got in (a, b, hx[0]):
         assert_bf16_close(got.double().cpu().numpy(), want, "chunk at 8k")
 
 
@@ -367,7 +371,9 @@ def test_wave_layouts_agree(shape, pool, splits):
     bits too (a unit's earlier tokens also run its later tokens' key tiles, fully masked for them, which must
     leave their bits alone); with several, a token whose 16-token unit saw one split may sit in a 32-token unit
     that sees two, and its row then goes through the merge's fp16 partials. There the bar is the oracle's, and
-    the layouts stay within a bf16 rounding and the fp16 partial's of each other."""
+    the layouts stay within a bf16 rounding and the fp16 partial's of each other. 16 waves over two key halves
+    combine each pair of key chunks in the workgroup first (its own arithmetic): held to that bar at every split
+    count."""
     Hq, Hkv, D = SHAPES[shape]
     ctx, qlen = [300, 1000, 33, 517], [64, 7, 33, 200]
     print(f"case wave layouts shape={shape} pool={pool} splits={splits}", flush=True)
@@ -379,7 +385,7 @@ def test_wave_layouts_agree(shape, pool, splits):
     run = lambda lay: paged_prefill_attention(q, k, v, bt, c, st, ln, D ** -0.5, max(ctx), max(qlen),  # noqa: E731
                                               num_splits=splits, quant=quant, wg_layout=lay)
     want = run("w4x2")
-    layouts = ["w8x1", "auto"] + (["w16x1"] if pool != "int8-kchannel" else [])
+    layouts = ["w8x1", "auto"] + (["w16x1", "w16h2"] if pool != "int8-kchannel" else [])
     got = {lay: run(lay) for lay in layouts}
     torch.cuda.synchronize()
     assert torch.equal(got["w8x1"], want)
@@ -387,8 +393,8 @@ def test_wave_layouts_agree(shape, pool, splits):
         assert torch.equal(got["auto"], want)
     else:
         rows = torch.cat([torch.arange(s, s + n) for s, n in zip(starts, qlen)]).cuda()
-        for lay in ("w16x1", "auto"):  # auto picks w8x1 or w16x1 for these small grids
-            if splits == 1:
+        for lay in ("w16x1", "w16h2", "auto"):  # auto picks w8x1 or w16x1 for these small grids
+            if splits == 1 and lay != "w16h2":
                 assert torch.equal(got[lay], want), lay
             else:
                 a, b = got[lay][rows].float(), want[rows].float()
@@ -399,9 +405,11 @@ def test_wave_layouts_agree(shape, pool, splits):
             args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
             ref32 = paged_ref.prefill(*args, dtype=np.float32)
             npr = rows.cpu().numpy()
-            assert_bf16_close(got["w16x1"].double().cpu().numpy()[npr], ref32[npr], "w16x1")
+            for lay in ("w16x1", "w16h2"):
+                assert_bf16_close(got[lay].double().cpu().numpy()[npr], ref32[npr], lay)
     with pytest.raises(ValueError):
         run("w2x4")
     if pool == "int8-kchannel":
-        with pytest.raises(ValueError, match="format B"):
-            run("w16x1")
+        for lay in ("w16x1", "w16h2"):
+            with pytest.raises(ValueError, match="format B"):
+                run(lay)
