@@ -227,10 +227,10 @@ typedef struct sipa_prefill_params {
   int32_t merge_path;
   /* Workgroup layout (ABI 6), a SIPA_PREFILL_* value. A column tile is a query head and 16 of a unit's tokens.
      SIPA_PREFILL_AUTO lets the library choose from g8, the grid of 8-column workgroups: SIPA_PREFILL_W8X1 for
-     g8 <= CUs; for a chunk at least its own length into its context, SIPA_PREFILL_W16H2 with 8 or more key
-     splits of at most 1024 keys, else SIPA_PREFILL_W16X1 with one split or splits of at least 1024 keys, else
-     W8X1; for fresh prompts W8X1 up to 3 workgroups per CU, then W16X1, except SIPA_PREFILL_W4X2 beyond 4 per
-     CU at head_dim 64. Format B pools (SIPA_KV_INT8_KCHAN) take W4X2 (W4X2 or W8X1 when forced). W4X2 and
+     g8 <= CUs; for a chunk at least its own length into its context, SIPA_PREFILL_W16H2 over bf16 pools with 8
+     or more key splits of at most 1024 keys, else SIPA_PREFILL_W16X1 with one split or splits of at least 1024
+     keys, else W8X1; for fresh prompts W8X1 up to 3 workgroups per CU, then W16X1, except SIPA_PREFILL_W4X2
+     beyond 4 per CU at head_dim 64. Format B pools (SIPA_KV_INT8_KCHAN) take W4X2 (W4X2 or W8X1 when forced). W4X2 and
      W8X1 give the same bits; W16X1 too with one split (with several, a row may go through the split merge's
      fp16 partials in one layout and not in the other); W16H2 combines key splits in its own order. Every
      layout meets the same error bound. With W16H2, num_splits counts key chunks, two to a workgroup. */

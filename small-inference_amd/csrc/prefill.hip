@@ -773,7 +773,9 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   //  - g8 <= CUs: 8-wave workgroups, one per CU (16-wave ones would leave half the CUs idle).
   //  - a chunk at least its own length into its context (balanced units: the causal triangle varies a unit's keys
   //    by at most a factor of two):
-  //    . 8 or more key chunks of at most 1024 keys: 16 waves over 8 column tiles and two consecutive key chunks,
+  //    . bf16 pools, 8 or more key chunks of at most 1024 keys: 16 waves over 8 column tiles and two consecutive
+  //      key chunks (INT8 pools: each half dequantizes its own tiles, twice the store work per CU; 512 at 8K
+  //      32.4 -> 34.8, so they keep W16X1),
   //      combined in the workgroup, so that half as many splits store partials and merge (one merging workgroup
   //      per unit reads 4 partials, not 8): 512 new tokens at 8K 29.0 -> 28.2, 256 at 8K 23.1 -> 20.5, 128 at 8K
   //      25.5 -> 18.5, at head_dim 128 512 at 8K 46.5 -> 43.8, 256 at 8K 39.2 -> 30.1 (best of the others ->);
@@ -795,9 +797,9 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
     if (mode == SIPA_KV_INT8_KCHAN) layout = SIPA_PREFILL_W4X2;
     else if (g8 <= cus) layout = SIPA_PREFILL_W8X1;
     else if (balanced)
-      layout = nchunk >= 8 && chunk <= 1024            ? SIPA_PREFILL_W16H2
-               : nchunk == 1 || chunk >= 1024 ? SIPA_PREFILL_W16X1
-                                                        : SIPA_PREFILL_W8X1;
+      layout = mode == SIPA_KV_PLAIN && nchunk >= 8 && chunk <= 1024 ? SIPA_PREFILL_W16H2
+               : nchunk == 1 || chunk >= 1024                      ? SIPA_PREFILL_W16X1
+                                                                   : SIPA_PREFILL_W8X1;
     else if (g8 <= 3LL * cus) layout = SIPA_PREFILL_W8X1;
     else if (D == 64 && g8 > 4LL * cus) layout = SIPA_PREFILL_W4X2;
     else layout = SIPA_PREFILL_W16X1;
