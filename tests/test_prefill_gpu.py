@@ -338,20 +338,21 @@ def test_merge_paths_agree(shape, splits):
 
 
 @pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
-def test_l2_merge_reads_this_calls_partials(shape):
+@pytest.mark.parametrize("layout", ["auto", "w16h2"])
+def test_l2_merge_reads_this_calls_partials(shape, layout):
     """The prefill merge from the XCD's L2: calls alternating between two inputs of one shape (the same workspace
     addresses) each give the memory-path bits of their own inputs, so no partial of an earlier call is read
-    back."""
+    back (16 waves over key halves too: 6 key chunks, 3 workgroups a unit)."""
     Hq, Hkv, D = SHAPES[shape]
     ctx, qlen = [3000, 700], [700, 300]
     cases = [make_prefill(ctx, qlen, Hq, Hkv, D, seed=s) for s in (51, 52)]
     scale = D ** -0.5
-    print(f"case prefill l2 merge alternation {shape}", flush=True)
+    print(f"case prefill l2 merge alternation {shape} {layout}", flush=True)
 
     def run(i, path):
         q, k, v, bt, c, st, ln = cases[i][:7]
         return paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), num_splits=6,
-                                       merge_path=path)
+                                       merge_path=path, wg_layout=layout)
 
     want = [run(i, "memory").clone() for i in (0, 1)]
     for rep in range(3):
@@ -359,6 +360,32 @@ def test_l2_merge_reads_this_calls_partials(shape):
             got = run(i, "auto")
             torch.cuda.synchronize()
             assert torch.equal(got, want[i]), f"rep {rep} input {i}"
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g1", "g3"])
+@pytest.mark.parametrize("splits", [2, 3, 5, 7, 8, 32])
+def test_key_halves_against_oracle(shape, splits):
+    """16 waves over two key splits each (W16H2) at every split parity: an odd count leaves the last workgroup's
+    second half without keys, and contexts that are not multiples of the split length leave it short; a chunk
+    shorter than its context's prefix (mid-context rows) and one at its start (fresh rows) in one call. Held to the
+    oracle bound, and the L2 and memory merges give the same bits."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [3001, 700, 129, 64], [500, 300, 17, 64]
+    print(f"case key halves shape={shape} splits={splits}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=81)
+    scale = D ** -0.5
+    run = lambda path: paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen),  # noqa: E731
+                                               num_splits=splits, merge_path=path, wg_layout="w16h2")
+    got, mem = run("auto"), run("memory")
+    torch.cuda.synchronize()
+    assert torch.equal(got, mem)
+    args = (as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale)
+    ref32 = paged_ref.prefill(*args, dtype=np.float32)
+    ref64 = paged_ref.prefill(*args, dtype=np.float64)
+    rows = np.concatenate([np.arange(s0, s0 + n) for s0, n in zip(starts, qlen)])
+    out = got.double().cpu().numpy()[rows]
+    assert_bf16_close(out, ref32[rows], "key halves")
+    np.testing.assert_allclose(out, ref64[rows], rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("shape", ["0.5B", "1.5B", "g4", "g1", "g3"])
