@@ -47,6 +47,9 @@
 
 namespace sipa {
 
+// Bytes of the bf16 kernel's leading scalar arguments (three pointers and six int32), before its DecodeArgs.
+constexpr int kHotArgBytes = 3 * 8 + 6 * 4;
+
 template <int D, int NB>  // NB: tiles in flight per wave (the register prefetch ring)
 __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __restrict__ hbt,
                                                              const int32_t* __restrict__ hctx,
@@ -70,27 +73,57 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __re
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
+  // Prologue: the split's block ids, the context length, the query and the kernel arguments the first tiles need
+  // are all requested before anything waits, so the first K/V loads follow one memory round trip.
   int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(hp.bt, hp.bt_ss, hp.bt_w, s, start, w.end, ids);
+  fetch_split_ids_flat(hp.bt, hp.bt_ss, hp.bt_w, s, start, w.end, ids);
+  const uint16_t* const kbase = (const uint16_t*)a.k;
+  const uint16_t* const vbase = (const uint16_t*)a.v;
+  const int64_t kv_sh = a.kv_sh, kv_sn = a.kv_sn;
+  const int nblocks = a.nb;
+  int ctx_raw;
+  {
+    // Every 64-byte line of the kernel arguments goes into the scalar cache in this same wait: the arguments the
+    // epilogue reads are otherwise fetched after the barrier, and the first tile's LDS read of its block id (counted
+    // with scalar loads) would wait for them.
+    static_assert(kHotArgBytes + sizeof(DecodeArgs) <= 6 * 64 && kHotArgBytes + sizeof(DecodeArgs) >= 0x144,
+                  "the six line loads stay inside the explicit kernel arguments");
+    // The context length is loaded in the same block: the compiler waits for every outstanding scalar load before
+    // an inline asm statement, so a load of its own would be one more round trip.
+    const auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+    const int32_t* ctx_p = hp.ctx + s;
+    uint32_t l0, l1, l2, l3, l4, l5;
+    asm volatile(
+        "s_load_dword %0, %8, 0x0\n"
+        "s_load_dword %1, %7, 0x0\n"
+        "s_load_dword %2, %7, 0x40\n"
+        "s_load_dword %3, %7, 0x80\n"
+        "s_load_dword %4, %7, 0xc0\n"
+        "s_load_dword %5, %7, 0x100\n"
+        "s_load_dword %6, %7, 0x140\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(ctx_raw), "=&s"(l0), "=&s"(l1), "=&s"(l2), "=&s"(l3), "=&s"(l4), "=&s"(l5)
+        : "s"(ka), "s"(ctx_p), "s"(kbase), "s"(vbase), "s"(kv_sh), "s"(kv_sn), "s"(nblocks)
+        : "memory");
+  }
+  const int ctx = min(ctx_raw, hp.max_ctx);  // as context_len()
+  // The query group as the QK B operand. Lanes of padding heads (r >= G) load head G - 1 again: their score
+  // columns run the same softmax as that head's and are never stored.
   bf16x8 qop[KS];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
 #pragma unroll
-    for (int j = 0; j < KS; ++j) {
-      u32x4 u = *(const u32x4*)(qrow + 32 * j + 8 * q4);
-      if (r >= G) u = u32x4{0, 0, 0, 0};
-      qop[j] = __builtin_bit_cast(bf16x8, u);
-    }
+    for (int j = 0; j < KS; ++j) qop[j] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qrow + 32 * j + 8 * q4));
   }
-  const int ctx = min(hp.ctx[s], hp.max_ctx);  // as context_len()
-  if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
+  const bool past_end = w.nvalid < 0 && start >= ctx;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
   const int nvalid = w.nvalid < 0 ? (ctx + hp.chunk - 1) / hp.chunk : w.nvalid;
-  commit_split_ids(nb_spec, ids, bids, a.nb);
+  commit_split_ids_flat(ids, bids, nblocks);
   __syncthreads();  // block ids staged
+  if (past_end) return;
 
-  const uint16_t* kh = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;
-  const uint16_t* vh = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
+  const uint16_t* kh = kbase + (int64_t)h * kv_sh;
+  const uint16_t* vh = vbase + (int64_t)h * kv_sh;
   uint16_t* vw = (uint16_t*)smem + wave * 32 * VP;
   const int tr_off = tr16_offset(r, q4, VP);
   const int ntile = (end - start + 31) >> 5;
@@ -108,8 +141,8 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __re
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int blk = mt ? b1 : b0;
-      const uint16_t* kb = kh + (int64_t)blk * a.kv_sn;
-      const uint16_t* vb = vh + (int64_t)blk * a.kv_sn;
+      const uint16_t* kb = kh + (int64_t)blk * kv_sn;
+      const uint16_t* vb = vh + (int64_t)blk * kv_sn;
 #pragma unroll
       for (int j = 0; j < KS; ++j) tl.k[mt][j] = stream_load(kb + r * D + 32 * j + 8 * q4);
 #pragma unroll

@@ -151,10 +151,24 @@ __device__ __forceinline__ float load_coherent(float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Four consecutive outputs. A bf16 row piece on a 4-byte boundary goes out as two packed words written through
+// to memory (relaxed agent-scope stores, sc1), so the launch ends with no dirty output lines in L2 to release
+// (C2: 26.17 -> 26.03 us against four 2-byte write-back stores).
 template <bool OUT_F32>
 __device__ __forceinline__ void store_out4(const DecodeArgs& a, int s, int hq, int d0, f32x4 v) {
+  const int64_t i = (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh + d0;
+  if (!OUT_F32) {
+    uint16_t* o = (uint16_t*)a.out + i;
+    if (((uintptr_t)o & 3) == 0) {
+      const uint32_t w0 = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+      const uint32_t w1 = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+      __hip_atomic_store((uint32_t*)o, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store((uint32_t*)o + 1, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) store_out<OUT_F32>(a, s, hq, d0 + i, v[i]);
+  for (int k = 0; k < 4; ++k) store_out<OUT_F32>(a, s, hq, d0 + k, v[k]);
 }
 
 // The partial rows of one (s, h): [G][splits][D] floats from part + ((s Hq + h G) splits) D, as a raw buffer
@@ -380,6 +394,29 @@ __device__ __forceinline__ int fetch_split_ids(const int32_t* bt, int64_t bt_ss,
     ids[i] = (j < nb_spec) ? btr[j] : 0;
   }
   return nb_spec;
+}
+
+// The same without a branch per load: every thread issues all N loads (entries past the split read its last id
+// again, an empty split reads column 0 of its row), so no use of one id can be placed between the loads and the
+// next memory operations: the ids, the context length and the kernel arguments are then in flight together and
+// the first K/V loads wait for one round trip. N x kThreads ids: the longest split the kernel stages.
+template <int N>
+__device__ __forceinline__ int fetch_split_ids_flat(const int32_t* bt, int64_t bt_ss, int bt_w, int s, int start,
+                                                    int end_spec, int (&ids)[N]) {
+  const int nb_spec = min((end_spec - start + 15) >> 4, bt_w - (start >> 4));  // never past the row's width
+  const int last = max(nb_spec - 1, 0);
+  const int32_t* btr = bt + (int64_t)s * bt_ss + (nb_spec > 0 ? (start >> 4) : 0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) ids[i] = btr[min((int)threadIdx.x + kThreads * i, last)];
+  return nb_spec;
+}
+
+// Stages every thread's ids (N x kThreads entries of bids, those past the split unused), clamped into the pool,
+// without a branch.
+template <int N>
+__device__ __forceinline__ void commit_split_ids_flat(const int (&ids)[N], int* bids, int nblocks) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) bids[threadIdx.x + kThreads * i] = min(max(ids[i], 0), nblocks - 1);
 }
 
 // Ids outside the pool are clamped into it: a bad table gives wrong results, never an access out of bounds.

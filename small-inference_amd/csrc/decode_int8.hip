@@ -70,9 +70,28 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
   __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
-  __shared__ int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
+  __shared__ __align__(8) int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
   __shared__ int last_flag;
 
+  {
+    // Each 64-byte line of the kernel arguments, requested at entry in one wait: the argument loads the compiler
+    // places later (work item, block table, epilogue) then hit the scalar cache instead of each costing a round trip
+    // (and the first tile's LDS reads, counted with scalar loads, do not wait behind them).
+    static_assert(sizeof(DecodeArgs) <= 5 * 64 && sizeof(DecodeArgs) >= 0x104,
+                  "the five line loads stay inside the kernel arguments");
+    const auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t l0, l1, l2, l3, l4;
+    asm volatile(
+        "s_load_dword %0, %5, 0x0\n"
+        "s_load_dword %1, %5, 0x40\n"
+        "s_load_dword %2, %5, 0x80\n"
+        "s_load_dword %3, %5, 0xc0\n"
+        "s_load_dword %4, %5, 0x100\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(l0), "=&s"(l1), "=&s"(l2), "=&s"(l3), "=&s"(l4)
+        : "s"(ka)
+        : "memory");
+  }
   const WorkItem w = work_item(a);
   const int sp = w.sp, h = w.h, s = w.s;
   const int start = w.start;
@@ -84,8 +103,12 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   auto kchan = [&](int jj) { return 64 * (jj >> 1) + 16 * q4 + 8 * (jj & 1); };
 
   const int wend = min(w.end, start + kMaxInt8Split);  // the host never makes longer splits; LDS holds no more
-  int ids[kIdsPerThread];
-  const int nb_spec = fetch_split_ids(a, s, start, wend, ids);
+  // Prologue: the split's block ids, the query, the context length and staging slot, and every line of the kernel
+  // arguments are requested before anything waits; the query's conversion runs after the first tiles' loads are
+  // issued. The first K/V loads then follow one memory round trip.
+  static_assert(kMaxInt8Split / 16 == kThreads, "one block id per thread");
+  int ids[1];
+  fetch_split_ids_flat(a.bt, a.bt_ss, a.bt_w, s, start, wend, ids);
   // The query group in bf16, channel order of the int8 K layout: k-step j of lane (r, q4) (zero for r >= G).
   const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)s * a.q_ss + (int64_t)(h * G + min(r, G - 1)) * a.q_sh;
   auto load_qb = [&](int j) {
@@ -93,57 +116,93 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     if (r >= G) u = u32x4{0, 0, 0, 0};
     return __builtin_bit_cast(bf16x8, u);
   };
-  bf16x8 qb[KS];
+  u32x4 qraw[KS];
 #pragma unroll
-  for (int j = 0; j < KS; ++j) qb[j] = load_qb(j);
+  for (int j = 0; j < KS; ++j) qraw[j] = *(const u32x4*)(qrow + kchan(j));
+  int ctx_raw, tail_raw;
+  {
+    // The context length and staging slot in one wait (the compiler waits for every outstanding scalar load before
+    // an inline asm statement, so separate loads would each cost a round trip).
+    const int32_t* ctx_p = a.ctx + s;
+    const int32_t* tail_p = MODE >= 2 ? a.tail + s : ctx_p;
+    asm volatile(
+        "s_load_dword %0, %2, 0x0\n"
+        "s_load_dword %1, %3, 0x0\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(ctx_raw), "=&s"(tail_raw)
+        : "s"(ctx_p), "s"(tail_p)
+        : "memory");
+  }
+  const int ctx = min(ctx_raw, a.max_ctx);  // as context_len()
+  const bool past_end = w.nvalid < 0 && start >= ctx;  // grid: a split past this sequence's end
+  const int end = max(start, min(wend, ctx));
+  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
+  const int n_quant = (ctx >> 4) << 4;  // mode 2: tokens in full (quantized) blocks
+  // staging slot of the partial last block, -1 if none (as tail_slot())
+  const int tail = (MODE >= 2) ? min(tail_raw, a.n_stage - 1) : -1;
+  // The split's token scales: thread t loads block t's two 16-byte half rows (per array) with the block id it
+  // fetched itself, so the loads need no LDS read; they are issued before the first tiles' loads, so that waiting
+  // for them does not wait for the tiles. Threads past the split read its last block again (not staged).
+  const uint16_t* ksh = (const uint16_t*)a.ks + (int64_t)h * a.ks_sh;
+  const uint16_t* vsh = (const uint16_t*)a.vs + (int64_t)h * a.vs_sh;
+  const int64_t own_bid = min(max(ids[0], 0), a.nb - 1);
+  u32x4 sreg[kScaleArrays][2];
+#pragma unroll
+  for (int arr = 0; arr < kScaleArrays; ++arr) {
+    const uint16_t* base = arr ? ksh : vsh;
+    const int64_t sn = arr ? a.ks_sn : a.vs_sn;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) sreg[arr][hf] = *(const u32x4*)(base + own_bid * sn + 8 * hf);
+  }
+  commit_split_ids_flat(ids, bids, a.nb);
+  __syncthreads();
+  if (past_end) return;
+
   constexpr bool kconst = MODE == 3;  // one channel scale per (head, channel) for every block
   // qh: the query in fp16 (modes 1, 2), or the high part of Q' = q * s (mode 3) with ql its low part,
   // fp16(Q' - qh), so that qh + ql carries Q' to about 2^-22. A head whose largest |q| (|Q'| in mode 3) lies
   // outside [2^-6, 2^8) is first scaled by 2^-shift to bring it into [2^6, 2^7): fp16 then holds it without
   // overflow (|q| > 65504) or subnormal loss, and mode 2's q * s products keep headroom. The factor is exact and
   // the softmax scale of that head (lane column r) takes its inverse, so the scores equal unscaled ones bit for
-  // bit wherever those are representable.
-  float qf[KS][8];
-  float qmax = 0.f;
-#pragma unroll
-  for (int j = 0; j < KS; ++j) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qf[j][i] = (float)qb[j][i];
-      if (kconst) {
-        const int64_t ci = (int64_t)h * a.ks_sh + kchan(j) + i;
-        qf[j][i] *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
-      }
-      qmax = fmaxf(qmax, fabsf(qf[j][i]));
-    }
-  }
-  qmax = max_over_rows(qmax);  // head r over the four lane groups
-  const int qexp = qmax > 0.f ? (int)((__float_as_uint(qmax) >> 23) & 0xff) - 127 : 0;  // floor(log2) of a normal
-  const int qshift = (qexp >= 8 || qexp < -6) ? qexp - 6 : 0;
-  const float sl2 = ldexpf(a.scale_log2, qshift);  // this lane's head: the softmax scale times 2^shift
+  // bit wherever those are representable. Computed by convert_query() once the first tiles' loads are out.
   f16x8 qh[KS], ql[KS];
+  int qshift = 0;
+  float sl2 = a.scale_log2;
+  auto convert_query = [&]() {
+    float qf[KS][8];
+    float qmax = 0.f;
 #pragma unroll
-  for (int j = 0; j < KS; ++j) {
+    for (int j = 0; j < KS; ++j) {
+      u32x4 u = qraw[j];
+      if (r >= G) u = u32x4{0, 0, 0, 0};
+      const bf16x8 qb = __builtin_bit_cast(bf16x8, u);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float x = ldexpf(qf[j][i], -qshift);
-      qh[j][i] = (_Float16)x;
-      ql[j][i] = (_Float16)(x - (float)qh[j][i]);
+      for (int i = 0; i < 8; ++i) {
+        qf[j][i] = (float)qb[i];
+        if (kconst) {
+          const int64_t ci = (int64_t)h * a.ks_sh + kchan(j) + i;
+          qf[j][i] *= a.ks_f32 ? ((const float*)a.ks)[ci] : f16_bits_to_f32(((const uint16_t*)a.ks)[ci]);
+        }
+        qmax = fmaxf(qmax, fabsf(qf[j][i]));
+      }
     }
-  }
-  const int ctx = context_len(a, s);
-  if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
-  const int end = max(start, min(wend, ctx));
-  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
-  const int n_quant = (ctx >> 4) << 4;                // mode 2: tokens in full (quantized) blocks
-  const int tail = (MODE >= 2) ? tail_slot(a, s) : -1;  // staging slot of the partial last block, -1 if none
-  commit_split_ids(nb_spec, ids, bids, a.nb);
-  __syncthreads();
+    qmax = max_over_rows(qmax);  // head r over the four lane groups
+    const int qexp = qmax > 0.f ? (int)((__float_as_uint(qmax) >> 23) & 0xff) - 127 : 0;  // floor(log2) of a normal
+    qshift = (qexp >= 8 || qexp < -6) ? qexp - 6 : 0;
+    sl2 = ldexpf(a.scale_log2, qshift);  // this lane's head: the softmax scale times 2^shift
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float x = ldexpf(qf[j][i], -qshift);
+        qh[j][i] = (_Float16)x;
+        ql[j][i] = (_Float16)(x - (float)qh[j][i]);
+      }
+    }
+  };
 
   const int8_t* kh = (const int8_t*)a.k + (int64_t)h * a.kv_sh;
   const int8_t* vh = (const int8_t*)a.v + (int64_t)h * a.kv_sh;
-  const uint16_t* ksh = (const uint16_t*)a.ks + (int64_t)h * a.ks_sh;
-  const uint16_t* vsh = (const uint16_t*)a.vs + (int64_t)h * a.vs_sh;
   _Float16* vw = (_Float16*)smem + wave * 32 * VP;
   const int tr_off = tr16_offset(r, q4, VP);
   const int ntile = (end - start + 31) >> 5;
@@ -294,34 +353,18 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     wave_sync();
   };
 
-  // The split's token scales: one 16-byte load per half block row and array, issued before the first tiles'
-  // loads so that waiting for them does not wait for the tiles.
-  constexpr int kScaleLoads = (2 * kScaleBlocks + kThreads - 1) / kThreads;
-  u32x4 sreg[kScaleArrays][kScaleLoads];
-#pragma unroll
-  for (int arr = 0; arr < kScaleArrays; ++arr) {
-    const uint16_t* base = arr ? ksh : vsh;
-    const int64_t sn = arr ? a.ks_sn : a.vs_sn;
-#pragma unroll
-    for (int i = 0; i < kScaleLoads; ++i) {
-      const int c = threadIdx.x + kThreads * i;  // half block row c % 2 of block c / 2
-      const int64_t bid = nblk > 0 ? bids[min(c >> 1, nblk - 1)] : 0;  // an empty split reads block 0, unused
-      sreg[arr][i] = *(const u32x4*)(base + bid * sn + 8 * (c & 1));
-    }
-  }
   Int8Tile<D> ring[NB];
   const bool piped = mine >= 2 * NB;
   if (piped) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) load_tile(j, ring[j]);
   }
+  convert_query();
 #pragma unroll
   for (int arr = 0; arr < kScaleArrays; ++arr)
 #pragma unroll
-    for (int i = 0; i < kScaleLoads; ++i) {
-      const int c = threadIdx.x + kThreads * i;
-      if (c < 2 * nblk) *(u32x4*)(tsc + (arr * kScaleBlocks + (c >> 1)) * 8 + 4 * (c & 1)) = sreg[arr][i];
-    }
+    for (int hf = 0; hf < 2; ++hf)
+      *(u32x4*)(tsc + (arr * kScaleBlocks + threadIdx.x) * 8 + 4 * hf) = sreg[arr][hf];
   __syncthreads();  // token scales staged
   if (piped) {
     int k0 = 0;
