@@ -824,7 +824,7 @@ def main() -> int:
         for fmt, key in (("int8", "c4b_int8_per_token"), ("int8-kchannel", "c4a_int8_kchannel")):
             if args.impl not in ("auto", "mfma") and fmt != "int8":
                 continue  # the VALU streaming kernels cover the per-token format only
-            wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl)
+            wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl, splits=args.splits)
             res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
             if fmt == "int8":
                 res[key]["paged_read_floor"] = paged_read_floor(wl, args.steps, args.warmup)
