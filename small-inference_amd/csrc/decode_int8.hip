@@ -67,7 +67,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   constexpr int CPR = D / 16;  // 16-code chunks per token row
 
   __shared__ __align__(16) char smem[MfmaSmem<D>::kBytes];
-  __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 64 : 1];  // mode 2: each wave's tile scales
+  // mode 2: each wave's channel scales of two tiles (slot = tile index parity), [wave][slot][block][lane]
+  __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 2 * 64 : 1];
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
   __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
   __shared__ __align__(8) int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
@@ -215,6 +216,13 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     const int bi = (t0 - start) >> 4;
     const int b0 = bids[bi];
     const int b1 = (t0 + 16 < end) ? bids[bi + 1] : b0;  // branch-free: a missing second block re-reads the first
+    // Mode 2's channel scales first: the staging of the next tile's scales (stage_kc) then waits for them alone,
+    // not for the tile's codes issued after them. Lane L holds channels 2L, 2L + 1 (lanes past D / 2 repeat).
+    if (MODE == 2) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        tl.kc[mt] = *(const uint32_t*)(ksh + (int64_t)(mt ? b1 : b0) * a.ks_sn + 2 * (lane % (D / 2)));
+    }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int64_t blk = mt ? b1 : b0;
@@ -225,8 +233,6 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
         tl.k[mt][j] = __builtin_nontemporal_load((const u32x4*)(kb + r * D + 64 * j + 16 * q4));
 #pragma unroll
       for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
-      if (MODE == 2)  // lane L holds channels 2L, 2L + 1 (lanes past D / 2 repeat the first half)
-        tl.kc[mt] = *(const uint32_t*)(ksh + blk * a.ks_sn + 2 * (lane % (D / 2)));
     }
   };
   // Token scales of tokens 4 q4 .. 4 q4 + 3 of the tile's block mt (a second block past the end reads the last).
@@ -242,12 +248,22 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
 
   // p <= 2^4 against the lazily raised max, so that p * s_v (s_v <= 65504 / 127) stays within fp16.
   constexpr float kRescaleSlack = 4.f;
-  uint32_t* kcw = kcs + (MODE == 2 ? wave * 2 * 64 : 0);
-  auto process_tile = [&](int t0, Int8Tile<D>& tl) {
+  // Mode 2: a tile's channel scales go through LDS (each lane then reads the 8 D / 32 it needs), into the wave's
+  // slot of the tile's index parity. The pipelined loop stages tile k + 1's scales right after tile k, so a tile
+  // starts with them in LDS; the short path stages them as it starts the tile.
+  auto kc_slot = [&](int slot) { return kcs + (MODE == 2 ? (wave * 2 + slot) * 128 : 0); };
+  auto stage_kc = [&](const Int8Tile<D>& tl, int slot) {
+    if (MODE == 2) {
+      uint32_t* w = kc_slot(slot);
+      w[lane] = tl.kc[0];
+      w[64 + lane] = tl.kc[1];
+    }
+  };
+  auto process_tile = [&](int t0, Int8Tile<D>& tl, int slot, bool prestaged) {
     const bool partial = t0 + 32 > end;
-    if (MODE == 2) {  // the tile's channel scales go through LDS: each lane then reads the 8 D / 32 it needs
-      kcw[lane] = tl.kc[0];
-      kcw[64 + lane] = tl.kc[1];
+    const uint32_t* kcw = kc_slot(slot);
+    if (MODE == 2) {
+      if (!prestaged) stage_kc(tl, slot);
       wave_sync();
     }
     // V codes -> fp16 -> LDS (rows at or past the end are zero).
@@ -367,26 +383,37 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       *(u32x4*)(tsc + (arr * kScaleBlocks + threadIdx.x) * 8 + 4 * hf) = sreg[arr][hf];
   __syncthreads();  // token scales staged
   if (piped) {
+    // Tile k is in ring[k % NB]; after tile k, tile k + 1's channel scales (mode 2) go to LDS slot (k + 1) & 1.
+    stage_kc(ring[0], 0);
     int k0 = 0;
     for (; k0 + 2 * NB <= mine; k0 += NB) {
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        process_tile(tile_t0(k0 + j), ring[j]);
-        load_tile(k0 + j + NB, ring[j]);
+        const int k = k0 + j;
+        process_tile(tile_t0(k), ring[j], k & 1, true);
+        load_tile(k + NB, ring[j]);
+        stage_kc(ring[(j + 1) % NB], (k + 1) & 1);  // k + 1 < k0 + 2 NB <= mine
       }
     }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      process_tile(tile_t0(k0 + j), ring[j]);
-      if (k0 + j + NB < mine) load_tile(k0 + j + NB, ring[j]);
+      const int k = k0 + j;
+      process_tile(tile_t0(k), ring[j], k & 1, true);
+      if (k + NB < mine) load_tile(k + NB, ring[j]);
+      if (k + 1 < mine) stage_kc(ring[(j + 1) % NB], (k + 1) & 1);
     }
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-      if (k0 + NB + j < mine) process_tile(tile_t0(k0 + NB + j), ring[j]);
+    for (int j = 0; j < NB; ++j) {
+      const int k = k0 + NB + j;
+      if (k < mine) {
+        process_tile(tile_t0(k), ring[j], k & 1, true);
+        if (k + 1 < mine) stage_kc(ring[(j + 1) % NB], (k + 1) & 1);
+      }
+    }
   } else {
     for (int k = 0; k < mine; ++k) {
       load_tile(k, ring[0]);
-      process_tile(tile_t0(k), ring[0]);
+      process_tile(tile_t0(k), ring[0], 0, false);
     }
   }
 
