@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 6
+#define SIPA_ABI_VERSION 7
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -380,6 +380,45 @@ int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dtype, int64_
                           const int64_t* blocks, const int64_t* offsets, void* pool, void* pool2,
                           int32_t pool_dtype, int64_t p_stride_h, int64_t p_stride_n, int64_t p_stride_b,
                           void* stream);
+
+/*
+ * Format B ("int8-kchannel") writes of a decode step in one launch, with no reference counterpart (the reference's
+ * cache makes three calls, engine/quant_cache.py:161-170, and this library's three equivalents are
+ * sipa_quantize_store_tokens, sipa_store_tokens and sipa_quantize_store_blocks). For every row t < T (one new
+ * token):
+ *   1. v[t] quantized per token into v_pool[h, blocks[t], offsets[t], :] and v_scale[h, blocks[t], offsets[t]];
+ *   2. the bf16 rounding of k[t] stored to stage[h, stage_slots[t], offsets[t], :];
+ *   3. when quant_dst[t] >= 0 (quant_dst == NULL: when offsets[t] == B - 1, into blocks[t]), the slot's B tokens
+ *      (row t's just staged) quantized per channel into k_pool[h, quant_dst[t]] and k_scale[h, quant_dst[t], :].
+ * Results equal those three calls bit for bit when no two rows share a staging slot (a decode step: one row per
+ * sequence). Rows that do share one (the graph runner's padding rows, all on a scratch block) leave that slot
+ * and its destination with unspecified contents.
+ *   k, v [T, H, D] in x_dtype (SIPA_F32 / SIPA_BF16 / SIPA_F16), last dim contiguous; blocks, offsets,
+ *   stage_slots, quant_dst [T] int64; v_pool, k_pool [H, N, B, D] int8 (offset stride D); v_scale [H, N, B] and
+ *   k_scale [H, N, D] fp16; stage [H, n_stage, B, D] bf16.
+ */
+typedef struct sipa_kchan_write_params {
+  const void* k;
+  const void* v;
+  int32_t x_dtype;
+  int64_t k_stride_t, k_stride_h, v_stride_t, v_stride_h;
+  int32_t T, H, D, B;
+  const int64_t* blocks;
+  const int64_t* offsets;
+  const int64_t* stage_slots;
+  const int64_t* quant_dst; /* may be NULL */
+  int8_t* v_pool;
+  void* v_scale;
+  int8_t* k_pool;
+  void* k_scale;
+  int64_t q_stride_h, q_stride_n;   /* both int8 pools */
+  int64_t vs_stride_h, vs_stride_n; /* v_scale */
+  int64_t ks_stride_h, ks_stride_n; /* k_scale */
+  void* stage;
+  int64_t st_stride_h, st_stride_n, st_stride_b;
+} sipa_kchan_write_params;
+
+int32_t sipa_kchan_write_rows(const sipa_kchan_write_params* p, void* stream);
 
 #ifdef __cplusplus
 }

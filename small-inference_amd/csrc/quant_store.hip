@@ -149,6 +149,85 @@ __global__ void __launch_bounds__(256) store_tokens_kernel(const StoreArgs a) {
   }
 }
 
+// Format B's writes of a decode step in one launch (sipa_kchan_write_rows): workgroup t takes row t's token.
+//   V: per-token quantization at (blocks[t], offsets[t]), one 16-lane group per head, as quantize_tokens_kernel.
+//   K: the bf16 rounding of k[t] into its staging slot at offsets[t], as store_tokens_kernel; then, when the row
+//   quantizes its slot (dst[t] >= 0, or offsets[t] == B - 1 without dst), the slot's B tokens per channel into
+//   block dst[t] (or blocks[t]), as quantize_blocks_kernel: token offsets[t] from the value just rounded, the
+//   others from the slot, so nothing this launch stores is read back through memory.
+struct KchanArgs {
+  const void* k;
+  const void* v;
+  int64_t k_st, k_sh, v_st, v_sh;
+  const int64_t* blocks;
+  const int64_t* offsets;
+  const int64_t* slots;
+  const int64_t* dst;  // NULL: the row's own block when its offset is B - 1
+  int8_t* vq;
+  uint16_t* vs;
+  int8_t* kq;
+  uint16_t* ks;
+  uint16_t* stage;
+  int64_t q_sh, q_sn, vs_sh, vs_sn, ks_sh, ks_sn, st_sh, st_sn, st_sb;
+  int32_t T, H, D, B, x_dtype;
+};
+
+template <int EPL>  // V channels per lane: D / 16
+__global__ void __launch_bounds__(256) kchan_write_rows_kernel(const KchanArgs a) {
+  const int t = blockIdx.x;
+  const int64_t blk = a.blocks[t], off = a.offsets[t], slot = a.slots[t];
+  // V: heads grp, grp + 16, ... of the row, 16 lanes each (whole 16-lane groups run each iteration together)
+  const int grp = threadIdx.x >> 4, sub = threadIdx.x & 15;
+  for (int h = grp; h < a.H; h += 16) {
+    const int64_t xi = (int64_t)t * a.v_st + (int64_t)h * a.v_sh + sub * EPL;
+    float x[EPL];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      x[i] = load_as_f32(a.v, xi + i, a.x_dtype);
+      amax = fmaxf(amax, fabsf(x[i]));
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const _Float16 sh = (_Float16)(amax / kQMax);
+    const float s32 = (float)sh;
+    int8_t* qrow = a.vq + (int64_t)h * a.q_sh + blk * a.q_sn + off * a.D + sub * EPL;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) qrow[i] = quantize_code(x[i], s32);
+    if (sub == 0) a.vs[(int64_t)h * a.vs_sh + blk * a.vs_sn + off] = __builtin_bit_cast(uint16_t, sh);
+  }
+  // K: one thread per (head, channel)
+  const int64_t qdst = a.dst ? a.dst[t] : (off == a.B - 1 ? blk : -1);
+  for (int e = threadIdx.x; e < a.H * a.D; e += 256) {
+    const int h = e / a.D, d = e % a.D;
+    const uint16_t kb = f32_to_bf16_bits(load_as_f32(a.k, (int64_t)t * a.k_st + (int64_t)h * a.k_sh + d, a.x_dtype));
+    uint16_t* srow = a.stage + (int64_t)h * a.st_sh + slot * a.st_sn + d;  // token b of the slot at srow[b st_sb]
+    srow[off * a.st_sb] = kb;
+    if (qdst < 0) continue;
+    auto value = [&](int b) { return bf16_bits_to_f32(b == off ? kb : srow[(int64_t)b * a.st_sb]); };
+    int8_t* qb = a.kq + (int64_t)h * a.q_sh + qdst * a.q_sn + d;
+    float amax = 0.f;
+    if (a.B == 16) {  // the paged block size: all loads in flight at once, values kept in registers
+      float v[16];
+#pragma unroll
+      for (int b = 0; b < 16; ++b) v[b] = value(b);
+#pragma unroll
+      for (int b = 0; b < 16; ++b) amax = fmaxf(amax, fabsf(v[b]));
+      const _Float16 sh = (_Float16)(amax / kQMax);
+      const float s32 = (float)sh;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) qb[(int64_t)b * a.D] = quantize_code(v[b], s32);
+      a.ks[(int64_t)h * a.ks_sh + qdst * a.ks_sn + d] = __builtin_bit_cast(uint16_t, sh);
+      continue;
+    }
+    for (int b = 0; b < a.B; ++b) amax = fmaxf(amax, fabsf(value(b)));
+    const _Float16 sh = (_Float16)(amax / kQMax);
+    const float s32 = (float)sh;
+    for (int b = 0; b < a.B; ++b) qb[(int64_t)b * a.D] = quantize_code(value(b), s32);
+    a.ks[(int64_t)h * a.ks_sh + qdst * a.ks_sn + d] = __builtin_bit_cast(uint16_t, sh);
+  }
+}
+
 static bool float_dtype(int dt) { return dt == SIPA_F32 || dt == SIPA_BF16 || dt == SIPA_F16; }
 
 static int check_launch(const char* what) {
@@ -264,4 +343,32 @@ extern "C" int32_t sipa_store_tokens(const void* x, const void* x2, int32_t x_dt
   const unsigned wgs = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(store_tokens_kernel, dim3(wgs), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("store_tokens");
+}
+
+extern "C" int32_t sipa_kchan_write_rows(const sipa_kchan_write_params* p, void* stream) {
+  SIPA_CHECK(p != nullptr, SIPA_EINVAL, "NULL parameter block");
+  if (p->T == 0) return SIPA_OK;
+  SIPA_CHECK(p->T > 0 && p->H > 0, SIPA_EINVAL, "T %d, H %d", p->T, p->H);
+  SIPA_CHECK(p->D > 0 && p->D % 16 == 0 && p->D <= 256, SIPA_EUNSUPPORTED, "head_dim %d must be a multiple of 16 <= 256",
+             p->D);
+  SIPA_CHECK(p->B > 0 && p->B <= 64, SIPA_EUNSUPPORTED, "block_size %d must be in [1, 64]", p->B);
+  SIPA_CHECK(float_dtype(p->x_dtype), SIPA_EUNSUPPORTED, "k/v dtype %d", p->x_dtype);
+  SIPA_CHECK(p->k && p->v && p->blocks && p->offsets && p->stage_slots && p->v_pool && p->v_scale && p->k_pool &&
+                 p->k_scale && p->stage,
+             SIPA_EINVAL, "NULL pointer");
+  KchanArgs a{p->k, p->v, p->k_stride_t, p->k_stride_h, p->v_stride_t, p->v_stride_h, p->blocks, p->offsets,
+              p->stage_slots, p->quant_dst, p->v_pool, (uint16_t*)p->v_scale, p->k_pool, (uint16_t*)p->k_scale,
+              (uint16_t*)p->stage, p->q_stride_h, p->q_stride_n, p->vs_stride_h, p->vs_stride_n, p->ks_stride_h,
+              p->ks_stride_n, p->st_stride_h, p->st_stride_n, p->st_stride_b, p->T, p->H, p->D, p->B, p->x_dtype};
+  const dim3 grid((unsigned)p->T);
+  hipStream_t st = (hipStream_t)stream;
+  switch (p->D / 16) {
+    case 1: hipLaunchKernelGGL(kchan_write_rows_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(kchan_write_rows_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(kchan_write_rows_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(kchan_write_rows_kernel<8>, grid, dim3(256), 0, st, a); break;
+    case 16: hipLaunchKernelGGL(kchan_write_rows_kernel<16>, grid, dim3(256), 0, st, a); break;
+    default: return fail(SIPA_EUNSUPPORTED, "head_dim %d not in {16,32,64,128,256}", p->D);
+  }
+  return check_launch("kchan_write_rows");
 }

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library; see th
 
 # SIPA_LIB overrides the location (for copies of these modules placed inside another package).
 LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # element types (SIPA_F32 ...)
 F32, BF16, F16, I8 = 0, 1, 2, 3
@@ -68,6 +68,20 @@ class PrefillParams(ctypes.Structure):
     ]
 
 
+class KchanWriteParams(ctypes.Structure):
+    """Mirror of struct sipa_kchan_write_params."""
+    _fields_ = [
+        ("k", vp), ("v", vp), ("x_dtype", i32),
+        ("k_stride_t", i64), ("k_stride_h", i64), ("v_stride_t", i64), ("v_stride_h", i64),
+        ("T", i32), ("H", i32), ("D", i32), ("B", i32),
+        ("blocks", vp), ("offsets", vp), ("stage_slots", vp), ("quant_dst", vp),
+        ("v_pool", vp), ("v_scale", vp), ("k_pool", vp), ("k_scale", vp),
+        ("q_stride_h", i64), ("q_stride_n", i64), ("vs_stride_h", i64), ("vs_stride_n", i64),
+        ("ks_stride_h", i64), ("ks_stride_n", i64),
+        ("stage", vp), ("st_stride_h", i64), ("st_stride_n", i64), ("st_stride_b", i64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol the header declares
 SIGNATURES = {
     "sipa_abi_version": (i32, []),
@@ -95,6 +109,7 @@ SIGNATURES = {
                                              i64, vp]),
     "sipa_store_tokens": (i32, [vp, vp, i32, i64, i64, i64, i64, vp, i32, i32, i32, vp, vp, vp, vp, i32, i64, i64,
                                 i64, vp]),
+    "sipa_kchan_write_rows": (i32, [_c.POINTER(KchanWriteParams), vp]),
 }
 
 _lib = None

@@ -9,6 +9,8 @@ The quantizer is bit-exact with engine/quant.py: scale = fp16(absmax / 127), cod
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _hip
@@ -148,3 +150,48 @@ def store_tokens(x: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor, p
         blocks.data_ptr(), offsets.data_ptr(), pool.data_ptr(), _hip.ptr(pool2), _hip.dtype_code(pool.dtype),
         pool.stride(0), pool.stride(1), pool.stride(2), _hip.stream_of(x))
     _hip.check(rc, "store_tokens")
+
+
+def kchan_write_rows(k: torch.Tensor, v: torch.Tensor, blocks: torch.Tensor, offsets: torch.Tensor,
+                     stage_slots: torch.Tensor, quant_dst: torch.Tensor | None, v_pool: torch.Tensor,
+                     v_scale: torch.Tensor, k_pool: torch.Tensor, k_scale: torch.Tensor, stage: torch.Tensor) -> None:
+    """Format B's writes of a decode step in one launch (no reference counterpart; the reference's cache makes
+    three calls, engine/quant_cache.py:161-170): row t's V quantized per token at (blocks[t], offsets[t]), its K
+    rounded to bf16 into stage[:, stage_slots[t], offsets[t]], and, when quant_dst[t] >= 0 (quant_dst None: when
+    offsets[t] is the block's last offset, into blocks[t]), the slot's block quantized per channel into
+    k_pool / k_scale. Equal bit for bit to quantize_store_tokens + store_tokens + quantize_store_blocks when no
+    two rows share a staging slot."""
+    T, H, D = v.shape
+    if T == 0:
+        return
+    _require(k.shape == v.shape and k.dtype == v.dtype, "k and v must match in shape and dtype")
+    _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k and v need a contiguous last dim")
+    _require(blocks.numel() == T and offsets.numel() == T and stage_slots.numel() == T,
+             f"{T} rows need {T} blocks, offsets and staging slots")
+    _require(quant_dst is None or quant_dst.numel() == T, f"quant_dst needs {T} entries")
+    _token_pools(v, v_pool, v_scale)
+    N, B = v_pool.shape[1], v_pool.shape[2]
+    _require(tuple(k_pool.shape) == tuple(v_pool.shape) and k_pool.dtype == torch.int8 and k_pool.is_contiguous(),
+             f"k_pool {tuple(k_pool.shape)} must be int8 {tuple(v_pool.shape)}, contiguous")
+    _require(tuple(k_scale.shape) == (H, N, D) and k_scale.dtype == torch.float16 and k_scale.is_contiguous(),
+             f"k_scale {tuple(k_scale.shape)} must be fp16 [H={H}, N={N}, D={D}], contiguous")
+    _require(stage.dim() == 4 and (stage.shape[0], stage.shape[2], stage.shape[3]) == (H, B, D)
+             and stage.dtype == torch.bfloat16 and stage.stride(-1) == 1,
+             f"stage {tuple(stage.shape)} must be bf16 [H={H}, n_stage, B={B}, D={D}]")
+    _hip.require_gpu(k, v, blocks, offsets, stage_slots, v_pool, v_scale, k_pool, k_scale, stage)
+    blocks, offsets, stage_slots = _i64(blocks), _i64(offsets), _i64(stage_slots)
+    if quant_dst is not None:
+        _hip.require_gpu(quant_dst)
+        quant_dst = _i64(quant_dst)
+    p = _hip.KchanWriteParams()
+    p.k, p.v, p.x_dtype = k.data_ptr(), v.data_ptr(), _hip.dtype_code(v.dtype)
+    p.k_stride_t, p.k_stride_h, p.v_stride_t, p.v_stride_h = k.stride(0), k.stride(1), v.stride(0), v.stride(1)
+    p.T, p.H, p.D, p.B = T, H, D, B
+    p.blocks, p.offsets, p.stage_slots = blocks.data_ptr(), offsets.data_ptr(), stage_slots.data_ptr()
+    p.quant_dst = quant_dst.data_ptr() if quant_dst is not None else None
+    p.v_pool, p.v_scale, p.k_pool, p.k_scale = v_pool.data_ptr(), v_scale.data_ptr(), k_pool.data_ptr(), k_scale.data_ptr()
+    p.q_stride_h, p.q_stride_n = v_pool.stride(0), v_pool.stride(1)
+    p.vs_stride_h, p.vs_stride_n = v_scale.stride(0), v_scale.stride(1)
+    p.ks_stride_h, p.ks_stride_n = k_scale.stride(0), k_scale.stride(1)
+    p.stage, p.st_stride_h, p.st_stride_n, p.st_stride_b = stage.data_ptr(), stage.stride(0), stage.stride(1), stage.stride(2)
+    _hip.check(_hip.lib().sipa_kchan_write_rows(ctypes.byref(p), _hip.stream_of(v)), "kchan_write_rows")

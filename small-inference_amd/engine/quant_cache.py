@@ -149,6 +149,7 @@ class QuantPagedKVCache(PagedKVCache):
         super().__init__(cfg, num_blocks, block_size, device, dtype, attn_backend)
         self.fused_writes = self.on_gpu  # HIP quantize-and-store on GPU pools; torch quantizer otherwise
         self._staged = self._done = self._direct = None
+        self._rows_write = None  # format B decode step: (staging slot per row, quantization block per row or None)
         self._static = None  # format B's staging plan in persistent buffers (graph-replayed decode steps)
         if fmt == "int8-kchannel":
             if manager is None:
@@ -201,6 +202,7 @@ class QuantPagedKVCache(PagedKVCache):
             self._staged = (rows[:T], slots[:T], meta.slot_offsets)
             self._done = (dst[:T], src[:T])
             self._direct = None
+            self._rows_write = (slots[:T], dst[:T])
             self._tails = self._tails_dec = self._tails_pf = tails[:T]
             return
         plan = plan_staging(self._book, meta.slots_cpu, meta.query_starts, meta.context_lens, self.block_size)
@@ -216,6 +218,13 @@ class QuantPagedKVCache(PagedKVCache):
         self._staged = views[0:3] if plan.staged_rows.size else None
         self._done = views[3:5] if plan.done_blocks.size else None
         self._direct = views[5:7] if plan.whole_blocks.size else None
+        # A decode step (every row staged, in row order, each in a slot of its own) takes the one-launch write; a
+        # row then quantizes its slot when it writes the block's last offset, as the plan's done list says.
+        T = plan.staged_rows.size
+        decode_step = (plan.whole_blocks.size == 0 and T == meta.num_tokens
+                       and np.array_equal(plan.staged_rows, np.arange(T))
+                       and np.unique(plan.staged_slots).size == T)
+        self._rows_write = (views[1], None) if decode_step and T else None
         self._tails = views[7].to(torch.int32)
         self._tails_dec = self._rows_of(self._tails, getattr(self, "_decode_seqs", None), self._decode, dev)
         self._tails_pf = self._rows_of(self._tails, getattr(self, "_prefill_seqs", None), self._prefill_launch, dev)
@@ -272,12 +281,18 @@ class QuantPagedKVCache(PagedKVCache):
 
     def _write_fused(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """write() through the HIP kernels: one launch per step below."""
-        from .hip_quant import quantize_store_block_rows, quantize_store_blocks, quantize_store_tokens, store_tokens
+        from .hip_quant import (kchan_write_rows, quantize_store_block_rows, quantize_store_blocks,
+                                quantize_store_tokens, store_tokens)
 
         m = self.meta
         if self.fmt == "int8":  # V and K in one launch
             quantize_store_tokens(v, m.slot_blocks, m.slot_offsets, self.v[layer], self.v_scale[layer],
                                   x2=k, q_pool2=self.k[layer], s_pool2=self.k_scale[layer])
+            return
+        if self._rows_write is not None:  # a decode step: V, the K staging store and completed blocks in one launch
+            slots, dst = self._rows_write
+            kchan_write_rows(k, v, m.slot_blocks, m.slot_offsets, slots, dst, self.v[layer], self.v_scale[layer],
+                             self.k[layer], self.k_scale[layer], self.stage[layer])
             return
         quantize_store_tokens(v, m.slot_blocks, m.slot_offsets, self.v[layer], self.v_scale[layer])
         if self._staged is not None:

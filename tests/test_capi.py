@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_and_struct_layout():
-    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 6
+    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 7
     # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives; the
     # work-list fields, then the table width and staging count come last.
     assert _hip.DecodeParams.work_items.offset == _hip.DecodeParams.workspace_bytes.offset + 8
@@ -273,3 +273,25 @@ def test_prefill_split_policy_and_workspace():
     assert lib.sipa_prefill_workspace_bytes(1, 4, 2, 64, 512, 8192, 8) < d64  # G = 2: 64-token units
     rc = lib.sipa_prefill(ctypes.byref(prefill_params(max_context=8192, num_splits=8)), None)
     assert rc == _hip.EWORKSPACE, lib.sipa_last_error()
+
+
+def test_kchan_write_rows_checks_arguments():
+    """The format-B decode write refuses bad shapes and missing pools before any launch; no rows is a no-op."""
+    lib = _hip.lib()
+
+    def params(**over):
+        p = _hip.KchanWriteParams()
+        p.T, p.H, p.D, p.B, p.x_dtype = 4, 2, 64, 16, _hip.BF16
+        for name in ("k", "v", "blocks", "offsets", "stage_slots", "v_pool", "v_scale", "k_pool", "k_scale", "stage"):
+            setattr(p, name, 4096)
+        for key, val in over.items():
+            setattr(p, key, val)
+        return p
+
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(T=0)), None) == _hip.OK
+    assert lib.sipa_kchan_write_rows(None, None) == _hip.EINVAL
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(D=24)), None) == _hip.EUNSUPPORTED
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(B=65)), None) == _hip.EUNSUPPORTED
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(x_dtype=99)), None) == _hip.EUNSUPPORTED
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(stage=None)), None) == _hip.EINVAL
+    assert lib.sipa_kchan_write_rows(ctypes.byref(params(H=0)), None) == _hip.EINVAL

@@ -16,7 +16,8 @@ from cases import HEADS, as_np32, assert_decode_close
 from engine.block_manager import BlockManager
 from engine.config import ModelConfig
 from engine.hip_decode import paged_decode_attention
-from engine.hip_quant import quantize_store_block_rows, quantize_store_blocks, quantize_store_tokens, store_tokens
+from engine.hip_quant import (kchan_write_rows, quantize_store_block_rows, quantize_store_blocks,
+                              quantize_store_tokens, store_tokens)
 from engine.paged_cache import build_metadata
 from engine.quant_cache import QuantPagedKVCache
 from oracle import paged_ref
@@ -197,6 +198,92 @@ def write_chunks(m, cache, seq, k, v, chunks, layer=0):
 def tiny_cfg(Hq, Hkv, D):
     return ModelConfig(vocab_size=10, hidden_size=Hq * D, intermediate_size=16, num_layers=1, num_q_heads=Hq,
                        num_kv_heads=Hkv, head_dim=D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16], ids=["bf16", "fp32", "fp16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("explicit_dst", [False, True], ids=["dst_from_offsets", "dst_given"])
+def test_kchan_write_rows_equals_the_three_calls(dtype, D, explicit_dst):
+    """Format B's one-launch decode write (V per token, K staged as bf16, completed blocks quantized per channel)
+    leaves every pool equal bit for bit to quantize_store_tokens + store_tokens + quantize_store_blocks, for rows
+    in slots of their own, with offsets 0, 15 (block completed) and between, over staging slots holding earlier
+    tokens; with explicit destinations, some rows quantize into blocks of their own choosing, others into none."""
+    g = torch.Generator().manual_seed(11)
+    H, N, B, n_stage, T = 2, 64, 16, 24, 13
+    big = (torch.randn(T, 2 * H, D, generator=g) * 3).to("cuda", dtype)
+    k, v = big[:, :H], big[:, H:]  # strided rows
+    blocks = torch.randperm(N, generator=g)[:T].cuda()
+    offsets = torch.tensor([15, 0, 7, 15, 3, 15, 14, 1, 15, 9, 15, 12, 2]).cuda()
+    slots = torch.randperm(n_stage, generator=g)[:T].cuda()
+    stage0 = (torch.randn(H, n_stage, B, D, generator=g) * 2).bfloat16().cuda()
+    pools0 = [torch.randint(-127, 128, (H, N, B, D), generator=g, dtype=torch.int8).cuda(),
+              torch.rand(H, N, B, generator=g).half().cuda(),
+              torch.randint(-127, 128, (H, N, B, D), generator=g, dtype=torch.int8).cuda(),
+              torch.rand(H, N, D, generator=g).half().cuda()]
+    if explicit_dst:
+        dst = torch.full((T,), -1, dtype=torch.int64)
+        dst[::2] = torch.randperm(N, generator=g)[:(T + 1) // 2]
+        dst = dst.cuda()
+    else:
+        dst = None
+    # the three calls
+    vq, vs, kq, ks = (t.clone() for t in pools0)
+    stage = stage0.clone()
+    quantize_store_tokens(v, blocks, offsets, vq, vs)
+    store_tokens(k, slots, offsets, stage)
+    quantize = dst >= 0 if explicit_dst else offsets == B - 1
+    quantize_store_blocks(stage, slots[quantize], (dst if explicit_dst else blocks)[quantize], kq, ks)
+    # one launch
+    vq2, vs2, kq2, ks2 = (t.clone() for t in pools0)
+    stage2 = stage0.clone()
+    kchan_write_rows(k, v, blocks, offsets, slots, dst, vq2, vs2, kq2, ks2, stage2)
+    torch.cuda.synchronize()
+    assert int(quantize.sum()) >= 5
+    for a, b in ((vq, vq2), (vs, vs2), (kq, kq2), (ks, ks2), (stage, stage2)):
+        assert torch.equal(a, b)
+
+
+def test_kchan_decode_steps_match_torch_cache():
+    """Several sequences decoding together through format B's cache: the one-launch decode write (taken for every
+    step after the prefill) leaves the same pools, scales and staging as the torch quantizer path over 40 steps,
+    with blocks completing at different steps and a sequence freed and replaced midway."""
+    cfg = tiny_cfg(14, 2, 64)
+    g = torch.Generator().manual_seed(5)
+    prompts = {0: 5, 1: 16, 2: 29, 3: 1}
+    states = []
+    for fused in (False, True):
+        m, cache = make_cache("int8-kchannel", 64, 16, torch.bfloat16, cfg, n_stage=16)
+        cache.fused_writes = fused
+        gg = torch.Generator().manual_seed(6)
+        pos = {}
+        for s, n in prompts.items():
+            kv = torch.randn(2, n, 2, 64, generator=gg).bfloat16().cuda()
+            write_chunks(m, cache, s, kv[0], kv[1], [n])
+            pos[s] = n
+        used_fused = 0
+        for step in range(40):
+            if step == 17:  # sequence 1 finishes; sequence 9 starts with a 3-token prompt
+                m.free(1)
+                del pos[1]
+                kv = torch.randn(2, 3, 2, 64, generator=gg).bfloat16().cuda()
+                write_chunks(m, cache, 9, kv[0], kv[1], [3])
+                pos[9] = 3
+            seqs = sorted(pos)
+            for s in seqs:
+                m.append_slots(s, 1)
+            meta = build_metadata(m, [(s, pos[s], 1) for s in seqs], "cuda")
+            cache.begin(len(seqs), meta)
+            used_fused += cache._rows_write is not None
+            kv = torch.randn(2, len(seqs), 2, 64, generator=gg).bfloat16().cuda()
+            cache.write(0, kv[0], kv[1])
+            for s in seqs:
+                pos[s] += 1
+        torch.cuda.synchronize()
+        assert used_fused == 40
+        states.append([cache.k.clone(), cache.v.clone(), cache.k_scale.clone(), cache.v_scale.clone(),
+                       cache.stage.clone()])
+    for a, b in zip(*states):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
