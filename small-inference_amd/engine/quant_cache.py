@@ -119,21 +119,27 @@ def plan_staging(book: StagingBook, slots_cpu: list[int], query_starts: list[int
     ends = np.cumsum(sizes)
     blocks = uniq[order]
     first_off, last_off = off[rows[ends - sizes]], off[rows[ends - 1]]
-    held = np.fromiter((b in book.slot_of for b in blocks.tolist()), dtype=bool, count=blocks.size)
+    get = book.slot_of.get
+    slot_of_block = np.fromiter((get(b, -1) for b in blocks.tolist()), dtype=np.int64, count=blocks.size)
+    held = slot_of_block >= 0
     whole = (first_off == 0) & (sizes == B) & ~held
-    book.assign(blocks[~whole & ~held].tolist())
-    slot_of_block = np.fromiter((book.slot_of.get(b, -1) for b in blocks.tolist()), dtype=np.int64,
-                                count=blocks.size)
+    fresh = np.flatnonzero(~whole & ~held)
+    book.assign(blocks[fresh].tolist())
+    slot_of_block[fresh] = np.fromiter((book.slot_of[b] for b in blocks[fresh].tolist()), dtype=np.int64,
+                                       count=fresh.size)
     group = np.repeat(np.arange(blocks.size), sizes)  # position of each grouped row's block
     staged = ~whole[group]
     done = ~whole & (last_off == B - 1)
     plan = _StagingPlan(rows[staged], slot_of_block[group][staged], off[rows[staged]], blocks[done],
                         slot_of_block[done], blocks[whole], rows[whole[group]], np.empty(0, dtype=np.int64))
     book.release(plan.done_blocks.tolist())
+    # each sequence's last block is one of this forward's blocks; its slot (a done block's is released, but a
+    # sequence whose last block is done has a full last block and no tail)
     last_block = blk[np.asarray(query_starts[1:], dtype=np.int64) - 1]
     ctx = np.asarray(context_lens, dtype=np.int64)
-    plan.tails = np.array([book.slot_of[b] if c % B else -1 for b, c in zip(last_block.tolist(), ctx.tolist())],
-                          dtype=np.int64)
+    slot_sorted = np.empty_like(slot_of_block)
+    slot_sorted[order] = slot_of_block  # by position in uniq (sorted block ids)
+    plan.tails = np.where(ctx % B != 0, slot_sorted[np.searchsorted(uniq, last_block)], -1).astype(np.int64)
     return plan
 
 
