@@ -781,7 +781,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=8, help="pool layers the calls rotate over (defeats the MALL)")
     ap.add_argument("--splits", type=int, default=None, help="force a split count (default: CU-count policy)")
-    ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "valu", "valu_stream", "valu_dot2"])
+    ap.add_argument("--impl", default="auto", choices=["auto", "mfma", "mfma_pbf16", "valu", "valu_stream", "valu_dot2"])
     ap.add_argument("--combine", default="fused", choices=["fused", "kernel"])
     ap.add_argument("--details", dest="details", action="store_true", default=True)
     ap.add_argument("--no-details", dest="details", action="store_false")

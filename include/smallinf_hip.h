@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIPA_ABI_VERSION 7
+#define SIPA_ABI_VERSION 8
 
 /* element types */
 enum { SIPA_F32 = 0, SIPA_BF16 = 1, SIPA_F16 = 2, SIPA_I8 = 3 };
@@ -47,8 +47,18 @@ enum {
 /* impl of sipa_decode_params: AUTO picks MFMA where it applies, else the VALU fallback (any supported shape).
    VALU_STREAM / VALU_DOT2: the MFMA kernels' streaming structure with the dot products on the vector ALUs, fp32
    FMAs or v_dot2 pair products (bf16 q, block 16, head_dim 64/128, group 6-8, bf16 or int8 per-token pools); they
-   exist to measure the matrix cores against the VALU and are never picked by AUTO. */
-enum { SIPA_IMPL_AUTO = 0, SIPA_IMPL_VALU = 1, SIPA_IMPL_MFMA = 2, SIPA_IMPL_VALU_STREAM = 3, SIPA_IMPL_VALU_DOT2 = 4 };
+   exist to measure the matrix cores against the VALU and are never picked by AUTO. The bf16 MFMA kernel feeds P
+   to its P.V product as a bf16 hi + lo pair (about 16 significant bits; the reference's TF32 P.V keeps 11);
+   MFMA_PBF16 runs it with P rounded to one bf16 term (8 bits) instead, bf16 pools only, for measurement, never
+   picked by AUTO. */
+enum {
+  SIPA_IMPL_AUTO = 0,
+  SIPA_IMPL_VALU = 1,
+  SIPA_IMPL_MFMA = 2,
+  SIPA_IMPL_VALU_STREAM = 3,
+  SIPA_IMPL_VALU_DOT2 = 4,
+  SIPA_IMPL_MFMA_PBF16 = 5
+};
 
 /* combine of sipa_decode_params */
 enum { SIPA_COMBINE_FUSED = 0, SIPA_COMBINE_KERNEL = 1 };
@@ -166,9 +176,20 @@ int32_t sipa_decode(const sipa_decode_params* p, void* stream);
  * zeroes its counters). A call whose splits need more than that (sipa_decode_workspace_bytes() > 16 MiB) fails with
  * SIPA_EWORKSPACE before launching anything. Allocates nothing: no hipMalloc, hipFree or allocating library call.
  * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (different streams, or
- * threads) race and give wrong results; order them on one stream.
+ * threads) race and give wrong results; order them on one stream. Each completed call leaves the array's merge
+ * counters at zero, which the next call relies on; a call that did not complete (an aborted launch) or a work list
+ * that disagrees with the context lengths can leave one non-zero, and later calls would then merge that pair
+ * wrongly. The recovery is sipa_decode_noalloc_reset.
  */
 int32_t sipa_decode_noalloc(const sipa_decode_params* p, void* stream);
+
+/*
+ * Zeroes the merge counters of the current GPU's sipa_decode_noalloc array with one small kernel on `stream`
+ * (no memset node, so it may be captured in a HIP graph), after which calls merge correctly again. Ordered like a
+ * call: enqueue it where no sipa_decode_noalloc call on that GPU is in flight. Allocates nothing. No counterpart in
+ * the reference; for the callers of sipa_decode_noalloc.
+ */
+int32_t sipa_decode_noalloc_reset(void* stream);
 
 /*
  * Paged attention for multi-token rows (prefill chunks): replaces the reference's gather path for rows with

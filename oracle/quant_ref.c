@@ -60,16 +60,6 @@ float oracle_f16_to_f32(uint16_t h) {
   return float_of(sign | ((e - 15u + 127u) << 23) | (m << 13));
 }
 
-/* bf16 bits -> binary32 (exact) and binary32 -> bf16 bits (round to nearest even), for staging round trips. */
-float oracle_bf16_to_f32(uint16_t b) { return float_of((uint32_t)b << 16); }
-
-uint16_t oracle_f32_to_bf16(float f) {
-  const uint32_t x = bits_of(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  const uint32_t lsb = (x >> 16) & 1u;
-  return (uint16_t)((x + 0x7fffu + lsb) >> 16);
-}
-
 /*
  * Quantize n_groups groups of group_len values. Element i of group g is x[g * group_stride + i * elem_stride];
  * its code goes to the same index of q and the group's fp16 scale bits to scales[g]. Per token: groups are the

@@ -30,7 +30,10 @@
 //     B = P^T comes from the S^T registers without any shuffle (token slot i of lane q4 is token
 //     16 (i / 4) + 4 q4 + i % 4); A = V^T needs 8 tokens of one channel per lane, so each wave stages its V
 //     tile in LDS (coalesced 2 KiB block loads, row-major with padding) and reads it back transposed.
-//   P is rounded to bf16 for the MFMA; the softmax itself and all accumulation stay fp32.
+//   P enters the MFMA as two bf16 terms, P = P_hi + P_lo with P_hi = bf16(p) and P_lo = bf16(p - P_hi), two
+//   MFMAs per d-tile on the same V operand: about 16 significant bits of P, where the reference keeps P in fp32
+//   and runs P.V in TF32 (11 bits, engine/triton_decode.py:14-18,206-210); one bf16 term (8 bits) is the PHL =
+//   false variant, selectable for measurement. The softmax itself and all accumulation stay fp32.
 //
 // VALU kernel (any supported shape, fp32 or bf16, all KV modes): lane = token for q.k (q of the group in
 // LDS as fp32, fp32 FMAs), lane = channel for p.v (p of the tile in LDS). IEEE fp32 arithmetic throughout,
@@ -50,7 +53,8 @@ namespace sipa {
 // Bytes of the bf16 kernel's leading scalar arguments (three pointers and six int32), before its DecodeArgs.
 constexpr int kHotArgBytes = 3 * 8 + 6 * 4;
 
-template <int D, int NB>  // NB: tiles in flight per wave (the register prefetch ring)
+// NB: tiles in flight per wave (the register prefetch ring); PHL: P as a bf16 hi + lo pair (else one bf16 term).
+template <int D, int NB, bool PHL>
 __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __restrict__ hbt,
                                                              const int32_t* __restrict__ hctx,
                                                              const int32_t* __restrict__ hitems, int32_t hbt_ss,
@@ -204,13 +208,14 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __re
       for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
       m_run = m_new;
     }
-    bf16x8 pop;
+    bf16x8 pop, plo;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float p = fast_exp2(fmaf(sc[i >> 2][i & 3], a.scale_log2, -m_run));
       psum += p;
       pop[i] = (__bf16)p;
+      if (PHL) plo[i] = (__bf16)(p - (float)pop[i]);  // the rounding residual, exact in fp32
     }
     l_run += psum;
 
@@ -219,6 +224,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_bf16(const int32_t* __re
     for (int dt = 0; dt < DT; ++dt) {
       const bf16x8 vop = read_v_operand<bf16x8>(vw, tr_off, VP, 16 * dt);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[dt], 0, 0, 0);
+      if (PHL) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo, acc[dt], 0, 0, 0);
     }
     wave_sync();  // reads done before the next tile overwrites the LDS tile
   };
@@ -560,28 +566,29 @@ static int prefetch_tiles(int D) {
 }
 
 // The bf16 kernel takes its prologue's fields as leading scalars (preloaded into SGPRs), then the whole block.
-template <int D, int NB>
+template <int D, int NB, bool PHL>
 static int launch_bf16(dim3 grid, const DecodeArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((decode_mfma_bf16<D, NB>), grid, dim3(kThreads), 0, st, a.bt, a.ctx, a.items, (int32_t)a.bt_ss,
+  hipLaunchKernelGGL((decode_mfma_bf16<D, NB, PHL>), grid, dim3(kThreads), 0, st, a.bt, a.ctx, a.items, (int32_t)a.bt_ss,
                      a.S * a.Hkv, a.S, a.chunk, a.max_ctx, a.bt_w, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIPA_EHIP, "decode launch failed: %s", hipGetErrorString(e));
   return SIPA_OK;
 }
 
+template <bool PHL>
 static int launch_mfma(int D, int nb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
   if (D == 64) {
     switch (nb) {
-      case 1: return launch_bf16<64, 1>(grid, a, st);
-      case 2: return launch_bf16<64, 2>(grid, a, st);
-      case 3: return launch_bf16<64, 3>(grid, a, st);
-      default: return launch_bf16<64, 4>(grid, a, st);
+      case 1: return launch_bf16<64, 1, PHL>(grid, a, st);
+      case 2: return launch_bf16<64, 2, PHL>(grid, a, st);
+      case 3: return launch_bf16<64, 3, PHL>(grid, a, st);
+      default: return launch_bf16<64, 4, PHL>(grid, a, st);
     }
   }
   switch (nb) {
-    case 1: return launch_bf16<128, 1>(grid, a, st);
-    case 2: return launch_bf16<128, 2>(grid, a, st);
-    default: return launch_bf16<128, 3>(grid, a, st);
+    case 1: return launch_bf16<128, 1, PHL>(grid, a, st);
+    case 2: return launch_bf16<128, 2, PHL>(grid, a, st);
+    default: return launch_bf16<128, 3, PHL>(grid, a, st);
   }
 }
 
@@ -726,10 +733,17 @@ __global__ void __launch_bounds__(256) zero_words(int32_t* p, int n) {
 static std::mutex g_scratch_lock;
 static void* g_scratch_ptr[64];  // per device: the array's address, NULL until that device's first call
 
+static int zero_scratch_counters(void* ptr, hipStream_t st) {
+  hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, (int32_t*)ptr, kMaxCounters);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIPA_EHIP, "clearing the scratch counters: %s", hipGetErrorString(e));
+  return SIPA_OK;
+}
+
 // The scratch array of the current device. Its first call on a device looks up the array's address and zeroes the
 // merge-counter region with a fill kernel on `st` (a kernel, not a memset, so that a first call under stream capture
-// records a kernel node); later calls reuse both.
-static int scratch_on_current_device(hipStream_t st, char** out) {
+// records a kernel node); later calls reuse both. reset: zero the counters again on every call.
+static int scratch_on_current_device(hipStream_t st, char** out, bool reset = false) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(SIPA_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
@@ -740,13 +754,20 @@ static int scratch_on_current_device(hipStream_t st, char** out) {
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr)
       return fail(SIPA_EHIP, "address of the scratch array on device %d: %s", dev, hipGetErrorString(e));
-    hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, (int32_t*)ptr, kMaxCounters);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(SIPA_EHIP, "clearing the scratch counters: %s", hipGetErrorString(e));
+    const int rc = zero_scratch_counters(ptr, st);
+    if (rc != SIPA_OK) return rc;
     g_scratch_ptr[dev] = ptr;
+  } else if (reset) {
+    const int rc = zero_scratch_counters(g_scratch_ptr[dev], st);
+    if (rc != SIPA_OK) return rc;
   }
   *out = (char*)g_scratch_ptr[dev];
   return SIPA_OK;
+}
+
+extern "C" int32_t sipa_decode_noalloc_reset(void* stream) {
+  char* base = nullptr;
+  return scratch_on_current_device((hipStream_t)stream, &base, true);
 }
 
 static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scratch);
@@ -915,10 +936,13 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
                SIPA_EUNSUPPORTED, "the VALU streaming kernels need a bf16 query, block 16, head_dim 64/128, a group "
                "of 6-8, a bf16 pool or an int8 per-token pool with fp16 scales, and 16-byte aligned rows");
   }
+  SIPA_CHECK(p->impl != SIPA_IMPL_MFMA_PBF16 || (mfma_ok && mode == SIPA_KV_PLAIN), SIPA_EUNSUPPORTED,
+             "the bf16-P MFMA variant needs a bf16 query and pool, block 16, head_dim 64/128, 16-byte aligned rows");
   SIPA_CHECK(p->impl != SIPA_IMPL_MFMA || mfma_ok, SIPA_EUNSUPPORTED,
              "the MFMA kernels need a bf16 query, block 16, head_dim 64/128, 16-byte aligned rows and fp16 scales "
              "(or fp32 channel scales with a zero block stride)");
-  const bool use_mfma = mfma_ok && (p->impl == SIPA_IMPL_AUTO || p->impl == SIPA_IMPL_MFMA);
+  const bool p_bf16 = p->impl == SIPA_IMPL_MFMA_PBF16;
+  const bool use_mfma = mfma_ok && (p->impl == SIPA_IMPL_AUTO || p->impl == SIPA_IMPL_MFMA || p_bf16);
 
   const int64_t wgs = n_items > 0 ? (int64_t)n_items : (int64_t)S * Hkv * splits;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
@@ -927,7 +951,8 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
   if (valu_stream)
     rc = launch_valu_stream(D, G, mode, p->impl == SIPA_IMPL_VALU_DOT2, grid, a, st);
   else if (use_mfma && mode == SIPA_KV_PLAIN)
-    rc = launch_mfma(D, prefetch_tiles(D), grid, a, st);
+    rc = p_bf16 ? launch_mfma<false>(D, prefetch_tiles(D), grid, a, st)
+                : launch_mfma<true>(D, prefetch_tiles(D), grid, a, st);
   else if (use_mfma)
     rc = launch_mfma_int8(D, int8_variant, prefetch_tiles(D), grid, a, st);
   else if (p->q_dtype == SIPA_F32)

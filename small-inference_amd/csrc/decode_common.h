@@ -175,8 +175,8 @@ __device__ __forceinline__ void store_out4(const DecodeArgs& a, int s, int hq, i
 // resource (gfx9 descriptor word 3). Loads and stores through it with the sc1 cache-policy bit (aux 16) are
 // agent-coherent, like the relaxed agent-scope atomics above, but move 16 bytes per lane in one instruction.
 constexpr int kAuxSc1 = 16;
-// The sc0 bit alone (aux 1): loads that bypass the CU's L1 and are served by the XCD's L2, coherent with every
-// store made on the same XCD.
+// The sc0 bit alone (aux 1): workgroup-scope loads, served by the XCD's L2 (coherent with every store made on the
+// same XCD) once the CU's L1 holds no copy of the line: the merge invalidates the L1 before using them.
 constexpr int kAuxSc0 = 1;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rows(const DecodeArgs& a, int s, int h, int D) {
@@ -283,9 +283,14 @@ __device__ void publish_and_merge(const DecodeArgs& a, int s, int h, int nvalid,
   }
   __syncthreads();
   if (!*last_flag) return;
-  if (*last_flag == 2)
+  if (*last_flag == 2) {
+    // sc0 loads are workgroup-scope: outside threadgroup-split mode the CU's L1 may serve them. A line of partials
+    // this CU read earlier in the launch (another pair's merge, with rows sharing the line) could be stale there,
+    // so the L1 is invalidated first; the loads then come from the XCD's L2, which every split's write-through
+    // stores passed.
+    asm volatile("buffer_inv sc0" ::: "memory");
     combine_group<D, OUT_F32, kMergeL2>(a, s, h, nvalid);
-  else
+  } else
     combine_group<D, OUT_F32, kMergeMemory>(a, s, h, nvalid);
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counters + (int64_t)s * a.Hkv + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -17,7 +17,13 @@
 //     query and bf16 staged K (exact products).
 //   O^T += V_int^T . P'^T on the fp16 MFMA with the per-token V scale folded into P (P' = p s_v, fp16), as the
 //     reference does (acc += (p s_v) v_int; l keeps the unscaled p). The V tile goes to LDS already converted to
-//     fp16 and is read back transposed.
+//     fp16 and is read back transposed. The reference forms P' in fp32 (engine/triton_decode.py:126-130); fp16
+//     has its 11 significant bits but not its exponent range: with small V scales (V absmax under about 0.05)
+//     most P' would fall into fp16 subnormals. Each split therefore takes p' = p 2^e, with 2^e chosen from the
+//     largest V scale of its tokens so that max(s_v) 2^e lies in [2^10, 2^11): P' = p' s_v <= 2^4 2^11 stays
+//     below fp16's 65504, and every term within 2^-29 of the largest stays normal. The factor rides on the exp2's
+//     offset (p' = 2^(x - (m - e))), so l and acc both carry it and the split reports its max as m - e: the merge
+//     and the final acc / l are exactly those of p.
 // Lane (r, q4) loads 16-byte pieces 64 j + 16 q4 of K row r (one load instruction covers 64 contiguous bytes of each
 // of 16 rows), so the query operand uses that channel order too: k-slot 8 jj + i of lane group q4 is channel
 // 64 (jj / 2) + 16 q4 + 8 (jj % 2) + i.
@@ -72,6 +78,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
   __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
   __shared__ __align__(8) int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
+  __shared__ uint32_t vmax_bits[kWaves];  // each wave's largest V scale of the split (fp16 bits)
   __shared__ int last_flag;
 
   {
@@ -169,6 +176,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   f16x8 qh[KS], ql[KS];
   int qshift = 0;
   float sl2 = a.scale_log2;
+  float vshift = 0.f;  // p' = p 2^vshift (set once the split's V scales are in)
   auto convert_query = [&]() {
     float qf[KS][8];
     float qmax = 0.f;
@@ -246,7 +254,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // p <= 2^4 against the lazily raised max, so that p * s_v (s_v <= 65504 / 127) stays within fp16.
+  // p <= 2^4 against the lazily raised max, so that P' = p 2^vshift s_v <= 2^4 2^11 stays within fp16.
   constexpr float kRescaleSlack = 4.f;
   // Mode 2: a tile's channel scales go through LDS (each lane then reads the 8 D / 32 it needs), into the wave's
   // slot of the tile's index parity. The pipelined loop stages tile k + 1's scales right after tile k, so a tile
@@ -353,7 +361,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int mt = i >> 2, e = i & 3;
-      const float p = fast_exp2(fmaf(sc[mt][e], sl2, -m_run));
+      const float p = fast_exp2(fmaf(sc[mt][e], sl2, vshift - m_run));  // p 2^vshift
       psum += p;
       const uint32_t vsw = (e < 2) ? vsc[mt].x : vsc[mt].y;
       pop[i] = (_Float16)(p * h2f(vsw >> (16 * (e & 1))));
@@ -381,7 +389,29 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
       *(u32x4*)(tsc + (arr * kScaleBlocks + threadIdx.x) * 8 + 4 * hf) = sreg[arr][hf];
+  {
+    // The largest V scale of the split's tokens [start, end): thread t holds block t's 16 scales. Scales are
+    // non-negative fp16, whose bit patterns order like their values.
+    const int nv = min(max(end - (start + 16 * (int)threadIdx.x), 0), 16);
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t b = (sreg[0][j >> 3][(j >> 1) & 3] >> (16 * (j & 1))) & 0xffffu;
+      if (j < nv) mb = max(mb, b);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
+    if (lane == 0) vmax_bits[wave] = mb;
+  }
   __syncthreads();  // token scales staged
+  // p' = p 2^vshift: 2^vshift brings the split's largest V scale into [2^10, 2^11) (0 when every scale is 0).
+  {
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) mb = max(mb, vmax_bits[i]);
+    const float vm = h2f(mb);
+    if (vm > 0.f) vshift = (float)(10 - ((int)((__float_as_uint(vm) >> 23) & 0xff) - 127));
+  }
   if (piped) {
     // Tile k is in ring[k % NB]; after tile k, tile k + 1's channel scales (mode 2) go to LDS slot (k + 1) & 1.
     stage_kc(ring[0], 0);
@@ -417,7 +447,8 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
     }
   }
 
-  mfma_epilogue<D, false>(a, s, h, sp, nvalid, m_run, l_run, acc, smem, &last_flag);
+  // l and acc carry 2^vshift: as the state of p they belong to the max m_run - vshift.
+  mfma_epilogue<D, false>(a, s, h, sp, nvalid, m_run - vshift, l_run, acc, smem, &last_flag);
 }
 
 template <typename Kernel>

@@ -607,9 +607,10 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
         }
       }
     };
-    if (from_l2)
+    if (from_l2) {
+      asm volatile("buffer_inv sc0" ::: "memory");  // sc0 loads may hit the CU's L1: drop any earlier copy first
       merge(std::integral_constant<int, kAuxSc0>());
-    else
+    } else
       merge(std::integral_constant<int, kAuxSc1>());
     if (threadIdx.x == 0)
       __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

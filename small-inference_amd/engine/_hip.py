@@ -17,7 +17,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library; see th
 
 # SIPA_LIB overrides the location (for copies of these modules placed inside another package).
 LIB_PATH = Path(os.environ.get("SIPA_LIB") or Path(__file__).resolve().parent.parent / "build" / "libsmallinf_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # element types (SIPA_F32 ...)
 F32, BF16, F16, I8 = 0, 1, 2, 3
@@ -25,7 +25,7 @@ F32, BF16, F16, I8 = 0, 1, 2, 3
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, -1, -2, -3, -4
 # kv modes, implementations, combine strategies
 KV_PLAIN, KV_INT8_TOKEN, KV_INT8_KCHAN = 0, 1, 2
-IMPL = {"auto": 0, "valu": 1, "mfma": 2, "valu_stream": 3, "valu_dot2": 4}
+IMPL = {"auto": 0, "valu": 1, "mfma": 2, "valu_stream": 3, "valu_dot2": 4, "mfma_pbf16": 5}
 COMBINE = {"fused": 0, "kernel": 1}
 
 _c = ctypes
@@ -93,6 +93,7 @@ SIGNATURES = {
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_decode_noalloc": (i32, [_c.POINTER(DecodeParams), vp]),
+    "sipa_decode_noalloc_reset": (i32, [vp]),
     "sipa_build_work_list": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp]),
     "sipa_check_work_list": (i32, [vp, i32, i32, i32, i32, i32]),
     "sipa_prefill": (i32, [_c.POINTER(PrefillParams), vp]),

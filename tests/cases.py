@@ -4,6 +4,9 @@ random-order pattern, reference tests/test_paged.py:23-32 and tests/test_decode_
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -94,23 +97,49 @@ def oracle_cache_decode(cache, layer: int, q: np.ndarray, tables: list[list[int]
     return out
 
 
+def bf16_bracket(ref: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The two bf16 values that bracket each element of ref (equal to ref where it is a bf16 value): (lower,
+    upper), each as float64."""
+    ref = np.asarray(ref, dtype=np.float64)
+    mag = np.abs(ref)
+    t = mag.astype(np.float32).view(np.uint32) & np.uint32(0xFFFF0000)  # |ref| in fp32, truncated to bf16
+    step = np.uint32(0x10000)
+    cand = [np.where(t >= step, t - step, t), t, np.minimum(t + step, np.uint32(0x7F800000))]
+    vals = [c.view(np.float32).astype(np.float64) for c in cand]
+    lo = np.max([np.where(v <= mag, v, -np.inf) for v in vals], axis=0)
+    hi = np.min([np.where(v >= mag, v, np.inf) for v in vals], axis=0)
+    sign = np.where(ref < 0, -1.0, 1.0)
+    return np.where(ref < 0, sign * hi, sign * lo), np.where(ref < 0, sign * lo, sign * hi)
+
+
 def assert_decode_close(got, ref, what: str = "decode", atol: float = 8e-3) -> float:
-    """The north-star bound on a bf16 attention output against the fp32 oracle: max-abs <= atol (8e-3) wherever
-    |ref| < 2, and relative 2^-7 where |ref| >= 2 (there half a bf16 unit of the output alone reaches 2^-8 |out|,
-    7.8e-3 at |out| = 2). Prints the raw max-abs error and the |out| distribution; returns the raw max-abs."""
+    """The north-star bound on a bf16 attention output against the fp32 oracle plus the output's own rounding:
+    every element within atol (8e-3) of the oracle, or equal to one of the two bf16 values that bracket the
+    oracle's value (a result the exact output could round to). Prints the raw max-abs error, how many elements
+    needed the rounding clause and the |ref| percentiles; with SIPA_PARITY_LOG set, appends them as a JSON line to
+    that file. Returns the raw max-abs."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     err = np.abs(got - ref)
-    mag = np.abs(ref)
-    small = mag < 2.0
+    near = err <= atol
+    lo, hi = bf16_bracket(ref)
+    rounded = (got == lo) | (got == hi)
+    clause = ~near & rounded
+    bad = ~near & ~rounded
     raw = float(err.max()) if err.size else 0.0
-    e_small = float(err[small].max()) if small.any() else 0.0
-    rel_big = float((err[~small] / mag[~small]).max()) if (~small).any() else 0.0
+    mag = np.abs(ref)
     q = np.percentile(mag, [50, 99, 100]) if mag.size else [0, 0, 0]
-    print(f"{what}: max-abs {raw:.2e} (|ref| < 2: {e_small:.2e}; relative above: {rel_big:.2e}); "
-          f"|ref| median {q[0]:.2f}, p99 {q[1]:.2f}, max {q[2]:.2f}, {int((~small).sum())} values >= 2", flush=True)
-    assert e_small <= atol, f"{what}: max-abs {e_small:.3e} where |ref| < 2 exceeds {atol}"
-    assert rel_big <= 2.0 ** -7, f"{what}: relative error {rel_big:.3e} where |ref| >= 2 exceeds 2^-7"
+    stats = {"case": what, "max_abs": raw, "elements": int(err.size), "rounding_clause": int(clause.sum()),
+             "ref_abs_p50": float(q[0]), "ref_abs_p99": float(q[1]), "ref_abs_max": float(q[2])}
+    print(f"{what}: max-abs {raw:.2e}; {stats['rounding_clause']} of {err.size} elements past {atol} are the "
+          f"bf16 rounding of the oracle; |ref| median {q[0]:.2f}, p99 {q[1]:.2f}, max {q[2]:.2f}", flush=True)
+    log = os.environ.get("SIPA_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps(stats) + "\n")
+    if bad.any():
+        i = int(np.flatnonzero(bad.ravel())[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} elements off by more than {atol} and not a bf16 rounding of "
+                             f"the oracle, e.g. got {got.ravel()[i]!r} for {ref.ravel()[i]!r}")
     return raw
-

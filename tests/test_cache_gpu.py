@@ -125,19 +125,21 @@ def test_quant_cache_mixed_batches(fmt, dtype, D):
 
 
 def test_model_mixed_batch_kernel_vs_gather():
-    """A tiny Qwen2-shaped model (engine/model.py) drives the cache as the reference's model does (fused QKV
-    views as K and V, per-layer write then attend): one prefill chunk and two decode rows in one packed forward;
-    the HIP backend's logits equal the gather backend's to fp32 summation order (reference
-    tests/test_paged.py:186-205)."""
+    """The reference's tiny model shape (tests/tiny_model.py:7-10: 2 layers, 6 query heads over 2 KV heads, so a
+    GQA group of 3, head_dim 16, hidden 96, MLP 160) in fp32 over 4-token blocks drives the cache as the reference's
+    model does (fused QKV views as K and V, per-layer write then attend): one prefill chunk and two decode rows in
+    one packed forward; the kernel backend's logits equal the gather backend's to fp32 summation order (reference
+    tests/test_paged.py:186-205, which sets attn_backend after construction, as here)."""
     from engine.model import Qwen2Model
 
-    tiny = ModelConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_layers=2, num_q_heads=4,
-                       num_kv_heads=2, head_dim=16)
-    model = Qwen2Model(tiny, "cuda", torch.float32, seed=1, max_positions=128, std=0.2)
+    tiny = ModelConfig(vocab_size=97, hidden_size=96, intermediate_size=160, num_layers=2, num_q_heads=6,
+                       num_kv_heads=2, head_dim=16, rope_theta=10_000.0, max_position_embeddings=256)
+    model = Qwen2Model(tiny, "cuda", torch.float32, seed=1, max_positions=128, std=0.1)
     outs = {}
     for backend in ("gather", "triton"):
         m = fragmented_manager(32, 4, torch.Generator().manual_seed(2))
-        cache = PagedKVCache(tiny, 32, 4, "cuda", torch.float32, attn_backend=backend)
+        cache = PagedKVCache(tiny, 32, 4, "cuda", torch.float32)
+        cache.attn_backend = backend
         for s, n in ((1, 9), (2, 30)):
             m.allocate(s, n)
             meta = build_metadata(m, [(s, 0, n)], "cuda")

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_and_struct_layout():
-    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 7
+    assert _hip.lib().sipa_abi_version() == _hip.ABI_VERSION == 8
     # 13 int32 + 1 float, then pointers/strides: the binding's layout is what the header's struct gives; the
     # work-list fields, then the table width and staging count come last.
     assert _hip.DecodeParams.work_items.offset == _hip.DecodeParams.workspace_bytes.offset + 8

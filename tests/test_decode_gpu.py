@@ -91,6 +91,39 @@ def test_bf16_error_is_output_rounding(impl):
     assert rel < 2 ** -8
 
 
+def correctly_rounded_fraction(got: np.ndarray, ref64: np.ndarray) -> float:
+    """Fraction of bf16 outputs equal to the fp64 oracle rounded to bf16 (round to nearest even)."""
+    r = torch.from_numpy(ref64.astype(np.float32)).bfloat16().double().numpy()
+    return float((got == r).mean())
+
+
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_pv_product_keeps_reference_precision_of_p(heads):
+    """The reference keeps P in fp32 and runs P.V in TF32, 11 significant bits of P (engine/triton_decode.py:14-18,
+    206-210). Max-abs hides P's precision under the output's own bf16 rounding, so this counts outputs equal to the
+    fp64 oracle rounded to bf16: with P carried to b bits that fraction is about 0.58 (b = 8), 0.89-0.93 (b = 11,
+    TF32) and 0.99 (b = 16) on these shapes (numpy simulation of the same softmax with P rounded to b bits). The
+    default kernel (P as a bf16 hi + lo pair) must reach 0.95; the one-term bf16-P variant must not, which shows
+    the statistic separates the two."""
+    lengths = [100, 777, 1000, 2048, 3000, 8192]
+    Hq, Hkv, D = HEADS[heads]
+    q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=11)
+    scale = D ** -0.5
+    ref64 = oracle_decode(q, k, v, tables, lengths, scale, np.float64)
+    frac = {}
+    for impl in ("auto", "mfma_pbf16"):
+        for splits in (1, None):
+            print(f"case {heads} lengths={lengths} impl={impl} splits={splits}", flush=True)
+            out = paged_decode_attention(q, k, v, bt, ctx, scale, max(lengths), num_splits=splits, impl=impl)
+            torch.cuda.synchronize()
+            got = out.double().cpu().numpy()
+            assert np.abs(got - ref64).max() <= 8e-3
+            frac[impl, splits] = correctly_rounded_fraction(got, ref64)
+    print(f"\ncorrectly rounded fraction: {frac}")
+    assert min(frac["auto", 1], frac["auto", None]) >= 0.95, frac
+    assert max(frac["mfma_pbf16", 1], frac["mfma_pbf16", None]) < 0.8, frac
+
+
 def test_split_policy_uses_cu_count():
     """The split policy reads the device's CU count and fills it: a 32 x 8k batch (64 programs) gets about one
     workgroup per CU, with splits of at most 2048 tokens."""
@@ -102,6 +135,29 @@ def test_split_policy_uses_cu_count():
     s = choose_splits(32, 2, 8192, cu)
     launched, chunk = split_plan(8192, s)
     assert chunk <= 2048 and 64 * launched >= min(cu, 64 * 8192 // 256)
+
+
+@pytest.mark.parametrize("impl", ["mfma", "valu"])
+def test_l2_and_memory_merges_agree_past_the_cu_count(impl):
+    """The fused merge reads the split partials from the XCD's L2 when every split of a pair ran there (the grid
+    with sequences x KV heads a multiple of 8) and through memory otherwise. Both read the same partials in the
+    same order, so 256 sequences (512 pairs: the L2 path) and the same 256 plus one more (514 pairs: memory)
+    give the same bits for the 256, on grids of 2,048 workgroups, eight per CU, where a CU merges several pairs
+    whose partial rows share cache lines; both match the oracle."""
+    Hq, Hkv, D = HEADS["0.5B"]
+    g = torch.Generator().manual_seed(17)
+    lengths = torch.randint(600, 2049, (257,), generator=g).tolist()
+    lengths[0] = 2048
+    q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=17)
+    scale = D ** -0.5
+    outs = []
+    for S in (256, 257):
+        print(f"case merge paths impl={impl} S={S} splits=4", flush=True)
+        outs.append(paged_decode_attention(q[:S], k, v, bt[:S], ctx[:S], scale, 2048, num_splits=4, impl=impl))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1][:256])
+    ref = oracle_decode(q[:32], k, v, tables[:32], lengths[:32], scale, np.float32)
+    assert_decode_close(outs[0][:32].double().cpu().numpy(), ref, f"merge paths {impl}")
 
 
 def test_repeated_calls_reuse_workspace():

@@ -487,3 +487,119 @@ def test_device_tables_follow_the_manager():
         live.add(s)
     with pytest.raises(RuntimeError):
         m.allocate(max(live) + 1, 1)
+
+
+def test_parity_helper_admits_only_output_rounding():
+    """assert_decode_close (the GPU parity bar): an element passes within 8e-3 of the fp32 oracle or as one of the
+    two bf16 values around it. Planted on the CPU: a result one bf16 unit beyond the bracket at |ref| in [4, 8)
+    (1.6e-2 off) fails; the correctly rounded value and the other side of the bracket pass; small values need 8e-3."""
+    import numpy as np
+    import pytest
+    import torch
+
+    from cases import assert_decode_close, bf16_bracket
+
+    rng = np.random.default_rng(0)
+    ref = np.concatenate([rng.standard_normal(500), rng.uniform(4, 8, 500) * rng.choice([-1, 1], 500)])
+    ref = ref.astype(np.float32).astype(np.float64)
+    lo, hi = bf16_bracket(ref)
+    rne = torch.from_numpy(ref.astype(np.float32)).bfloat16().double().numpy()
+    assert np.all((rne == lo) | (rne == hi)) and np.all(lo <= ref) and np.all(ref <= hi)
+    assert np.all(hi - lo <= np.abs(ref) * 2.0 ** -7)
+    assert_decode_close(rne, ref, "correctly rounded")
+    assert_decode_close(np.where(rne == lo, hi, lo), ref, "other side of the bracket")
+    big = np.abs(ref) >= 4
+    bad = rne.copy()
+    bad[big] = np.where(ref[big] > 0, hi[big] + (hi[big] - lo[big]), lo[big] - (hi[big] - lo[big]))
+    with pytest.raises(AssertionError):
+        assert_decode_close(bad, ref, "one unit past the bracket")
+    ref2, off = ref.copy(), rne.copy()
+    ref2[3], off[3] = 0.5, 0.51171875  # three bf16 units (1.2e-2) above a bf16 oracle value of 0.5
+    with pytest.raises(AssertionError):
+        assert_decode_close(off, ref2, "1.2e-2 off at |ref| = 0.5")
+
+
+def _plan_per_token(slot_of: dict, free: list, slots_cpu, query_starts, context_lens, B):
+    """A plain per-token restatement of the reference's format-B staging plan (engine/quant_cache.py:84-122): group
+    the forward's slots by block in order of first token; a block without a slot written whole at offsets 0 .. B-1
+    is quantized directly from its rows; every other block takes a slot (from the end of the free list) on first
+    use and stages its rows; a block whose last offset is written is done and gives its slot back after the loop;
+    each sequence's tail is the slot of its last block when that block is partial. Mutates slot_of and free."""
+    by_block = {}
+    for row, slot in enumerate(slots_cpu):
+        by_block.setdefault(slot // B, []).append((row, slot % B))
+    staged, done, whole, whole_rows = [], [], [], []
+    for b, items in by_block.items():
+        if b not in slot_of and items[0][1] == 0 and len(items) == B:
+            whole.append(b)
+            whole_rows += [r for r, _ in items]
+            continue
+        if b not in slot_of:
+            slot_of[b] = free.pop()
+        staged += [(r, slot_of[b], o) for r, o in items]
+        if items[-1][1] == B - 1:
+            done.append(b)
+    done_slots = [slot_of[b] for b in done]
+    for b in done:
+        free.append(slot_of.pop(b))
+    tails = []
+    for i, ctx in enumerate(context_lens):
+        last_block = slots_cpu[query_starts[i + 1] - 1] // B
+        tails.append(slot_of[last_block] if ctx % B else -1)
+    return staged, done, done_slots, whole, whole_rows, tails
+
+
+def test_plan_staging_equals_the_per_token_plan():
+    """engine/quant_cache.plan_staging (vectorised: one pass over held slots, tails by binary search) equals the
+    plain per-token plan over 400 random mixed forwards of a live block manager: decode rows, prefill chunks of
+    1-40 tokens (whole 16-token blocks among them), sequences that start and finish (freed blocks return their
+    slots through the manager's listener, in the same order for both); every plan field and the book's state
+    (block -> slot map, free-slot stack order) after each forward."""
+    import random
+
+    from engine.block_manager import BlockManager
+    from engine.paged_cache import build_metadata
+    from engine.quant_cache import StagingBook, plan_staging
+
+    B, rng = 16, random.Random(3)
+    m = BlockManager(4096, B)
+    book = StagingBook(256)
+    ref_slot_of, ref_free = {}, list(book.free)
+
+    def release_both(blocks):
+        book.release(blocks)
+        for b in blocks:
+            s = ref_slot_of.pop(b, None)
+            if s is not None:
+                ref_free.append(s)
+
+    m.add_free_listener(release_both)
+    live, next_id, checked = {}, 0, 0
+    for step in range(400):
+        for s in [s for s in live if rng.random() < 0.08]:
+            m.free(s)
+            del live[s]
+        while len(live) < 12 and rng.random() < 0.7:
+            m.allocate(next_id, 0)
+            live[next_id] = 0
+            next_id += 1
+        batch = []
+        for s in sorted(live):
+            n = 1 if rng.random() < 0.6 else rng.choice([rng.randint(1, 40), B, 2 * B, B - live[s] % B])
+            m.append_slots(s, n)
+            batch.append((s, live[s], n))
+            live[s] += n
+        if not batch:
+            continue
+        meta = build_metadata(m, batch, "cpu")
+        args = (meta.slots_cpu, meta.query_starts, meta.context_lens, B)
+        plan = plan_staging(book, *args)
+        staged, done, done_slots, whole, whole_rows, tails = _plan_per_token(ref_slot_of, ref_free, *args)
+        assert [tuple(x) for x in zip(plan.staged_rows.tolist(), plan.staged_slots.tolist(),
+                                      plan.staged_offs.tolist())] == staged, step
+        assert plan.done_blocks.tolist() == done and plan.done_slots.tolist() == done_slots, step
+        assert plan.whole_blocks.tolist() == whole and plan.whole_rows.tolist() == whole_rows, step
+        assert plan.tails.tolist() == tails, step
+        assert book.slot_of == ref_slot_of and book.free == ref_free, step
+        checked += len(meta.slots_cpu)
+    assert checked > 3000 and next_id > 20

@@ -355,7 +355,7 @@ def test_kernel_matches_dequantized_reference(dtype, fmt, heads, B, splits):
 
 # ---- INT8 decode kernels, forced: MFMA and VALU, both formats, and constant channel scales ------------------------
 
-def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False):
+def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False, v_mag=1.0):
     """INT8 pools built by the HIP quantizers (through the cache), outlier channels in K, and the oracle's fp32
     dequantized K/V per sequence. Returns (q, cache, meta, k32 list, v32 list). The closing step re-writes every
     sequence's last token, so format B stages one block per sequence: twice as many staging slots as sequences
@@ -371,7 +371,7 @@ def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False):
         m.allocate(s, 0)
     for s, n in enumerate(lengths):
         k = (torch.randn(n, Hkv, D, generator=g) * outlier).to("cuda", torch.bfloat16)
-        v = torch.randn(n, Hkv, D, generator=g).to("cuda", torch.bfloat16)
+        v = (torch.randn(n, Hkv, D, generator=g) * v_mag).to("cuda", torch.bfloat16)
         write_chunks(m, cache, s, k, v, [n] if n < 50 else [37, n - 37])
     meta = build_metadata(m, [(s, n - 1, 1) for s, n in enumerate(lengths)], "cuda")
     cache.begin(len(lengths), meta)
@@ -546,3 +546,89 @@ def test_int8_mfma_query_magnitudes(fmt, const, heads):
     ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
                     for s in range(len(lengths))])
     assert_decode_close(got, ref, f"int8 query magnitudes {fmt} const={const} {heads}")
+
+
+@pytest.mark.parametrize("v_mag", [2.0 ** -8, 2.0 ** -14], ids=["v_2^-8", "v_2^-14"])
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_int8_mfma_small_v_scales(v_mag, fmt, heads):
+    """The INT8 MFMA kernels form P' = p s_v in fp16, whose exponent range is far narrower than the reference's
+    fp32 P' (engine/triton_decode.py:126-130): V of magnitude 2^-8 (scales about 1e-4) or 2^-14 (fp16-subnormal
+    scales) would put most P' among fp16 subnormals. Each split scales p by a power of two chosen from its largest
+    V scale, so the output divided by the V magnitude meets the unit-scale bound against the oracle's fp32
+    dequantize-then-attend of the same cache, divided likewise (the factor is a power of two: exact)."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [1, 17, 300, 1000, 3000]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=21, v_mag=v_mag)
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    for splits in (1, None):
+        print(f"case int8 small V {v_mag:g} {fmt} {heads} splits={splits}", flush=True)
+        out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                     max(lengths), num_splits=splits, quant=quant, impl="mfma")
+        got = out.double().cpu().numpy()
+        assert np.isfinite(got).all()
+        assert_decode_close(got / v_mag, ref / v_mag, f"int8 V x {v_mag:g} {fmt} {heads} splits={splits}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_c4_quantize_store_of_64_new_tokens_is_exact(fmt):
+    """Config C4's write: 64 sequences of the 1.5B shape (2 KV heads, head_dim 128) each append one token through
+    the cache, K with 4 of 128 channels per head scaled by U[20, 68] (C4's outlier channels), K and V strided views
+    of one fused projection output, one with a zero vector. Codes and fp16 scale bits equal the oracle's quantizer
+    (reference tests/test_quant_cache.py:246-266): per token for V and format A's K; for format B's K, the staged
+    bf16 rows of a partial block, and the per-channel codes and scales of every block the new token completes,
+    over that block's 16 rows."""
+    Hq, Hkv, D, B, S = 12, 2, 128, 16, 64
+    g = torch.Generator().manual_seed(31)
+    outlier = torch.ones(Hkv, D)
+    for h in range(Hkv):
+        outlier[h, torch.randperm(D, generator=g)[:4]] = 20 + 48 * torch.rand(4, generator=g)
+    before = torch.randint(0, 48, (S,), generator=g).tolist()
+    for s in range(0, S, 4):
+        before[s] = 16 * (s % 3) + 15  # these sequences' new token completes a block
+    m, cache = make_cache(fmt, S * 4 + 8, B, torch.bfloat16, tiny_cfg(Hq, Hkv, D), n_stage=2 * S)
+    hist_k = {}
+    for s, n in enumerate(before):
+        m.allocate(s, 0)
+        kx = (torch.randn(max(n, 1), Hkv, D, generator=g) * outlier).bfloat16()
+        hist_k[s] = kx[:n]
+        if n:
+            write_chunks(m, cache, s, kx[:n].cuda(), torch.randn(n, Hkv, D, generator=g).bfloat16().cuda(), [n])
+    qkv = torch.randn(S, Hq + 2 * Hkv, D, generator=g)
+    qkv[:, Hq:Hq + Hkv] *= outlier
+    qkv = qkv.bfloat16().cuda()
+    k_new, v_new = qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
+    k_new[9, 1] = 0
+    v_new[9, 0] = 0
+    for s in range(S):
+        m.append_slots(s, 1)
+    meta = build_metadata(m, [(s, before[s], 1) for s in range(S)], "cuda")
+    print(f"case c4 store {fmt} sequences={S} completed blocks={sum(1 for n in before if n % B == B - 1)}", flush=True)
+    cache.begin(S, meta)
+    cache.write(0, k_new, v_new)
+    torch.cuda.synchronize()
+    slots = np.asarray(meta.slot_mapping.cpu().numpy(), dtype=np.int64)
+    blk, off = torch.from_numpy(slots // B).cuda(), torch.from_numpy(slots % B).cuda()
+    v_ref, vs_ref = paged_ref.quantize_per_token(as_np32(v_new))
+    assert np.array_equal(cache.v[0][:, blk, off].transpose(0, 1).cpu().numpy(), v_ref)
+    assert np.array_equal(bits16(cache.v_scale[0][:, blk, off].t().cpu().numpy()), bits16(vs_ref))
+    if fmt == "int8":
+        k_ref, ks_ref = paged_ref.quantize_per_token(as_np32(k_new))
+        assert np.array_equal(cache.k[0][:, blk, off].transpose(0, 1).cpu().numpy(), k_ref)
+        assert np.array_equal(bits16(cache.k_scale[0][:, blk, off].t().cpu().numpy()), bits16(ks_ref))
+        return
+    kq, ks, stage = cache.k[0].cpu().numpy(), cache.k_scale[0].cpu().numpy(), cache.stage[0].cpu()
+    done = 0
+    for s in range(S):
+        b, o = int(slots[s] // B), int(slots[s] % B)
+        rows = torch.cat([hist_k[s][before[s] - o:], k_new[s:s + 1].cpu()])  # the block's rows so far, [o + 1, H, D]
+        if o == B - 1:  # completed: quantized per channel from its 16 bf16 rows
+            q_ref, s_ref = paged_ref.quantize_per_channel(as_np32(rows.transpose(0, 1)), axis=1)
+            assert np.array_equal(kq[:, b], q_ref), s
+            assert np.array_equal(bits16(ks[:, b]), bits16(s_ref)), s
+            done += 1
+        else:  # partial: the rows wait in the block's staging slot, rounded to bf16
+            slot = cache._stage_of[b]
+            assert torch.equal(stage[:, slot, :o + 1], rows.transpose(0, 1)), s
+    assert done == sum(1 for n in before if n % B == B - 1) >= S // 4
