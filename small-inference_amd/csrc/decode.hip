@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
   const int start = w.start;
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
-  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
+  const int nvalid = w.nvalid < 0 ? splits_holding(ctx, a.chunk, a.chunk_old, a.n_old) : w.nvalid;
   const int G = a.G, B = a.B;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -462,7 +462,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu(const DecodeArgs a) {
 template <int D, bool OUT_F32>
 __global__ void __launch_bounds__(kThreads) combine_splits(const DecodeArgs a) {
   const int h = blockIdx.x, s = blockIdx.y;
-  const int nvalid = (context_len(a, s) + a.chunk - 1) / a.chunk;
+  const int nvalid = splits_holding(context_len(a, s), a.chunk, a.chunk_old, a.n_old);
   if (nvalid <= 1) return;  // the single split wrote the output itself
   combine_group<D, OUT_F32, kMergePlain>(a, s, h, nvalid);
 }
@@ -613,6 +613,39 @@ extern "C" int32_t sipa_choose_splits_for(int32_t num_seqs, int32_t num_kv_heads
   int splits = choose_splits_host(num_seqs, num_kv_heads, max_context, (int8 ? 2 : 1) * cu, int8);
   if (int8 && max_context > 0) splits = std::max(splits, ceil_div(max_context, kMaxInt8Split));
   return splits;
+}
+
+// Grids of exactly two workgroups per CU, each CU holding workgroups L and L + CUs (the dispatcher deals the first
+// CU-count workgroups one per CU, then the next ones): the older of each pair wins instruction-issue arbitration
+// and streams faster while both run (C4, equal splits: 17.5 against 23 us to the end of streaming), so the older
+// class gets splits `ratio` times as long. This needs sequences x KV heads to divide the CU count (the first
+// CUs / SH splits of every pair are then the older class). Default ratio: kOldSplitRatio; SIPA_OLD_RATIO, read once
+// per process, overrides it for tuning sweeps (<= 1: equal splits).
+constexpr double kOldSplitRatio = 1.6;
+
+static double old_split_ratio() {
+  static const double r = [] {
+    const char* e = getenv("SIPA_OLD_RATIO");
+    return e ? atof(e) : kOldSplitRatio;
+  }();
+  return r;
+}
+
+static void two_class_splits(int64_t SH, int max_ctx, int splits, int cu, int max_split, int* chunk, int* chunk_old,
+                             int* n_old) {
+  *n_old = 0;
+  *chunk_old = 0;
+  const double r = old_split_ratio();
+  if (r <= 1.0 || cu <= 0 || SH <= 0 || cu % SH != 0 || splits != 2 * (cu / SH)) return;
+  const int n = (int)(cu / SH);
+  constexpr int kAlign = 32 * kWaves;  // whole 32-token tiles for every wave of the MFMA kernels
+  const int co = ceil_div((int64_t)std::ceil(r * max_ctx / (n * (1.0 + r))), kAlign) * kAlign;
+  if (co > max_split || (int64_t)n * co >= max_ctx) return;
+  const int cy = ceil_div(ceil_div(max_ctx - (int64_t)n * co, n), kAlign) * kAlign;
+  if (cy > co) return;
+  *n_old = n;
+  *chunk_old = co;
+  *chunk = cy;
 }
 
 // int8: the INT8 kernels' splits are at most kMaxInt8Split tokens (more splits than requested if need be).
@@ -944,6 +977,12 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
   const bool p_bf16 = p->impl == SIPA_IMPL_MFMA_PBF16;
   const bool use_mfma = mfma_ok && (p->impl == SIPA_IMPL_AUTO || p->impl == SIPA_IMPL_MFMA || p_bf16);
 
+  // Measured on C4 (sweeps of the ratio, alternating runs): format B 30.9 -> 30.1 us at 1.6; the per-token format
+  // within noise at every ratio (and 0.2 us slower at 1.6 with its workgroup-wide scale staging), so it keeps equal
+  // splits, as does the bf16 kernel, whose policy grid is one workgroup per CU.
+  if (n_items == 0 && use_mfma && splits > 1 && mode == SIPA_KV_INT8_KCHAN)
+    two_class_splits((int64_t)S * Hkv, p->max_context, splits, sipa_device_cu_count(-1), kMaxInt8Split, &a.chunk,
+                     &a.chunk_old, &a.n_old);
   const int64_t wgs = n_items > 0 ? (int64_t)n_items : (int64_t)S * Hkv * splits;
   SIPA_CHECK(wgs <= 0x7fffffff, SIPA_EINVAL, "%lld workgroups exceed the grid limit", (long long)wgs);
   const dim3 grid((unsigned)wgs);

@@ -66,6 +66,25 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Token ranges of the split grid: the first n_old splits of every sequence hold chunk_old tokens, the others chunk
+// (n_old = 0: all chunk). On a grid of two workgroups per CU the first CU-count workgroups (the earlier-dispatched
+// of each CU's pair) are given the longer splits: the older workgroup of a CU wins the instruction-issue arbitration
+// and streams faster while both run, so with equal splits it finished ~5 us before its partner, which then ran
+// alone at half the CU's occupancy.
+__device__ __forceinline__ int split_begin(int sp, int chunk, int chunk_old, int n_old) {
+  return sp <= n_old ? sp * chunk_old : n_old * chunk_old + (sp - n_old) * chunk;
+}
+
+__device__ __forceinline__ int split_length(int sp, int chunk, int chunk_old, int n_old) {
+  return sp < n_old ? chunk_old : chunk;
+}
+
+// Splits that hold tokens of a ctx-token sequence.
+__device__ __forceinline__ int splits_holding(int ctx, int chunk, int chunk_old, int n_old) {
+  const int b = n_old * chunk_old;
+  return ctx <= b ? (ctx + chunk_old - 1) / chunk_old : n_old + (ctx - b + chunk - 1) / chunk;
+}
+
 // Without a work list the grid is one-dimensional, sequence index fastest, then KV head, then split. The hardware
 // hands workgroup L to XCD L % 8, so consecutive sequences land on different XCDs and a ragged batch's work spreads
 // evenly over them; and every sequence's first split (the only one a short sequence has) is dispatched before any
@@ -94,7 +113,8 @@ __device__ __forceinline__ WorkItem work_item(const DecodeArgs& a) {
   }
   const int sh = L % (a.S * a.Hkv);
   const int sp = L / (a.S * a.Hkv);
-  return WorkItem{sh % a.S, sh / a.S, sp, sp * a.chunk, min(sp * a.chunk + a.chunk, a.max_ctx), -1};
+  const int b = split_begin(sp, a.chunk, a.chunk_old, a.n_old);
+  return WorkItem{sh % a.S, sh / a.S, sp, b, min(b + split_length(sp, a.chunk, a.chunk_old, a.n_old), a.max_ctx), -1};
 }
 
 // The fields a bf16 decode workgroup needs before its first K/V load, passed as leading scalar kernel arguments
@@ -106,7 +126,7 @@ struct HotArgs {
   const int32_t* items;  // work list or NULL
   int32_t bt_ss;         // block-table row stride (elements)
   int32_t SH;            // sequences x KV heads
-  int32_t S, chunk, max_ctx, bt_w;
+  int32_t S, chunk, max_ctx, bt_w;  // equal splits of chunk tokens (the host gives the bf16 kernel no two-class grid)
 };
 
 __device__ __forceinline__ WorkItem work_item(const HotArgs& hp, const DecodeArgs& a) {

@@ -19,10 +19,10 @@
 //     reference does (acc += (p s_v) v_int; l keeps the unscaled p). The V tile goes to LDS already converted to
 //     fp16 and is read back transposed. The reference forms P' in fp32 (engine/triton_decode.py:126-130); fp16
 //     has its 11 significant bits but not its exponent range: with small V scales (V absmax under about 0.05)
-//     most P' would fall into fp16 subnormals. Each split therefore takes p' = p 2^e, with 2^e chosen from the
+//     most P' would fall into fp16 subnormals. Each wave therefore takes p' = p 2^e, with 2^e chosen from the
 //     largest V scale of its tokens so that max(s_v) 2^e lies in [2^10, 2^11): P' = p' s_v <= 2^4 2^11 stays
 //     below fp16's 65504, and every term within 2^-29 of the largest stays normal. The factor rides on the exp2's
-//     offset (p' = 2^(x - (m - e))), so l and acc both carry it and the split reports its max as m - e: the merge
+//     offset (p' = 2^(x - (m - e))), so l and acc both carry it and the wave reports its max as m - e: the merges
 //     and the final acc / l are exactly those of p.
 // Lane (r, q4) loads 16-byte pieces 64 j + 16 q4 of K row r (one load instruction covers 64 contiguous bytes of each
 // of 16 rows), so the query operand uses that channel order too: k-slot 8 jj + i of lane group q4 is channel
@@ -55,11 +55,21 @@ struct Int8Tile {
   uint32_t kc[2];       // mode 2: one 32-bit word (2 fp16 channel scales) of the block's D scales per lane
 };
 
-// Per-token scales (K in mode 1, V in every mode) of a whole split live in LDS, loaded in the prologue with one
-// 16-byte load per half block row: a tile then issues only its eight 16-byte code loads. (Per-tile 8-byte scale
-// loads made a third of the load instructions for 1.5% of the bytes, and load issue, not bytes, limited the
-// kernel.) Each block's 16 fp16 scales are 8 words.
+// Per-token scales (K in mode 1, V in every mode) live in LDS, loaded in the prologue with one 16-byte load per half
+// block row: a tile then issues only its eight 16-byte code loads. (Per-tile 8-byte scale loads made a third of the
+// load instructions for 1.5% of the bytes, and load issue, not bytes, limited the kernel.) Each block's 16 fp16
+// scales are 8 words. Two stagings:
+// - per wave (modes 2 and 3, V scales only): each wave stages only the blocks its own tiles cover, in a region of its
+//   own: lane l holds block 2 (wave + 4 (l / 2)) + l % 2 of the split (tile l / 2 of the wave), loaded after the ids
+//   are staged and before the wave's first tile loads, and the wave syncs with itself alone, so it starts on its
+//   first tile when that tile is in. With the workgroup-wide staging below, every wave waited for all of its
+//   workgroup's first tiles (512 workgroups issue 32 MiB at once; the first tile was processed ~8 us into the call):
+//   C4(a) 31.9 -> 30.0 us.
+// - per workgroup (mode 1, K and V scales): thread t loads block t's rows with the block id it fetched itself, before
+//   the ids barrier, and the workgroup waits for all of them (and the first tiles) at one barrier. Per-wave staging
+//   made mode 1 slower (C4(b) 27.8 -> 28.3 us, and 28.7 with a barrier restoring a common start).
 constexpr int kScaleBlocks = kMaxInt8Split / 16;
+constexpr int kWaveScaleBlocks = kScaleBlocks / kWaves;  // blocks of one wave's tiles in a split
 
 // MODE 1: per-token K scales; 2: per-(block, channel) K scales; 3: mode 2 with one channel scale per (head,
 // channel) for every block (a zero block stride), folded into the query once.
@@ -76,9 +86,11 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   // mode 2: each wave's channel scales of two tiles (slot = tile index parity), [wave][slot][block][lane]
   __shared__ __align__(16) uint32_t kcs[(MODE == 2) ? kWaves * 2 * 2 * 64 : 1];
   constexpr int kScaleArrays = (MODE == 1) ? 2 : 1;                              // [V, K] or [V] token scales
+  constexpr bool kWaveScales = MODE != 1;  // the token-scale staging (see kScaleBlocks)
+  // [wave][arr][block of the wave][8] (kWaveScales) or [arr][block of the split][8]
   __shared__ __align__(16) uint32_t tsc[kScaleArrays * kScaleBlocks * 8];
   __shared__ __align__(8) int bids[kMaxInt8Split / 16];  // a split of at most kMaxInt8Split tokens
-  __shared__ uint32_t vmax_bits[kWaves];  // each wave's largest V scale of the split (fp16 bits)
+  __shared__ uint32_t vmax_bits[kWaves];  // per-workgroup staging: each wave's largest V scale (fp16 bits)
   __shared__ int last_flag;
 
   {
@@ -144,27 +156,34 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int ctx = min(ctx_raw, a.max_ctx);  // as context_len()
   const bool past_end = w.nvalid < 0 && start >= ctx;  // grid: a split past this sequence's end
   const int end = max(start, min(wend, ctx));
-  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
+  const int nvalid = w.nvalid < 0 ? splits_holding(ctx, a.chunk, a.chunk_old, a.n_old) : w.nvalid;
   const int n_quant = (ctx >> 4) << 4;  // mode 2: tokens in full (quantized) blocks
   // staging slot of the partial last block, -1 if none (as tail_slot())
   const int tail = (MODE >= 2) ? min(tail_raw, a.n_stage - 1) : -1;
-  // The split's token scales: thread t loads block t's two 16-byte half rows (per array) with the block id it
-  // fetched itself, so the loads need no LDS read; they are issued before the first tiles' loads, so that waiting
-  // for them does not wait for the tiles. Threads past the split read its last block again (not staged).
   const uint16_t* ksh = (const uint16_t*)a.ks + (int64_t)h * a.ks_sh;
   const uint16_t* vsh = (const uint16_t*)a.vs + (int64_t)h * a.vs_sh;
-  const int64_t own_bid = min(max(ids[0], 0), a.nb - 1);
+  // The token scales of one block (two 16-byte half rows per array) into sreg.
   u32x4 sreg[kScaleArrays][2];
+  auto load_scales = [&](int64_t blk) {
 #pragma unroll
-  for (int arr = 0; arr < kScaleArrays; ++arr) {
-    const uint16_t* base = arr ? ksh : vsh;
-    const int64_t sn = arr ? a.ks_sn : a.vs_sn;
+    for (int arr = 0; arr < kScaleArrays; ++arr) {
+      const uint16_t* base = arr ? ksh : vsh;
+      const int64_t sn = arr ? a.ks_sn : a.vs_sn;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) sreg[arr][hf] = *(const u32x4*)(base + own_bid * sn + 8 * hf);
-  }
+      for (int hf = 0; hf < 2; ++hf) sreg[arr][hf] = *(const u32x4*)(base + blk * sn + 8 * hf);
+    }
+  };
+  // Per-workgroup staging: thread t's block t, with the id it fetched (threads past the split read its last block
+  // again, not staged).
+  if (!kWaveScales) load_scales(min(max(ids[0], 0), a.nb - 1));
   commit_split_ids_flat(ids, bids, a.nb);
   __syncthreads();
   if (past_end) return;
+  const int nblk = (end - start + 15) >> 4;  // blocks of this split, <= kMaxInt8Split / 16
+  // The block whose scales this thread stages: per wave, lane l's block of the wave's tiles (lanes past the split
+  // read its last block again, never used), issued before the wave's first tile loads; per workgroup, block t.
+  const int my_bi = kWaveScales ? 2 * (wave + kWaves * (lane >> 1)) + (lane & 1) : (int)threadIdx.x;
+  if (kWaveScales) load_scales(bids[min(my_bi, nblk - 1)]);
 
   constexpr bool kconst = MODE == 3;  // one channel scale per (head, channel) for every block
   // qh: the query in fp16 (modes 1, 2), or the high part of Q' = q * s (mode 3) with ql its low part,
@@ -176,7 +195,7 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   f16x8 qh[KS], ql[KS];
   int qshift = 0;
   float sl2 = a.scale_log2;
-  float vshift = 0.f;  // p' = p 2^vshift (set once the split's V scales are in)
+  float vshift = 0.f;  // p' = p 2^vshift (set once the wave's V scales are in)
   auto convert_query = [&]() {
     float qf[KS][8];
     float qmax = 0.f;
@@ -218,7 +237,6 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   const int mine = ntile > wave ? (ntile - wave + kWaves - 1) / kWaves : 0;
   auto tile_t0 = [&](int k) { return start + 32 * (wave + kWaves * k); };
 
-  const int nblk = (end - start + 15) >> 4;  // blocks of this split, <= kScaleBlocks
   auto load_tile = [&](int k, Int8Tile<D>& tl) {
     const int t0 = tile_t0(k);
     const int bi = (t0 - start) >> 4;
@@ -243,10 +261,43 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
       for (int i = 0; i < VC; ++i) tl.v[mt][i] = __builtin_nontemporal_load((const u32x4*)(vb + 16 * (lane + 64 * i)));
     }
   };
-  // Token scales of tokens 4 q4 .. 4 q4 + 3 of the tile's block mt (a second block past the end reads the last).
+  // Token scales of tokens 4 q4 .. 4 q4 + 3 of the tile's block mt. Per wave: tile t0 is the wave's tile
+  // k = ((t0 - start) / 32 - wave) / kWaves, whose blocks lanes 2 k, 2 k + 1 staged; per workgroup: the split's
+  // block (t0 - start) / 16 + mt. A second block past the end holds the split's last block: its tokens are masked.
+  uint32_t* const tsw = tsc + (kWaveScales ? wave * kScaleArrays * kWaveScaleBlocks * 8 : 0);
+  constexpr int kRegionBlocks = kWaveScales ? kWaveScaleBlocks : kScaleBlocks;
   auto token_scales = [&](int arr, int t0, int mt) {
-    const int bl = min(((t0 - start) >> 4) + mt, nblk - 1);
-    return *(const uint2*)(tsc + (arr * kScaleBlocks + bl) * 8 + 2 * q4);
+    const int bl = kWaveScales ? 2 * ((((t0 - start) >> 5) - wave) >> 2) + mt : min(((t0 - start) >> 4) + mt, nblk - 1);
+    return *(const uint2*)(tsw + (arr * kRegionBlocks + bl) * 8 + 2 * q4);
+  };
+  // p' = p 2^vshift: 2^vshift brings the largest V scale of the wave's tokens (per wave) or of the split's (per
+  // workgroup) into [2^10, 2^11), or 1 when every scale is 0. Scales are non-negative fp16, whose bit patterns
+  // order like their values.
+  auto shift_of = [](uint32_t mb) {
+    const float vm = h2f(mb);
+    return vm > 0.f ? (float)(10 - ((int)((__float_as_uint(vm) >> 23) & 0xff) - 127)) : 0.f;
+  };
+  // This thread's block's scales into LDS and the wave's largest V scale among them. Per wave it is called where the
+  // compiler can count the loads issued after the scale loads (inside each branch), so that the wait is exact.
+  auto stage_scales = [&]() {
+#pragma unroll
+    for (int arr = 0; arr < kScaleArrays; ++arr)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        *(u32x4*)(tsw + (arr * kRegionBlocks + (kWaveScales ? lane : (int)threadIdx.x)) * 8 + 4 * hf) = sreg[arr][hf];
+    const int nv = min(max(end - (start + 16 * my_bi), 0), 16);  // tokens of this thread's block in the split
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t b = (sreg[0][j >> 3][(j >> 1) & 3] >> (16 * (j & 1))) & 0xffffu;
+      if (j < nv) mb = max(mb, b);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
+    if (kWaveScales)
+      vshift = shift_of(mb);
+    else if (lane == 0)
+      vmax_bits[wave] = mb;
   };
 
   float m_run = kNegInf, l_run = 0.f;
@@ -382,35 +433,21 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
   if (piped) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) load_tile(j, ring[j]);
+    convert_query();
+    if (kWaveScales) stage_scales();
+  } else {
+    convert_query();
+    if (kWaveScales) stage_scales();
   }
-  convert_query();
-#pragma unroll
-  for (int arr = 0; arr < kScaleArrays; ++arr)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-      *(u32x4*)(tsc + (arr * kScaleBlocks + threadIdx.x) * 8 + 4 * hf) = sreg[arr][hf];
-  {
-    // The largest V scale of the split's tokens [start, end): thread t holds block t's 16 scales. Scales are
-    // non-negative fp16, whose bit patterns order like their values.
-    const int nv = min(max(end - (start + 16 * (int)threadIdx.x), 0), 16);
-    uint32_t mb = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint32_t b = (sreg[0][j >> 3][(j >> 1) & 3] >> (16 * (j & 1))) & 0xffffu;
-      if (j < nv) mb = max(mb, b);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
-    if (lane == 0) vmax_bits[wave] = mb;
-  }
-  __syncthreads();  // token scales staged
-  // p' = p 2^vshift: 2^vshift brings the split's largest V scale into [2^10, 2^11) (0 when every scale is 0).
-  {
+  if (kWaveScales) {
+    wave_sync();  // the wave's token scales are in its LDS region
+  } else {
+    stage_scales();
+    __syncthreads();  // the split's token scales are staged
     uint32_t mb = 0;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) mb = max(mb, vmax_bits[i]);
-    const float vm = h2f(mb);
-    if (vm > 0.f) vshift = (float)(10 - ((int)((__float_as_uint(vm) >> 23) & 0xff) - 127));
+    vshift = shift_of(mb);
   }
   if (piped) {
     // Tile k is in ring[k % NB]; after tile k, tile k + 1's channel scales (mode 2) go to LDS slot (k + 1) & 1.

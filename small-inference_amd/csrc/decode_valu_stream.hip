@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu_stream(const DecodeArgs 
   const int ctx = context_len(a, s);
   if (w.nvalid < 0 && start >= ctx) return;  // grid: a split past this sequence's end
   const int end = max(start, min(w.end, ctx));
-  const int nvalid = w.nvalid < 0 ? (ctx + a.chunk - 1) / a.chunk : w.nvalid;
+  const int nvalid = w.nvalid < 0 ? splits_holding(ctx, a.chunk, a.chunk_old, a.n_old) : w.nvalid;
   commit_split_ids(nb_spec, ids, bids, a.nb);
   __syncthreads();  // block ids staged
 

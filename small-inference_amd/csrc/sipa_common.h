@@ -90,6 +90,7 @@ struct DecodeArgs {
   float* pl;          // [S, Hq, splits] split softmax denominators
   int32_t* counters;  // [S, Hkv] splits finished, for the last-arriving merge
   int32_t S, Hq, Hkv, G, B, splits, chunk;
+  int32_t chunk_old, n_old;  // the first n_old splits hold chunk_old tokens each, the rest chunk (n_old 0: uniform)
   int32_t max_ctx;    // every block-table row covers ceil(max_ctx / B) blocks; context lengths are clamped to it
   int32_t nb;         // blocks in the pool: block ids are clamped to [0, nb)
   int32_t bt_w;       // entries per block-table row (>= ceil(max_ctx / B)): table columns are clamped below it

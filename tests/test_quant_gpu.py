@@ -632,3 +632,27 @@ def test_c4_quantize_store_of_64_new_tokens_is_exact(fmt):
             slot = cache._stage_of[b]
             assert torch.equal(stage[:, slot, :o + 1], rows.transpose(0, 1)), s
     assert done == sum(1 for n in before if n % B == B - 1) >= S // 4
+
+
+def test_kchannel_two_class_split_grid_with_ragged_lengths():
+    """Format B on a grid of exactly two workgroups per CU (64 sequences x 2 KV heads x 4 splits on 256 CUs) takes
+    splits of two lengths: the first CU-count workgroups (the earlier-dispatched of each CU's pair) get the longer
+    ones. Sequences whose contexts end inside the long splits, at their boundaries and inside the short ones all
+    match the oracle's dequantize-then-attend, through the fused merge and the separate combine kernel."""
+    from engine.hip_decode import device_cu_count
+
+    cu = device_cu_count()
+    if cu % 128:
+        pytest.skip(f"{cu} CUs: 128 (sequence, KV head) pairs do not divide the CU count")
+    Hq, Hkv, D = HEADS["1.5B"]
+    g = torch.Generator().manual_seed(41)
+    lengths = torch.randint(1, 4097, (64,), generator=g).tolist()
+    lengths[:8] = [4096, 1, 1280, 1281, 2560, 2561, 3000, 17]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, "int8-kchannel", seed=42)
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    for combine in ("fused", "kernel"):
+        print(f"case kchannel two-class grid, 64 ragged sequences, {combine}", flush=True)
+        out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                     4096, num_splits=2 * cu // 128, quant=quant, impl="mfma", combine=combine)
+        assert_decode_close(out.double().cpu().numpy(), ref, f"kchannel two-class grid {combine}")
