@@ -74,6 +74,8 @@ class Decode:
         self.v_ptrs = [v[i].data_ptr() for i in range(self.layers)]
         self.out_ptr = self.out.data_ptr()
         self.meta = dict(meta or {}, splits=self.plan.splits, chunk=self.plan.chunk, impl=impl, combine=combine)
+        if self.plan.n_old:
+            self.meta.update(longer_splits=self.plan.n_old, longer_split_tokens=self.plan.chunk_old)
         if self.plan.items is not None:
             self.meta.update(work_items=int(self.plan.items.shape[0]), combine="fused")
 
@@ -467,37 +469,49 @@ def prefill_bench(steps: int, warmup: int) -> dict:
 
 def paged_read_floor(wl, steps: int, warmup: int) -> dict:
     """The same call's HBM reads without the decode arithmetic or the split merge (csrc/probe.hip
-    sipa_probe_paged_read: same grid, block-table staging, two 32-token tiles in flight per wave, and the INT8
-    kernels' token-scale reads): the floor a decode kernel of this layout reaches on this access pattern."""
+    sipa_probe_paged_read: the same grid or work list, block-table staging, two 32-token tiles in flight per wave,
+    and the INT8 kernels' scale reads: per-token rows, or format B's per-channel K rows and per-token V rows): the
+    floor a decode kernel of this layout reaches on this access pattern."""
     lib = ctypes.CDLL(str(ROOT / "small-inference_amd" / "build" / "libsmallinf_probe.so"))
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
-    lib.sipa_probe_paged_read.argtypes = [vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, i64, i64, i64, i64, i32, vp,
-                                          vp]
+    lib.sipa_probe_paged_read.argtypes = [vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32, i32, vp, i32, i64, i64,
+                                          i64, i64, i32, i64, i64, i32, i32, vp, vp]
     lib.sipa_probe_paged_read.restype = i32
     sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     k0, esz = wl.k[0], wl.k.element_size()
     Hkv, N, B, D = k0.shape
     ctx = max(wl.lengths)
-    assert min(wl.lengths) == ctx, "the floor probe takes a uniform batch"
-    sc = None if wl.quant is None or wl.quant[0].mode != 1 else wl.quant  # per-token scales (format "int8")
+    plan = wl.plan
+    items = plan.items
+    if items is None:
+        assert min(wl.lengths) == ctx, "the grid floor takes a uniform batch"
+    mode = 0 if wl.quant is None else wl.quant[0].mode
 
     def call(i):
         layer = i % wl.layers
         ks = vs = None
-        if sc is not None:
-            ks, vs = sc[layer].k_scale.data_ptr(), sc[layer].v_scale.data_ptr()
+        ks_sh = ks_sn = vs_sh = vs_sn = ks_row = vs_row = 0
+        if mode:
+            q = wl.quant[layer]
+            ks, vs = q.k_scale.data_ptr(), q.v_scale.data_ptr()
+            vs_sh, vs_sn, vs_row = q.v_scale.stride(0) * 2, q.v_scale.stride(1) * 2, B * 2
+            ks_sh, ks_sn = q.k_scale.stride(0) * q.k_scale.element_size(), q.k_scale.stride(1) * q.k_scale.element_size()
+            ks_row = (B if mode == 1 else D) * q.k_scale.element_size()
         rc = lib.sipa_probe_paged_read(wl.k[layer].data_ptr(), wl.v[layer].data_ptr(), ks, vs, wl.bt.data_ptr(),
-                                       wl.bt.stride(0), len(wl.lengths), Hkv, ctx, wl.plan.chunk,
-                                       k0.stride(0) * esz, k0.stride(1) * esz, N * B * 2, B * 2, D * esz,
+                                       wl.bt.stride(0), len(wl.lengths), Hkv, ctx, plan.chunk or 0, plan.chunk_old,
+                                       plan.n_old, None if items is None else items.data_ptr(),
+                                       0 if items is None else items.shape[0], k0.stride(0) * esz,
+                                       k0.stride(1) * esz, ks_sh, ks_sn, ks_row, vs_sh, vs_sn, vs_row, D * esz,
                                        sink.data_ptr(), stream)
         if rc:
             raise RuntimeError(f"sipa_probe_paged_read: {rc}")
 
     ms, _ = time_calls(call, steps, warmup, per_launch=False)
     r = {"us_per_call": round(ms * 1e3, 2), "gb_s": round(wl.bytes / (ms * 1e-3) / 1e9, 1),
-         "frac_of_peak": round(wl.bytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "splits": wl.plan.splits,
-         "token_scales": sc is not None}
+         "frac_of_peak": round(wl.bytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "splits": plan.splits,
+         "scales": ["none", "per token", "per channel K, per token V"][mode],
+         "grid": "work list" if items is not None else ("two-length splits" if plan.n_old else "equal splits")}
     log(f"[bench] {wl.name} paged-read floor: {json.dumps(r)}")
     return r
 
@@ -561,6 +575,7 @@ def details(steps: int, warmup: int) -> dict:
         out[key]["max_abs_vs_oracle_first32"] = round(check_against_oracle(c3), 5)
         if wlist == "auto":
             out[key].update(cpu_path(c3))
+            out[key]["paged_read_floor"] = paged_read_floor(c3, steps, warmup)
         del c3
         torch.cuda.empty_cache()
     torch.cuda.empty_cache()
@@ -571,7 +586,6 @@ def details(steps: int, warmup: int) -> dict:
         out[key] = measure(wl, steps, warmup)
         if not f32s:
             out[key].update(cpu_path(wl))
-        if fmt == "int8":
             out[key]["paged_read_floor"] = paged_read_floor(wl, steps, warmup)
         del wl
         torch.cuda.empty_cache()
@@ -826,7 +840,7 @@ def main() -> int:
                 continue  # the VALU streaming kernels cover the per-token format only
             wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl, splits=args.splits)
             res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
-            if fmt == "int8":
+            if args.impl in ("auto", "mfma"):
                 res[key]["paged_read_floor"] = paged_read_floor(wl, args.steps, args.warmup)
             del wl
             torch.cuda.empty_cache()

@@ -161,6 +161,15 @@ int32_t sipa_choose_splits_for(int32_t num_seqs, int32_t num_kv_heads, int32_t m
  * of 64 tokens, at most 32768. Calls launch ceil(max_context / chunk) splits, which may be fewer than asked. */
 int32_t sipa_split_chunk(int32_t max_context, int32_t num_splits);
 
+/* The split grid sipa_decode launches for a call of these sizes without a work list, on the MFMA kernels (bf16
+ * query, 16-token blocks, head_dim 64 / 128): returns the number of splits per sequence and writes the token counts
+ * of its splits: the first *n_old splits hold *chunk_old tokens, the others *chunk (*n_old 0: all *chunk). INT8
+ * per-channel-K pools on a grid of exactly two workgroups per CU take two lengths (the earlier-dispatched workgroup
+ * of each CU's pair streams faster and gets the longer split). Replaces the chunk computation of the reference's
+ * wrapper (engine/triton_decode.py:203-204). Negative SIPA_E* on bad arguments. */
+int32_t sipa_decode_split_grid(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context, int32_t num_splits,
+                               int32_t kv_mode, int32_t* chunk, int32_t* chunk_old, int32_t* n_old);
+
 /* Workspace bytes sipa_decode needs for these sizes (0 when num_splits resolves to 1). */
 int64_t sipa_decode_workspace_bytes(int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                                     int32_t head_dim, int32_t num_splits);

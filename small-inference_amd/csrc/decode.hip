@@ -657,6 +657,23 @@ static int resolve_splits(int S, int Hkv, int max_ctx, int requested, bool int8,
   return ceil_div(max_ctx, *chunk);  // no split that is empty for every sequence
 }
 
+extern "C" int32_t sipa_decode_split_grid(int32_t num_seqs, int32_t num_kv_heads, int32_t max_context,
+                                          int32_t num_splits, int32_t kv_mode, int32_t* chunk, int32_t* chunk_old,
+                                          int32_t* n_old) {
+  SIPA_CHECK(num_seqs > 0 && num_kv_heads > 0 && max_context > 0 && kv_mode >= 0 && kv_mode <= 2 && chunk &&
+                 chunk_old && n_old,
+             SIPA_EINVAL, "split grid: bad arguments");
+  int c = 0, co = 0, no = 0;
+  const int splits = resolve_splits(num_seqs, num_kv_heads, max_context, num_splits, kv_mode != SIPA_KV_PLAIN, &c);
+  if (splits > 1 && kv_mode == SIPA_KV_INT8_KCHAN)
+    two_class_splits((int64_t)num_seqs * num_kv_heads, max_context, splits, sipa_device_cu_count(-1), kMaxInt8Split,
+                     &c, &co, &no);
+  *chunk = c;
+  *chunk_old = co;
+  *n_old = no;
+  return splits;
+}
+
 extern "C" int32_t sipa_build_work_list(const int32_t* ctx, int32_t S, int32_t Hkv, int32_t cu_count,
                                         int32_t items_per_cu, int32_t max_piece, int32_t* items, int32_t capacity,
                                         int32_t* max_splits) {

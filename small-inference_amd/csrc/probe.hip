@@ -71,44 +71,64 @@ extern "C" int32_t sipa_probe_copy(void* dst, const void* src, int64_t bytes, in
 }
 
 // sipa_probe_paged_read: the HBM reads of one paged-decode call and nothing else, the floor a decode kernel of this
-// layout can reach. Workgroup (sequence s, KV head h, split sp) of a (S, Hkv, splits) grid, 4 waves, stages the
-// split's block ids in LDS, then each wave streams its 32-token tiles (blocks 2t, 2t + 1 of the split) of K and V,
-// row_bytes per token row, 16-byte nontemporal loads, two tiles in flight, like the decode kernels. With token-scale
-// pools (ks, vs: row_bytes 0 when absent), the split's 32-byte scale rows of every block are read first, as the INT8
-// kernel stages them. The data is folded into a word that is never stored in practice, so the loads stay live.
+// layout can reach. Workgroup L takes the token range the decode kernels give it: item L of a work list (items, 8
+// int32 each: sequence, KV head, split, splits, start, end), or split sp = L / (S Hkv) of pair L % (S Hkv) on the
+// grid, the first n_old splits chunk_old tokens long and the others chunk (every sequence has ctx tokens). 4 waves
+// stage the range's block ids in LDS, then each wave streams its 32-token tiles (blocks 2t, 2t + 1 of the range) of
+// K and V, row_bytes per token row, 16-byte nontemporal loads, two tiles in flight, like the decode kernels. With
+// scale pools (ks and/or vs non-NULL), the range's scale rows of every block are read first (ks_row / vs_row bytes
+// each: 32 for per-token scales, D x 2 for per-channel K scales). The data is folded into a word that is never
+// stored in practice, so the loads stay live.
 namespace {
 constexpr int kProbeWaves = 4;
 constexpr int kProbeMaxBlocks = 2048;
 
-__global__ void __launch_bounds__(256) probe_paged_read_kernel(const uint8_t* __restrict__ k,
-                                                                const uint8_t* __restrict__ v,
-                                                                const uint8_t* __restrict__ ks,
-                                                                const uint8_t* __restrict__ vs,
-                                                                const int32_t* __restrict__ bt, int64_t bt_ss, int S,
-                                                                int Hkv, int chunk, int ctx, int64_t kv_sh,
-                                                                int64_t kv_sn, int64_t sc_sh, int64_t sc_sn,
-                                                                int row_bytes, uint32_t zero,
-                                                                uint32_t* __restrict__ sink) {
+struct ProbeArgs {
+  const uint8_t* k;
+  const uint8_t* v;
+  const uint8_t* ks;
+  const uint8_t* vs;
+  const int32_t* bt;
+  const int32_t* items;
+  int64_t bt_ss, kv_sh, kv_sn, ks_sh, ks_sn, vs_sh, vs_sn;
+  int32_t S, Hkv, ctx, chunk, chunk_old, n_old, row_bytes, ks_row, vs_row;
+  uint32_t zero;
+  uint32_t* sink;
+};
+
+__global__ void __launch_bounds__(256) probe_paged_read_kernel(const ProbeArgs a) {
   __shared__ int bids[kProbeMaxBlocks];
   __shared__ u32x4 stage[kProbeWaves * 8 * 64];
   const int L = blockIdx.x;
-  const int s = L % S, h = (L / S) % Hkv, sp = L / (S * Hkv);
-  const int start = sp * chunk, end = min(start + chunk, ctx);
-  const int nblk = (end - start + 15) >> 4;
-  for (int j = threadIdx.x; j < nblk; j += 256) bids[j] = bt[(int64_t)s * bt_ss + (start >> 4) + j];
+  int s, h, start, end;
+  if (a.items != nullptr) {
+    const int32_t* it = a.items + 8 * (int64_t)L;
+    s = it[0], h = it[1], start = it[4], end = min(it[5], start + kProbeMaxBlocks * 16);
+  } else {
+    s = L % a.S, h = (L / a.S) % a.Hkv;
+    const int sp = L / (a.S * a.Hkv);
+    start = sp <= a.n_old ? sp * a.chunk_old : a.n_old * a.chunk_old + (sp - a.n_old) * a.chunk;
+    end = min(start + (sp < a.n_old ? a.chunk_old : a.chunk), a.ctx);
+  }
+  const int nblk = max((end - start + 15) >> 4, 0);
+  for (int j = threadIdx.x; j < nblk; j += 256) bids[j] = a.bt[(int64_t)s * a.bt_ss + (start >> 4) + j];
   __syncthreads();
   uint32_t acc = 0;
-  if (ks != nullptr) {  // the split's token scales: 16-byte loads, half a block's 32-byte row each
-    for (int c = threadIdx.x; c < 2 * nblk; c += 256) {
-      const int64_t off = (int64_t)h * sc_sh + (int64_t)bids[c >> 1] * sc_sn + 16 * (c & 1);
-      const u32x4 a = *(const u32x4*)(ks + off), b = *(const u32x4*)(vs + off);
-      acc ^= a.x ^ b.w;
+  // the range's scale rows, 16 bytes a lane
+  for (int arr = 0; arr < 2; ++arr) {
+    const uint8_t* base = arr ? a.vs : a.ks;
+    if (base == nullptr) continue;
+    const int per = (arr ? a.vs_row : a.ks_row) >> 4;
+    const int64_t sh = arr ? a.vs_sh : a.ks_sh, sn = arr ? a.vs_sn : a.ks_sn;
+    for (int c = threadIdx.x; c < per * nblk; c += 256) {
+      const u32x4 x = *(const u32x4*)(base + (int64_t)h * sh + (int64_t)bids[c / per] * sn + 16 * (c % per));
+      acc ^= x.x ^ x.w;
     }
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int ntile = (nblk + 1) >> 1;
   const int mine = ntile > wave ? (ntile - wave + kProbeWaves - 1) / kProbeWaves : 0;  // tiles wave, wave + 4, ...
-  const int per_lane = 16 * row_bytes / (64 * 16);  // 16-byte loads per lane per block: 2 (2 KiB) or 1 (1 KiB)
+  const int per_lane = 16 * a.row_bytes / (64 * 16);  // 16-byte loads per lane per block: 2 (2 KiB) or 1 (1 KiB)
   // One tile: blocks 2t, 2t + 1 of K and V, two 16-byte loads per lane and block (a 1 KiB block reads its first
   // kilobyte twice); branch-free. Each ring slot folds into its own word, and a slot's refill address takes that
   // word (& zero, 0 at run time), and a wave-scope fence separates the refill from the other slot's fold: the
@@ -117,12 +137,12 @@ __global__ void __launch_bounds__(256) probe_paged_read_kernel(const uint8_t* __
     const int t = wave + kProbeWaves * kk;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      const int64_t base = (int64_t)h * kv_sh + (int64_t)bids[min(2 * t + mt, nblk - 1)] * kv_sn + (dep & zero);
+      const int64_t base = (int64_t)h * a.kv_sh + (int64_t)bids[min(2 * t + mt, nblk - 1)] * a.kv_sn + (dep & a.zero);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int64_t o = base + 16 * (lane + 64 * (i < per_lane ? i : 0));
-        r[4 * mt + 2 * i] = __builtin_nontemporal_load((const u32x4*)(k + o));
-        r[4 * mt + 2 * i + 1] = __builtin_nontemporal_load((const u32x4*)(v + o));
+        r[4 * mt + 2 * i] = __builtin_nontemporal_load((const u32x4*)(a.k + o));
+        r[4 * mt + 2 * i + 1] = __builtin_nontemporal_load((const u32x4*)(a.v + o));
       }
     }
   };
@@ -167,24 +187,43 @@ __global__ void __launch_bounds__(256) probe_paged_read_kernel(const uint8_t* __
   }
   order();
   acc ^= a0 ^ a1 ^ stage[(wave * 8 + (lane & 7)) * 64 + lane].y;
-  if (acc == 0x9e3779b9u) sink[L] = acc;
+  if (acc == 0x9e3779b9u) a.sink[L] = acc;
 }
 }  // namespace
 
-// k, v: pools (row_bytes per token row, 16-token blocks, kv_sh / kv_sn in bytes); bt: [S, >= ceil(ctx / 16)] block
-// ids with row stride bt_ss; every sequence has ctx tokens, cut into splits of `chunk` (a multiple of 32). ks, vs:
-// optional token-scale pools (32-byte rows per block, strides in bytes) or NULL. Returns 0, or -1 on bad arguments.
+// k, v: pools (row_bytes per token row, 16-token blocks, kv_sh / kv_sn in bytes); bt: [S, ...] block ids with row
+// stride bt_ss. Grid (items NULL): every sequence has ctx tokens, split as above (chunk, chunk_old multiples of 32;
+// n_old 0 for equal splits). Work list (items non-NULL, n_items entries): each item's range as given. ks, vs: scale
+// pools or NULL (rows of ks_row / vs_row bytes, multiples of 16; strides in bytes). Returns 0, or -1 on bad
+// arguments.
 extern "C" int32_t sipa_probe_paged_read(const void* k, const void* v, const void* ks, const void* vs,
                                          const int32_t* bt, int64_t bt_ss, int32_t S, int32_t Hkv, int32_t ctx,
-                                         int32_t chunk, int64_t kv_sh, int64_t kv_sn, int64_t sc_sh, int64_t sc_sn,
+                                         int32_t chunk, int32_t chunk_old, int32_t n_old, const int32_t* items,
+                                         int32_t n_items, int64_t kv_sh, int64_t kv_sn, int64_t ks_sh, int64_t ks_sn,
+                                         int32_t ks_row, int64_t vs_sh, int64_t vs_sn, int32_t vs_row,
                                          int32_t row_bytes, void* sink, void* stream) {
-  if (!k || !v || !bt || !sink || S <= 0 || Hkv <= 0 || ctx <= 0 || chunk <= 0 || chunk % 32) return -1;
-  if (chunk / 16 > kProbeMaxBlocks || (row_bytes != 64 && row_bytes != 128) || ((uintptr_t)k & 15) ||
-      ((uintptr_t)v & 15) || kv_sh % 16 || kv_sn % 16 || (ks && (!vs || sc_sh % 16 || sc_sn % 16)))
+  if (!k || !v || !bt || !sink || S <= 0 || Hkv <= 0) return -1;
+  if ((row_bytes != 64 && row_bytes != 128) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) || kv_sh % 16 ||
+      kv_sn % 16)
     return -1;
-  const int splits = (ctx + chunk - 1) / chunk;
-  hipLaunchKernelGGL(probe_paged_read_kernel, dim3(S * Hkv * splits), dim3(256), 0, (hipStream_t)stream,
-                     (const uint8_t*)k, (const uint8_t*)v, (const uint8_t*)ks, (const uint8_t*)vs, bt, bt_ss, S, Hkv,
-                     chunk, ctx, kv_sh, kv_sn, sc_sh, sc_sn, row_bytes, 0u, (uint32_t*)sink);
+  if ((ks && (ks_row <= 0 || ks_row % 16 || ks_sh % 16 || ks_sn % 16)) ||
+      (vs && (vs_row <= 0 || vs_row % 16 || vs_sh % 16 || vs_sn % 16)))
+    return -1;
+  int64_t wgs;
+  if (items) {
+    if (n_items <= 0) return -1;
+    wgs = n_items;
+  } else {
+    if (ctx <= 0 || chunk <= 0 || chunk % 32 || chunk / 16 > kProbeMaxBlocks || n_old < 0 ||
+        (n_old > 0 && (chunk_old <= 0 || chunk_old % 32 || chunk_old / 16 > kProbeMaxBlocks)))
+      return -1;
+    const int64_t covered = (int64_t)n_old * chunk_old;
+    const int64_t splits = covered >= ctx ? (ctx + chunk_old - 1) / chunk_old : n_old + (ctx - covered + chunk - 1) / chunk;
+    wgs = (int64_t)S * Hkv * splits;
+  }
+  ProbeArgs a{(const uint8_t*)k, (const uint8_t*)v, (const uint8_t*)ks, (const uint8_t*)vs, bt, items, bt_ss, kv_sh,
+              kv_sn, ks_sh, ks_sn, vs_sh, vs_sn, S, Hkv, ctx, chunk, chunk_old, n_old, row_bytes, ks_row, vs_row, 0u,
+              (uint32_t*)sink};
+  hipLaunchKernelGGL(probe_paged_read_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -91,6 +91,7 @@ SIGNATURES = {
     "sipa_choose_splits_for": (i32, [i32, i32, i32, i32, i32]),
     "sipa_split_chunk": (i32, [i32, i32]),
     "sipa_decode_workspace_bytes": (i64, [i32, i32, i32, i32, i32]),
+    "sipa_decode_split_grid": (i32, [i32, i32, i32, i32, i32, vp, vp, vp]),
     "sipa_decode": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_decode_noalloc": (i32, [_c.POINTER(DecodeParams), vp]),
     "sipa_decode_noalloc_reset": (i32, [vp]),

@@ -114,6 +114,17 @@ def split_plan(max_context: int, num_splits: int) -> tuple[int, int]:
     return math.ceil(max_context / chunk), chunk
 
 
+def split_grid(num_seqs: int, num_kv_heads: int, max_context: int, num_splits: int, kv_mode: int = 0):
+    """(splits, chunk, chunk_old, n_old): the split grid a call launches on the MFMA kernels without a work list:
+    the first n_old splits of every sequence hold chunk_old tokens, the others chunk (sipa_decode_split_grid)."""
+    c, co, no = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_int32(0)
+    n = _hip.lib().sipa_decode_split_grid(num_seqs, num_kv_heads, max_context, num_splits, kv_mode, ctypes.byref(c),
+                                          ctypes.byref(co), ctypes.byref(no))
+    if n < 0:
+        _hip.check(n, "split grid")
+    return int(n), int(c.value), int(co.value), int(no.value)
+
+
 # Workspace (split partials + merge counters) per (device, stream): zero-filled once, the kernels leave the
 # counters zero again, so later calls on the same stream reuse it without a memset.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
@@ -199,6 +210,7 @@ class DecodePlan:
             raise ValueError("work_list='on' needs host_context_lens")
         self.items = None
         self.workspace = None
+        self.chunk_old = self.n_old = 0  # the split grid's longer splits (see split_grid)
         if use_list:
             if len(host_context_lens) != S or max(host_context_lens, default=0) > max_context:
                 raise ValueError("host_context_lens must hold S lengths, none above max_context")
@@ -216,6 +228,10 @@ class DecodePlan:
             if quant is not None:
                 self.requested = max(self.requested, math.ceil(max_context / INT8_MAX_SPLIT))
             self.splits, self.chunk = split_plan(max_context, self.requested)
+            if S > 0:
+                _, chunk, self.chunk_old, self.n_old = split_grid(S, Hkv, max_context, self.requested, self.quant_mode)
+                if self.n_old:
+                    self.chunk = chunk
 
         p = self.params = _hip.DecodeParams()
         p.struct_size = ctypes.sizeof(_hip.DecodeParams)

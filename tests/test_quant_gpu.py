@@ -651,6 +651,13 @@ def test_kchannel_two_class_split_grid_with_ragged_lengths():
     q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, "int8-kchannel", seed=42)
     ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
                     for s in range(len(lengths))])
+    from engine.hip_decode import split_grid
+
+    splits, chunk, chunk_old, n_old = split_grid(64, Hkv, 4096, 2 * cu // 128, 2)
+    print(f"grid: {splits} splits, {n_old} of {chunk_old} tokens, the rest {chunk}", flush=True)
+    assert splits == 2 * cu // 128 and n_old == cu // 128 and chunk_old > chunk and chunk_old % 128 == 0
+    assert n_old * chunk_old + (splits - n_old) * chunk >= 4096
+    assert split_grid(64, Hkv, 4096, 2 * cu // 128, 1)[3] == 0  # the per-token format keeps equal splits
     for combine in ("fused", "kernel"):
         print(f"case kchannel two-class grid, 64 ragged sequences, {combine}", flush=True)
         out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
