@@ -91,11 +91,14 @@ class Decode:
 # clocks, and a few calls do not raise them again (one 512-token prefill chunk at 8K context took 34.6-35.5 µs a
 # call timed after 1 s idle, 33.1 after 10 warm-up calls, 30.9 after 0.5 s of calls).
 WARM_S = 0.3
+LAST_WARM_CALLS = 0  # calls time_calls made before its last timed region began
 
 
 def time_calls(fn, steps: int, warmup: int, per_launch: bool, warm_s: float = WARM_S):
     """(ms per call over a back-to-back region, mean µs per call from event pairs around each call or None).
-    Warm-up: `warmup` calls, then more until `warm_s` seconds of calls have run."""
+    Warm-up: `warmup` calls, then more until `warm_s` seconds of calls have run; their count is left in
+    LAST_WARM_CALLS."""
+    global LAST_WARM_CALLS
     t0, i = time.perf_counter(), 0
     while i < warmup or time.perf_counter() - t0 < warm_s:
         fn(i)
@@ -103,6 +106,7 @@ def time_calls(fn, steps: int, warmup: int, per_launch: bool, warm_s: float = WA
         if i % 32 == 0:
             torch.cuda.synchronize()  # the host stays within 32 calls of the GPU
     torch.cuda.synchronize()
+    LAST_WARM_CALLS = i
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
@@ -545,9 +549,15 @@ def stream_ceiling(steps: int) -> dict:
     return best
 
 
-def details(steps: int, warmup: int) -> dict:
+def c3_context_lengths() -> list[int]:
+    """C3's 256 ragged context lengths: seeded log-normal around 600 tokens, clipped to [16, 8192]."""
     import numpy as np
 
+    rng = np.random.default_rng(0)
+    return np.clip(np.rint(rng.lognormal(math.log(600), 1.0, 256)), 16, 8192).astype(int).tolist()
+
+
+def details(steps: int, warmup: int) -> dict:
     out = {}
     c2 = bf16_decode("c2_single_pass", [8192] * 32, 32768, splits=1)
     out["c2_single_pass"] = measure(c2, steps, warmup)
@@ -566,8 +576,7 @@ def details(steps: int, warmup: int) -> dict:
     out["c1_1x1024"] = measure(c1, steps, warmup)
     out["c1_1x1024"]["max_abs_vs_oracle"] = round(check_against_oracle(c1), 5)
     out["c1_1x1024"].update(cpu_path(c1))
-    rng = np.random.default_rng(0)
-    c3_lengths = np.clip(np.rint(rng.lognormal(math.log(600), 1.0, 256)), 16, 8192).astype(int).tolist()
+    c3_lengths = c3_context_lengths()
     for key, wlist in (("c3_ragged256", "auto"), ("c3_ragged256_split_grid", "off")):
         c3 = bf16_decode(key, c3_lengths, 200_000, layers=4, work_list=wlist)
         out[key] = measure(c3, steps, warmup)
@@ -809,6 +818,8 @@ def main() -> int:
                     "model at batch 512 through the paged cache) and print its JSON")
     ap.add_argument("--c4", action="store_true", help="only run config C4 (INT8 decode, 1.5B shape, 64 x 4096: "
                     "per-token, then per-channel K) for --steps calls each and print its JSON")
+    ap.add_argument("--c3", action="store_true", help="only run config C3 (bf16 decode of 256 ragged sequences "
+                    "on the work list) for --steps calls and print its JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the probe library's plain copy kernel over MIB MiB, 10 times (the reference "
                          "point for rocprof's FETCH_SIZE / WRITE_SIZE counters), and print its byte count")
@@ -846,6 +857,15 @@ def main() -> int:
             torch.cuda.empty_cache()
         print(json.dumps(res), flush=True)
         return 0
+    if args.c3:
+        wl = bf16_decode("c3_ragged256", c3_context_lengths(), 200_000, layers=4, impl=args.impl,
+                         splits=args.splits)
+        res = measure(wl, args.steps, args.warmup, per_launch=False)
+        log(f"[bench] c3 timed region: decode dispatches {LAST_WARM_CALLS} to {LAST_WARM_CALLS + args.steps - 1}")
+        if args.impl in ("auto", "mfma"):
+            res["paged_read_floor"] = paged_read_floor(wl, args.steps, args.warmup)
+        print(json.dumps({"c3_ragged256": res}), flush=True)
+        return 0
     if args.c5:
         res = {}
         for fmt in ("bf16", "int8", "int8-kchannel"):
@@ -866,6 +886,9 @@ def main() -> int:
     # agrees to about 1%.
     calls = args.steps * args.layers
     ms, _ = time_calls(wl.call, calls, args.warmup * args.layers, per_launch=False)  # ms per call
+    # No decode call precedes the warm-up, so these are the timed calls' places among the process's decode
+    # dispatches (0-based, launch order): a kernel trace can average exactly the timed region.
+    log(f"[bench] c2 timed region: decode dispatches {LAST_WARM_CALLS} to {LAST_WARM_CALLS + calls - 1}")
     kern_us = ms * 1e3
     _, pair_us = time_calls(wl.call, min(args.steps, 200), 0, per_launch=True)
     value = wl.bytes / (ms * 1e-3) / 1e9

@@ -177,12 +177,17 @@ __global__ void __launch_bounds__(256) probe_paged_read_kernel(const ProbeArgs a
     // tiles k0, k0 + 1 are loaded; one more may remain
     fold(r0, a0);
     if (k0 + 2 < mine) load(k0 + 2, r0, a0);
+    order();
     fold(r1, a1);
+    order();
     if (k0 + 2 < mine) fold(r0, a0);
   } else {
+    // Every fold overwrites the same LDS words: without the fence between two folds the compiler drops the first
+    // one's stores as dead, and that tile's loads with them.
     for (int kk = 0; kk < mine; ++kk) {
       load(kk, r0, a0);
       fold(r0, a0);
+      order();
     }
   }
   order();
