@@ -218,9 +218,14 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   const int wcol = wave % CWV, whalf = wave / CWV;  // the wave's column-tile slot and key half
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
 
+  // bf16 pools stage each block's offset in 16-byte units (the host checks that it fits 32 bits), so that a
+  // tile load's address is one shift-add; INT8 pools stage block ids (their scales have strides of their own).
   const int32_t* btr = a.bt + (int64_t)s * a.bt_ss + (k_lo >> 4);
   const int last_col = a.bt_w - 1 - (k_lo >> 4);  // >= nblk - 1 when the host's width check held
-  for (int i = threadIdx.x; i < nblk; i += PT) bids[i] = min(max(btr[min(i, last_col)], 0), a.nb - 1);
+  for (int i = threadIdx.x; i < nblk; i += PT) {
+    const int blk = min(max(btr[min(i, last_col)], 0), a.nb - 1);
+    bids[i] = MODE == 0 ? (int)(uint32_t)((uint64_t)blk * (uint64_t)(a.kv_sn >> 3)) : blk;
+  }
 
   // Column tiles c = wcol + (NC / CW) ci of the unit: query head g = c % G of the group, tokens 16 tt .. 16 tt + 15
   // with tt = c / G (G * TT <= NC). A column tile's B operand holds token r of head g (zero past the unit's
@@ -270,6 +275,8 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   const int nq = MODE == 2 ? ctx / 16 * 16 : 0;
   const int tail = MODE == 2 ? min(a.tails[s], a.n_stage - 1) : -1;
   KvRaw<MODE> raw[NPRE][LPT];
+  const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)h * a.kv_sh;  // MODE 0: the KV head's planes
+  const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)h * a.kv_sh;
   // keys past the half's end (an empty half: past the split's) re-read its last key
   const int rel_lo = half_lo(hx) - k_lo, rel_cap = max(half_end(hx), half_lo(hx) + 1) - 1 - k_lo;
   auto gload = [&](int set, int t) {
@@ -278,14 +285,14 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
     for (int i = 0; i < LPT; ++i) {
       const int c = tx + PTH * i, cg = c % CPK;
       const int rel = min(rel_lo + KT * t + c / CPK, min(rel_cap, kv_end - 1 - k_lo));  // key offset in the split
-      const int64_t blk = bids[rel >> 4];
       const int off = rel & 15;
       KvRaw<MODE>& x = raw[set][i];
       if constexpr (MODE == 0) {
-        const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + 8 * cg;
-        x.k = *(const u32x4*)((const uint16_t*)a.k + e);
-        x.v = *(const u32x4*)((const uint16_t*)a.v + e);
+        const int64_t e = (int64_t)(uint32_t)bids[rel >> 4] * 8 + (off * D + 8 * cg);
+        x.k = *(const u32x4*)(kbase + e);
+        x.v = *(const u32x4*)(vbase + e);
       } else {
+        const int64_t blk = bids[rel >> 4];
         const int64_t e = (int64_t)h * a.kv_sh + blk * a.kv_sn + off * D + CH * cg;
         x.k = *(const u32x4*)((const int8_t*)a.k + e);
         x.v = *(const u32x4*)((const int8_t*)a.v + e);
@@ -402,9 +409,19 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
             if (kp > tok_pos || kp >= h_end) sc[mt][i] = kNegInf;
           }
       }
-      float mx = kNegInf;
+      float mx;
+      if constexpr (MT == 4) {  // 16 scores in 8 three-input maxima
+        auto m3 = [](float x, float y, float z) { return vmax(vmax(x, y), z); };
+        const float a0 = m3(sc[0][0], sc[0][1], sc[0][2]), a1 = m3(sc[0][3], sc[1][0], sc[1][1]);
+        const float a2 = m3(sc[1][2], sc[1][3], sc[2][0]), a3 = m3(sc[2][1], sc[2][2], sc[2][3]);
+        const float a4 = m3(sc[3][0], sc[3][1], sc[3][2]);
+        mx = vmax(m3(a0, a1, sc[3][3]), m3(a2, a3, a4));
+      } else {
+        mx = kNegInf;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) mx = vmax(mx, vmax(vmax(sc[mt][0], sc[mt][1]), vmax(sc[mt][2], sc[mt][3])));
+        for (int mt = 0; mt < MT; ++mt)
+          mx = vmax(mx, vmax(vmax(sc[mt][0], sc[mt][1]), vmax(sc[mt][2], sc[mt][3])));
+      }
       mx = max_over_rows_swap(mx) * a.scale_log2;
       // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
       // below are taken as 0 then, so that -inf - -inf never forms.
@@ -739,6 +756,9 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
              "kv_mode %d", mode);
   SIPA_CHECK(aligned16p(p->k_cache) && aligned16p(p->v_cache) && p->kv_stride_h % 8 == 0 &&
                  p->kv_stride_n % 8 == 0, SIPA_EINVAL, "K/V pools must be 16-byte aligned");
+  SIPA_CHECK(mode != SIPA_KV_PLAIN || (int64_t)(p->num_blocks - 1) * (p->kv_stride_n / 8) <= 0xffffffffLL,
+             SIPA_EUNSUPPORTED, "bf16 pool blocks must lie within 64 GiB of the head's first block (%d blocks of "
+             "stride %lld)", p->num_blocks, (long long)p->kv_stride_n);
   if (mode != SIPA_KV_PLAIN) {
     SIPA_CHECK(p->k_scale && p->v_scale, SIPA_EINVAL, "INT8 pools need k_scale and v_scale");
     SIPA_CHECK((p->k_scale_dtype == SIPA_F16 || p->k_scale_dtype == SIPA_F32) &&
