@@ -68,6 +68,19 @@ def test_single_sequence_lengths(n, impl):
 
 
 @pytest.mark.parametrize("heads", list(HEADS))
+def test_short_splits_each_tile_count(heads):
+    """Splits of 1 to 3 32-token tiles a wave take their own load paths in the MFMA kernel (the tiles' loads in
+    flight together): one sequence per length, so that the waves of its single split hold 1 (96, 100 tokens), 1 or
+    2 (200), 2 or 3 (288, 300) and 3 (352, 383, 384) tiles, partial last tiles included; the same lengths in one
+    batch on 3 splits and on the work list, whose items are that short too."""
+    lengths = [96, 100, 200, 288, 300, 352, 383, 384]
+    for n in lengths:
+        run([n], heads, 16, torch.bfloat16, 1, impl="mfma")
+    run(lengths, heads, 16, torch.bfloat16, 3, impl="mfma")
+    run(lengths, heads, 16, torch.bfloat16, None, impl="mfma", work_list="on")
+
+
+@pytest.mark.parametrize("heads", list(HEADS))
 def test_context_longer_than_one_split_holds(heads):
     """A 40,000-token sequence asked for a single pass: a split stages at most 32,768 tokens of block ids, so the
     library cuts it into two and the output still matches the oracle; on the split grid and the work list."""
