@@ -851,6 +851,9 @@ def main() -> int:
                 continue  # the VALU streaming kernels cover the per-token format only
             wl = int8_decode(key, fmt, [4096] * 64, 32768, impl=args.impl, splits=args.splits)
             res[key] = measure(wl, args.steps, args.warmup, per_launch=False)
+            # each format runs its own kernel, so the indices count that kernel's dispatches
+            log(f"[bench] c4 {key} timed region: decode dispatches {LAST_WARM_CALLS} to "
+                f"{LAST_WARM_CALLS + args.steps - 1}")
             if args.impl in ("auto", "mfma"):
                 res[key]["paged_read_floor"] = paged_read_floor(wl, args.steps, args.warmup)
             del wl
