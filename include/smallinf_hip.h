@@ -84,7 +84,7 @@ typedef struct sipa_decode_params {
   int32_t kv_mode;       /* SIPA_KV_* */
   int32_t impl;          /* SIPA_IMPL_* */
   int32_t combine;       /* SIPA_COMBINE_* */
-  float scale;           /* softmax scale, head_dim^-0.5 in the model */
+  float scale;           /* softmax scale, head_dim^-0.5 in the model; positive and finite (else SIPA_EINVAL) */
   const void* q;         /* [S, Hq, D]; last dim contiguous */
   int64_t q_stride_s, q_stride_h;
   const void* k_cache;   /* [Hkv, N, B, D] */
@@ -216,7 +216,7 @@ typedef struct sipa_prefill_params {
   int32_t num_tokens;    /* T: rows of q and out (rows past T are neither read nor written) */
   int32_t num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context;
   int32_t max_query_len; /* max over s of query_lens[s] (sizes the grid) */
-  float scale;
+  float scale;           /* softmax scale; positive and finite (else SIPA_EINVAL) */
   const void* q;         /* [T, Hq, D] bf16, last dim contiguous */
   int64_t q_stride_t, q_stride_h;
   const void* k_cache;   /* [Hkv, N, B, D] bf16 */

@@ -872,6 +872,8 @@ static int decode_impl(const sipa_decode_params* p, void* stream, bool use_scrat
   const int G = Hq / Hkv;
   SIPA_CHECK(G <= kMaxGroup, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kMaxGroup);
   SIPA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {16,32,64,128}", D);
+  SIPA_CHECK(p->scale > 0.f && p->scale < __builtin_inff(), SIPA_EINVAL,
+             "scale %g must be positive and finite (the kernels take maxima of the unscaled scores)", (double)p->scale);
   SIPA_CHECK(B > 0 && 64 % B == 0, SIPA_EINVAL, "block_size %d must divide 64 (block-aligned 64-token tiles)", B);
   SIPA_CHECK(p->max_context > 0, SIPA_EINVAL, "max_context %d must be >= 1", p->max_context);
   SIPA_CHECK(p->num_blocks > 0, SIPA_EINVAL, "num_blocks %d must be >= 1", p->num_blocks);

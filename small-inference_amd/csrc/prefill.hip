@@ -366,6 +366,12 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   const bf16x8 kOnes = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
                         (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
   constexpr float kRescaleSlack = 8.f;  // p <= 2^8 against the lazily raised max (as in the decode kernel)
+  // p <= 2^16 against a max left as it stands: O stays finite for |v| < 2^94 over 2^17 keys
+  constexpr float kFastRange = 16.f;
+  const float inv_scale_log2 = 1.f / a.scale_log2;
+  float fast_thr[CW];
+#pragma unroll
+  for (int ci = 0; ci < CW; ++ci) fast_thr[ci] = kNegInf;
 
   auto tile = [&](int t) {
     const int buf = t & 1;
@@ -409,29 +415,39 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
             if (kp > tok_pos || kp >= h_end) sc[mt][i] = kNegInf;
           }
       }
-      float mx;
+      // Each lane's largest score (the tile's max needs two cross-lane steps more).
+      float lmax;
       if constexpr (MT == 4) {  // 16 scores in 8 three-input maxima
         auto m3 = [](float x, float y, float z) { return vmax(vmax(x, y), z); };
         const float a0 = m3(sc[0][0], sc[0][1], sc[0][2]), a1 = m3(sc[0][3], sc[1][0], sc[1][1]);
         const float a2 = m3(sc[1][2], sc[1][3], sc[2][0]), a3 = m3(sc[2][1], sc[2][2], sc[2][3]);
         const float a4 = m3(sc[3][0], sc[3][1], sc[3][2]);
-        mx = vmax(m3(a0, a1, sc[3][3]), m3(a2, a3, a4));
+        lmax = vmax(m3(a0, a1, sc[3][3]), m3(a2, a3, a4));
       } else {
-        mx = kNegInf;
+        lmax = kNegInf;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          mx = vmax(mx, vmax(vmax(sc[mt][0], sc[mt][1]), vmax(sc[mt][2], sc[mt][3])));
+          lmax = vmax(lmax, vmax(vmax(sc[mt][0], sc[mt][1]), vmax(sc[mt][2], sc[mt][3])));
       }
-      mx = max_over_rows_swap(mx) * a.scale_log2;
-      // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
-      // below are taken as 0 then, so that -inf - -inf never forms.
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[ci] + kRescaleSlack)) {
-        const float m_new = fmaxf(m_run[ci], mx);
-        const float alpha = fast_exp2(m_run[ci] - (m_new == kNegInf ? 0.f : m_new));  // 0 while m_run is -inf
-        l_run[ci] *= alpha;
+      // The tile's max is taken only when some score exceeds the running max by more than kFastRange (fast_thr,
+      // in raw score units; -inf while a token has no max yet, so a wave's first visible scores always take it):
+      // otherwise every p is at most 2^kFastRange against the running max as it stands, and the exponentials use
+      // it unchanged (the lazily raised max would mostly leave it too). Two cross-lane swaps, a multiply and a
+      // compare per tile fewer: 512 new tokens at 8K context 28.2 -> 27.2 us, four 2048-token prompts 48.1 ->
+      // 46.1, the same over INT8 pools 32.7 -> 31.1.
+      if (__builtin_amdgcn_ballot_w64(lmax > fast_thr[ci])) {
+        const float mx = max_over_rows_swap(lmax) * a.scale_log2;
+        // A token of a later split may see none of the keys so far (m_run = -inf, l = 0, acc = 0): the offsets
+        // below are taken as 0 then, so that -inf - -inf never forms.
+        if (__builtin_amdgcn_ballot_w64(mx > m_run[ci] + kRescaleSlack)) {
+          const float m_new = fmaxf(m_run[ci], mx);
+          const float alpha = fast_exp2(m_run[ci] - (m_new == kNegInf ? 0.f : m_new));  // 0 while m_run is -inf
+          l_run[ci] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[ci][dt] *= alpha;
-        m_run[ci] = m_new;
+          for (int dt = 0; dt < DT; ++dt) acc[ci][dt] *= alpha;
+          m_run[ci] = m_new;
+          fast_thr[ci] = (m_new + kFastRange) * inv_scale_log2;
+        }
       }
       const float m_off = m_run[ci] == kNegInf ? 0.f : m_run[ci];
 #pragma unroll
@@ -737,6 +753,8 @@ extern "C" int32_t sipa_prefill(const sipa_prefill_params* p, void* stream) {
   const int G = Hq / Hkv;
   SIPA_CHECK(G <= kPrefillMaxGroup, SIPA_EUNSUPPORTED, "GQA group %d > %d", G, kPrefillMaxGroup);
   SIPA_CHECK(D == 64 || D == 128, SIPA_EUNSUPPORTED, "head_dim %d not in {64, 128}", D);
+  SIPA_CHECK(p->scale > 0.f && p->scale < __builtin_inff(), SIPA_EINVAL,
+             "scale %g must be positive and finite (the kernel takes maxima of the unscaled scores)", (double)p->scale);
   SIPA_CHECK(p->block_size == 16, SIPA_EUNSUPPORTED, "block_size %d != 16", p->block_size);
   SIPA_CHECK(p->max_context > 0 && p->max_context <= kMaxSplitBlocks * 16, SIPA_EUNSUPPORTED,
              "max_context %d outside [1, %d]", p->max_context, kMaxSplitBlocks * 16);

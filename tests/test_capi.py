@@ -61,6 +61,9 @@ def bad_params(**over):
     ({"max_context": 0}, _hip.EINVAL),
     ({"num_blocks": 0}, _hip.EINVAL),
     ({"q_dtype": _hip.F16}, _hip.EUNSUPPORTED),
+    ({"scale": 0.0}, _hip.EINVAL),                      # the kernels take maxima of the unscaled scores
+    ({"scale": -0.125}, _hip.EINVAL),
+    ({"scale": float("inf")}, _hip.EINVAL),
     ({"kv_mode": 1}, _hip.EINVAL),                      # INT8 without scales
     ({"k_cache": 4100}, _hip.EINVAL),                   # unaligned pool
     ({"out": None}, _hip.EINVAL),
@@ -232,6 +235,8 @@ def prefill_params(**over):
     ({"block_size": 32}, _hip.EUNSUPPORTED),
     ({"max_context": 32784}, _hip.EUNSUPPORTED),
     ({"num_tokens": 0}, _hip.EINVAL),
+    ({"scale": -0.125}, _hip.EINVAL),
+    ({"scale": float("nan")}, _hip.EINVAL),
     ({"query_lens": None}, _hip.EINVAL),
     ({"q": 4100}, _hip.EINVAL),                         # unaligned rows
     ({"out_stride_h": 66}, _hip.EINVAL),
