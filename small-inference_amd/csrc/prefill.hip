@@ -369,9 +369,13 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   // p <= 2^16 against a max left as it stands: O stays finite for |v| < 2^94 over 2^17 keys
   constexpr float kFastRange = 16.f;
   const float inv_scale_log2 = 1.f / a.scale_log2;
-  float fast_thr[CW];
+  float fast_thr[CW], m_off[CW];  // m_off: the exponentials' offset, m_run or 0 while m_run is -inf
 #pragma unroll
-  for (int ci = 0; ci < CW; ++ci) fast_thr[ci] = kNegInf;
+  for (int ci = 0; ci < CW; ++ci) fast_thr[ci] = kNegInf, m_off[ci] = 0.f;
+  // The all-ones operand of the row sums, opaque to the compiler so that it stays in registers instead of being
+  // rematerialized for every tile.
+  bf16x8 ones = kOnes;
+  asm volatile("" : "+v"(ones));
 
   auto tile = [&](int t) {
     const int buf = t & 1;
@@ -406,14 +410,13 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
           sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[mt][jj], qop[ci][jj], sc[mt], 0, 0, 0);
       }
       if (masked) {
-        const int tok_pos = P0 + ctok[ci] + r;
+        // row (mt, q4, i) holds key t0 + 16 mt + 4 q4 + i: hidden past the token's position or the half's end
+        const int lim = min(P0 + ctok[ci] + r, h_end - 1) - t0 - 4 * q4;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = t0 + 16 * mt + 4 * q4 + i;  // key position of accumulator row (mt, q4, i)
-            if (kp > tok_pos || kp >= h_end) sc[mt][i] = kNegInf;
-          }
+          for (int i = 0; i < 4; ++i)
+            if (16 * mt + i > lim) sc[mt][i] = kNegInf;
       }
       // Each lane's largest score (the tile's max needs two cross-lane steps more).
       float lmax;
@@ -446,20 +449,20 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) acc[ci][dt] *= alpha;
           m_run[ci] = m_new;
+          m_off[ci] = m_new == kNegInf ? 0.f : m_new;
           fast_thr[ci] = (m_new + kFastRange) * inv_scale_log2;
         }
       }
-      const float m_off = m_run[ci] == kNegInf ? 0.f : m_run[ci];
 #pragma unroll
       for (int hf = 0; hf < HT; ++hf)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          pop[ci][hf][i] = (__bf16)fast_exp2(fmaf(sc[2 * hf + (i >> 2)][i & 3], a.scale_log2, -m_off));
+          pop[ci][hf][i] = (__bf16)fast_exp2(fmaf(sc[2 * hf + (i >> 2)][i & 3], a.scale_log2, -m_off[ci]));
       // The denominators on the matrix cores: ones . P^T sums each token's bf16 probabilities (the values the
       // P.V product uses) into every row of l_run, in place of VALU adds and a cross-row reduction.
 #pragma unroll
       for (int hf = 0; hf < HT; ++hf)
-        l_run[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[ci][hf], l_run[ci], 0, 0, 0);
+        l_run[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pop[ci][hf], l_run[ci], 0, 0, 0);
     }
     // V^T operands (32 keys each), each shared by both column tiles.
 #pragma unroll
@@ -477,21 +480,39 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   // in buffer t & 1). The set of tile t is free once tile t is in LDS, and is refilled with tile t + NPRE. The
   // loads are issued unconditionally (past the last tile they re-read the split's last key), so that the wait
   // before each LDS store is a fixed count that leaves the NPRE - 1 younger sets in flight.
+  // in ring order (the compiler would otherwise issue set 0's V after set 1, and the first store would wait for
+  // both sets)
 #pragma unroll
-  for (int k = 0; k < NPRE; ++k) gload(k, k);
+  for (int k = 0; k < NPRE; ++k) {
+    gload(k, k);
+    asm volatile("" ::: "memory");
+  }
   sstore(0, 0);
   __syncthreads();
-  for (int tb = 0; tb < ntiles; tb += NPRE) {
+  // Whole passes of NPRE tiles, then the last ntiles % NPRE tiles outside the loop: an exit from the middle of a
+  // pass would reach the loop head (in the compiler's control flow) with a register set's loads outstanding, and
+  // every pass would then wait for its next tile's loads before issuing the ones after it.
+  int tb = 0;
+  for (; tb + NPRE <= ntiles; tb += NPRE) {
 #pragma unroll
     for (int k = 0; k < NPRE; ++k) {
       const int t = tb + k;
-      if (t >= ntiles) break;
       gload(k, t + NPRE);
       if (KH == 1 || t < my_tiles) tile(t);  // wave-uniform
-      // buffer (t + 1) & 1 was last read in tile t - 1, before the last barrier
-      if (t + 1 < ntiles) sstore((k + 1) % NPRE, (t + 1) & 1);
+      // buffer (t + 1) & 1 was last read in tile t - 1, before the last barrier (after the last tile: the
+      // re-read last key, never used)
+      sstore((k + 1) % NPRE, (t + 1) & 1);
       __syncthreads();
     }
+  }
+  // their loads, and the first one's LDS store, were issued in the loop
+#pragma unroll
+  for (int k = 0; k < NPRE - 1; ++k) {
+    const int t = tb + k;
+    if (t >= ntiles) break;
+    if (KH == 1 || t < my_tiles) tile(t);
+    if (t + 1 < ntiles) sstore((k + 1) % NPRE, (t + 1) & 1);
+    __syncthreads();
   }
 
   float lsum[CW];  // token r's denominators (every row of the l_run accumulator holds the same sum)
