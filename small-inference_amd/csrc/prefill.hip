@@ -56,9 +56,9 @@ struct PrefillArgs {
   float scale_log2;
   bool mem_merge;          // merge every unit through memory (SIPA_MERGE_MEMORY)
   int* counters;           // [units] split arrivals, zero between launches
-  float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
-  float* pl;               // same shape: softmax denominators
-  float* part;             // [units][nsplit][8 columns][16 tokens][D] each split's output O / l, as fp16
+  float* pm;               // [units][nsplit][8 columns][16 tokens] log2 of the split's weight, m + log2 l (exp2 domain)
+  float* pl;               // same shape: e of the stored row (int32 bits): O / l 2^-e, e = 0 unless it reaches 2^15
+  float* part;             // [units][nsplit][8 columns][16 tokens][D] each split's output O / l 2^-e, as fp16
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -547,9 +547,12 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   // the column tiles' state is half 0's now: half 1's waves only take part in the barriers and the merge
   const bool owner = KH == 1 || whalf == 0;
   if (nvalid > 1) {
-    // This split's state for column c, token r: m, l at slot 16 c + r, and the split's own output O / l (the
-    // weighted mean of its V rows, so fp16 holds it to 2^-11 relative) at channels 16 dt + 4 q4 .. of that row:
-    // half the bytes of unnormalised fp32 partials, which the merge reads back in one or two memory round trips.
+    // This split's state for column c, token r, at slot 16 c + r: its weight in the merge as one exp2-domain
+    // value, m + log2 l, and its own output O / l (the weighted mean of its V rows, so fp16 holds it to 2^-11
+    // relative) at channels 16 dt + 4 q4 .. of that row: half the bytes of unnormalised fp32 partials, which the
+    // merge reads back in one or two memory round trips. A row whose largest |O / l| reaches 2^15 (V values
+    // beyond fp16's range) is stored times 2^-e, so that it stays below 65504, and e goes to the slot's second
+    // word; the merge scales the row back exactly.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kSlots;
     const int split_bytes = kSlots * D * 2;
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
@@ -559,17 +562,28 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
       if (!owner || !cvalid[ci] || ctok[ci] + r >= ntok) continue;
       const int slot = 16 * (wcol + CWV * ci) + r;
       const float inv = lsum[ci] > 0.f ? 1.f / lsum[ci] : 0.f;  // l = 0: the token sees no key of this split
+      // the row's largest |O / l|: this lane's 4 DT channels, then the row's other three lanes (q4)
+      float big = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        big = vmax(big, vmax(vmax(fabsf(acc[ci][dt][0]), fabsf(acc[ci][dt][1])),
+                             vmax(fabsf(acc[ci][dt][2]), fabsf(acc[ci][dt][3]))));
+      big = max_over_rows_swap(big * inv);
+      // big < 2^ex; e = ex - 15 keeps the row under 2^15 (inf and NaN rows keep e = 0 and stay inf and NaN)
+      const int e = big < 32768.f ? 0 : max(__builtin_amdgcn_frexp_expf(big) - 15, 0);
+      const float inv_e = __builtin_amdgcn_ldexpf(inv, -e);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const f32x4 o = acc[ci][dt] * inv;
+        const f32x4 o = acc[ci][dt] * inv_e;
         const u32x2 h = {f32_to_f16_bits(o[0]) | ((uint32_t)f32_to_f16_bits(o[1]) << 16),
                          f32_to_f16_bits(o[2]) | ((uint32_t)f32_to_f16_bits(o[3]) << 16)};
         __builtin_amdgcn_raw_buffer_store_b64(h, rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 2, 0,
                                               kAuxSc1);
       }
       if (q4 == 0) {
-        store_coherent(a.pm + base + slot, m_run[ci]);
-        store_coherent(a.pl + base + slot, lsum[ci]);
+        // l = 0 only where m = -inf (a token that sees no key of this split): -inf, weight 0
+        store_coherent(a.pm + base + slot, m_run[ci] + __builtin_amdgcn_logf(lsum[ci]));
+        store_coherent(a.pl + base + slot, __int_as_float(e));
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -610,15 +624,16 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
 #pragma unroll
           for (int qd = 0; qd < CB / 4; ++qd) num[qd] = f32x4{0.f, 0.f, 0.f, 0.f};
           for (int j0 = 0; j0 < nvalid; j0 += KB) {
-            float mj[KB], lj[KB];
+            float mj[KB];  // the splits' weights, log2
+            int ej[KB];    // their rows were stored times 2^-e
             u32x2 oj[KB][CB / 4];
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu) {
               const int j = min(j0 + uu, nvalid - 1);  // entries past nvalid re-read the last split, weight 0
               mj[uu] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                      mrows, (j * kSlots + slot) * 4, 0, AUX));
-              lj[uu] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                     lrows, (j * kSlots + slot) * 4, 0, AUX));
+              ej[uu] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   lrows, (j * kSlots + slot) * 4, 0, AUX));
 #pragma unroll
               for (int qd = 0; qd < CB / 4; ++qd)
                 oj[uu][qd] = __builtin_amdgcn_raw_buffer_load_b64(
@@ -636,14 +651,15 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
             for (int qd = 0; qd < CB / 4; ++qd) num[qd] *= rescale;
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu) {
-              const float w = fast_exp2(mj[uu] - mb) * lj[uu];  // 0 for padding entries and keyless splits
+              const float w = fast_exp2(mj[uu] - mb);  // 0 for padding entries and keyless splits
               den += w;
+              const float wo = __builtin_amdgcn_ldexpf(w, ej[uu]);
 #pragma unroll
               for (int qd = 0; qd < CB / 4; ++qd) {
                 const u32x2 hw = oj[uu][qd];
                 const f32x4 o = {f16_bits_to_f32(hw[0] & 0xffffu), f16_bits_to_f32(hw[0] >> 16),
                                  f16_bits_to_f32(hw[1] & 0xffffu), f16_bits_to_f32(hw[1] >> 16)};
-                num[qd] += w * o;
+                num[qd] += wo * o;
               }
             }
             M = mb;

@@ -339,6 +339,28 @@ def test_merge_paths_agree(shape, splits):
 
 @pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
 @pytest.mark.parametrize("layout", ["auto", "w16h2"])
+def test_split_partials_beyond_fp16_range(shape, layout):
+    """V at 2^24 times unit scale, so that every split's O / l rows (weighted means of V rows, about 0.05 to 3 at
+    unit scale) pass fp16's 65504: the fp16 partial rows are stored times 2^-e and merged back, and the output
+    divided by 2^24 (exact in bf16) meets the oracle's bound at unit scale, with every value finite (unscaled
+    fp16 partials would be inf)."""
+    Hq, Hkv, D = SHAPES[shape]
+    ctx, qlen = [3000, 700], [700, 300]
+    print(f"case prefill partials beyond fp16 range {shape} {layout}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=61)
+    scale = D ** -0.5
+    out = paged_prefill_attention(q, k, v * 2.0 ** 24, bt, c, st, ln, scale, max(ctx), max(qlen), num_splits=6,
+                                  wg_layout=layout)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    ref32 = paged_ref.prefill(as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale,
+                              dtype=np.float32)
+    rows = np.concatenate([np.arange(s0, s0 + n) for s0, n in zip(starts, qlen)])
+    assert_bf16_close(out.double().cpu().numpy()[rows] / 2.0 ** 24, ref32[rows], "V x 2^24, divided back")
+
+
+@pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
+@pytest.mark.parametrize("layout", ["auto", "w16h2"])
 def test_l2_merge_reads_this_calls_partials(shape, layout):
     """The prefill merge from the XCD's L2: calls alternating between two inputs of one shape (the same workspace
     addresses) each give the memory-path bits of their own inputs, so no partial of an earlier call is read
