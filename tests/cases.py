@@ -44,6 +44,26 @@ def make_case(lengths, Hq, Hkv, D, B, dtype, seed=0, device="cuda", spare=2):
     return q, k, v, bt, ctx, tables
 
 
+def ramp_scores(q, k, tables, lengths, B, direction, q0=64.0, span=8.0):
+    """Scores that trend across the keys: channel 0 of every key goes linearly from -span to +span over its
+    sequence's positions (reversed for direction -1) and channel 0 of every query is q0, so that with head_dim 64
+    (scale 1/8) a score moves by about 4 in the exp2 domain every 64 keys. Direction 0: a spike instead, channel
+    0 zero but for the key at two thirds of each sequence, which gets +span (about 90 above the other scores in
+    the exp2 domain). q and k are modified in place."""
+    q[..., 0] = q0
+    kk = k.float()
+    for s, n in enumerate(lengths):
+        pos = torch.arange(n)
+        blk = torch.tensor(tables[s][:-(-n // B)])[pos // B]
+        if direction == 0:
+            x = torch.zeros(n)
+            x[2 * n // 3] = span
+        else:
+            x = direction * (2.0 * span * pos / max(n - 1, 1) - span)
+        kk[:, blk, pos % B, 0] = x.to(kk)
+    k.copy_(kk.to(k.dtype))
+
+
 def as_np32(t: torch.Tensor) -> np.ndarray:
     """A tensor's values as a float32 numpy array on the CPU (bf16 widens exactly)."""
     return t.detach().float().cpu().numpy()

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import HEADS, RAGGED, assert_decode_close, make_case, oracle_decode
+from cases import HEADS, RAGGED, assert_decode_close, make_case, oracle_decode, ramp_scores
 from engine.hip_decode import choose_splits, paged_decode_attention, split_plan
 
 pytestmark = pytest.mark.gpu
@@ -355,3 +355,22 @@ def test_l2_merge_reads_this_calls_partials(heads):
             assert_decode_close(out.double().cpu().numpy(), refs[i], f"l2 merge rep {rep} batch {i}")
         q, k, v, bt, ctx, _ = odd
         paged_decode_attention(q, k, v, bt, ctx, D ** -0.5, max(lengths[:3]), num_splits=4)
+
+
+@pytest.mark.parametrize("direction", [1, -1, 0], ids=["rising", "falling", "spike"])
+@pytest.mark.parametrize("splits", [1, 3, None], ids=["single", "split3", "auto"])
+def test_scores_trending_across_keys(direction, splits):
+    """Scores rising (or falling) by about 4 in the exp2 domain every 64 keys, or one key's score about 90 above
+    the rest: rising, the running max is passed by more than the lazy-rescale slack every few tiles and acc and l
+    are rescaled there; falling, the later probabilities underflow against the first tiles' max; the spike
+    rescales once. The bf16 MFMA kernel against the fp32 oracle."""
+    lengths = [3000, 700, 129, 17]
+    Hq, Hkv, D = HEADS["0.5B"]
+    q, k, v, bt, ctx, tables = make_case(lengths, Hq, Hkv, D, 16, torch.bfloat16, seed=71)
+    ramp_scores(q, k, tables, lengths, 16, direction)
+    print(f"case trending scores direction={direction} splits={splits}", flush=True)
+    out = paged_decode_attention(q, k, v, bt, ctx, D ** -0.5, max(lengths), num_splits=splits, impl="mfma",
+                                 host_context_lens=lengths)
+    torch.cuda.synchronize()
+    ref32 = oracle_decode(q, k, v, tables, lengths, D ** -0.5, np.float32)
+    assert_decode_close(out.double().cpu().numpy(), ref32, "trending scores")

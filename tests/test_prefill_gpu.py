@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import as_np32, fragmented_manager
+from cases import as_np32, fragmented_manager, ramp_scores
 from engine.hip_prefill import paged_prefill_attention
 from oracle import paged_ref
 
@@ -335,6 +335,30 @@ def test_merge_paths_agree(shape, splits):
     assert_bf16_close(mem.double().cpu().numpy()[rows], ref32[rows], "merge through memory")
     with pytest.raises(ValueError):
         run("l2")
+
+
+@pytest.mark.parametrize("direction", [1, -1, 0], ids=["rising", "falling", "spike"])
+@pytest.mark.parametrize("splits", [1, 6])
+@pytest.mark.parametrize("layout", ["auto", "w16h2", "w16x1"])
+def test_scores_trending_across_keys(direction, splits, layout):
+    """Scores rising (or falling) by about 4 in the exp2 domain every 64 keys, or one key's score about 90 above
+    the rest. Rising, some score passes the running max by more than 2^16 every few tiles, so the kernel takes
+    those tiles' max and rescales, and uses the standing max for the tiles between; falling, the later
+    probabilities underflow against the first tile's max; the spike's tile (whose p would overflow against the
+    standing max) takes the max. The output meets the oracle's bound on every row."""
+    Hq, Hkv, D = SHAPES["0.5B"]
+    ctx, qlen = [3000, 700], [700, 300]
+    print(f"case prefill trending scores direction={direction} splits={splits} layout={layout}", flush=True)
+    q, k, v, bt, c, st, ln, tables, starts, T = make_prefill(ctx, qlen, Hq, Hkv, D, seed=71)
+    ramp_scores(q, k, tables, ctx, 16, direction)
+    scale = D ** -0.5
+    out = paged_prefill_attention(q, k, v, bt, c, st, ln, scale, max(ctx), max(qlen), num_splits=splits,
+                                  wg_layout=layout)
+    torch.cuda.synchronize()
+    ref32 = paged_ref.prefill(as_np32(q), as_np32(k), as_np32(v), tables, ctx, starts, qlen, scale,
+                              dtype=np.float32)
+    rows = np.concatenate([np.arange(s0, s0 + n) for s0, n in zip(starts, qlen)])
+    assert_bf16_close(out.double().cpu().numpy()[rows], ref32[rows], "trending scores")
 
 
 @pytest.mark.parametrize("shape", ["0.5B", "1.5B"])
