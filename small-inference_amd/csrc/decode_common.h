@@ -180,8 +180,8 @@ __device__ __forceinline__ void store_out4(const DecodeArgs& a, int s, int hq, i
   if (!OUT_F32) {
     uint16_t* o = (uint16_t*)a.out + i;
     if (((uintptr_t)o & 3) == 0) {
-      const uint32_t w0 = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-      const uint32_t w1 = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+      const uint32_t w0 = pack_bf16x2(v[0], v[1]);
+      const uint32_t w1 = pack_bf16x2(v[2], v[3]);
       __hip_atomic_store((uint32_t*)o, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store((uint32_t*)o + 1, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;

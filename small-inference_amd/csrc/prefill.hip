@@ -149,7 +149,7 @@ __device__ __forceinline__ u32x4 dequant8(u32x2 codes, Scale scale) {
     const uint32_t w = codes[j >> 2];
     const float a0 = (float)(int8_t)(w >> (8 * (j & 3))) * scale(j);
     const float a1 = (float)(int8_t)(w >> (8 * ((j + 1) & 3))) * scale(j + 1);
-    out[j >> 1] = f32_to_bf16_bits(a0) | ((uint32_t)f32_to_bf16_bits(a1) << 16);
+    out[j >> 1] = pack_bf16x2(a0, a1);
   }
   return out;
 }
@@ -575,8 +575,7 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4 o = acc[ci][dt] * inv_e;
-        const u32x2 h = {f32_to_f16_bits(o[0]) | ((uint32_t)f32_to_f16_bits(o[1]) << 16),
-                         f32_to_f16_bits(o[2]) | ((uint32_t)f32_to_f16_bits(o[3]) << 16)};
+        const u32x2 h = {pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
         __builtin_amdgcn_raw_buffer_store_b64(h, rows, sp * split_bytes + (slot * D + 16 * dt + 4 * q4) * 2, 0,
                                               kAuxSc1);
       }
@@ -669,10 +668,8 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
           for (int qd = 0; qd < CB / 4; qd += 2) {
             const f32x4 x = num[qd] * inv, y = num[qd + 1] * inv;
             *(u32x4*)(orow + c0 + 4 * qd) =
-                u32x4{f32_to_bf16_bits(x[0]) | ((uint32_t)f32_to_bf16_bits(x[1]) << 16),
-                      f32_to_bf16_bits(x[2]) | ((uint32_t)f32_to_bf16_bits(x[3]) << 16),
-                      f32_to_bf16_bits(y[0]) | ((uint32_t)f32_to_bf16_bits(y[1]) << 16),
-                      f32_to_bf16_bits(y[2]) | ((uint32_t)f32_to_bf16_bits(y[3]) << 16)};
+                u32x4{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(y[0], y[1]),
+                      pack_bf16x2(y[2], y[3])};
           }
         }
       }
@@ -695,10 +692,8 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
     uint16_t* orow = (uint16_t*)a.out + (int64_t)(row0 + ctok[ci] + r) * a.o_st + (int64_t)(h * G + cg[ci]) * a.o_sh;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t lo = f32_to_bf16_bits(acc[ci][dt][0] * inv) |
-                          ((uint32_t)f32_to_bf16_bits(acc[ci][dt][1] * inv) << 16);
-      const uint32_t hi2 = f32_to_bf16_bits(acc[ci][dt][2] * inv) |
-                           ((uint32_t)f32_to_bf16_bits(acc[ci][dt][3] * inv) << 16);
+      const uint32_t lo = pack_bf16x2(acc[ci][dt][0] * inv, acc[ci][dt][1] * inv);
+      const uint32_t hi2 = pack_bf16x2(acc[ci][dt][2] * inv, acc[ci][dt][3] * inv);
       *(u32x2*)(orow + 16 * dt + 4 * q4) = u32x2{lo, hi2};
     }
   }

@@ -38,6 +38,20 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even (v_cvt_pk_bf16_f32)
 }
 
+// Two values rounded to nearest even and packed (lo in bits 0-15), as one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: two
+// scalar conversions shifted and or-ed together cost four instructions a pair.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t u16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)u16);
 }
