@@ -56,8 +56,8 @@ struct PrefillArgs {
   float scale_log2;
   bool mem_merge;          // merge every unit through memory (SIPA_MERGE_MEMORY)
   int* counters;           // [units] split arrivals, zero between launches
-  float* pm;               // [units][nsplit][8 columns][16 tokens] log2 of the split's weight, m + log2 l (exp2 domain)
-  float* pl;               // same shape: e of the stored row (int32 bits): O / l 2^-e, e = 0 unless it reaches 2^15
+  float* pm;               // [units][nsplit][8 columns][16 tokens] running max (exp2 domain)
+  float* pl;               // same shape: softmax denominators, the row's exponent e in the low 8 mantissa bits
   float* part;             // [units][nsplit][8 columns][16 tokens][D] each split's output O / l 2^-e, as fp16
 };
 
@@ -547,12 +547,11 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
   // the column tiles' state is half 0's now: half 1's waves only take part in the barriers and the merge
   const bool owner = KH == 1 || whalf == 0;
   if (nvalid > 1) {
-    // This split's state for column c, token r, at slot 16 c + r: its weight in the merge as one exp2-domain
-    // value, m + log2 l, and its own output O / l (the weighted mean of its V rows, so fp16 holds it to 2^-11
-    // relative) at channels 16 dt + 4 q4 .. of that row: half the bytes of unnormalised fp32 partials, which the
-    // merge reads back in one or two memory round trips. A row whose largest |O / l| reaches 2^15 (V values
-    // beyond fp16's range) is stored times 2^-e, so that it stays below 65504, and e goes to the slot's second
-    // word; the merge scales the row back exactly.
+    // This split's state for column c, token r: m, l at slot 16 c + r, and the split's own output O / l (the
+    // weighted mean of its V rows, so fp16 holds it to 2^-11 relative) at channels 16 dt + 4 q4 .. of that row:
+    // half the bytes of unnormalised fp32 partials, which the merge reads back in one or two memory round trips.
+    // A row whose largest |O / l| reaches 2^15 (V values beyond fp16's range) is stored times 2^-e, so that it
+    // stays below 65504, with e in l's low mantissa bits; the merge scales the row back exactly.
     const int64_t base = ((int64_t)u * a.nsplit + sp) * kSlots;
     const int split_bytes = kSlots * D * 2;
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
@@ -580,9 +579,9 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
                                               kAuxSc1);
       }
       if (q4 == 0) {
-        // l = 0 only where m = -inf (a token that sees no key of this split): -inf, weight 0
-        store_coherent(a.pm + base + slot, m_run[ci] + __builtin_amdgcn_logf(lsum[ci]));
-        store_coherent(a.pl + base + slot, __int_as_float(e));
+        // e (at most 113) in the low 8 bits of l's mantissa: l changes by less than 2^-15 relative
+        store_coherent(a.pm + base + slot, m_run[ci]);
+        store_coherent(a.pl + base + slot, __uint_as_float((__float_as_uint(lsum[ci]) & ~0xffu) | (uint32_t)e));
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -623,16 +622,17 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
 #pragma unroll
           for (int qd = 0; qd < CB / 4; ++qd) num[qd] = f32x4{0.f, 0.f, 0.f, 0.f};
           for (int j0 = 0; j0 < nvalid; j0 += KB) {
-            float mj[KB];  // the splits' weights, log2
-            int ej[KB];    // their rows were stored times 2^-e
+            float mj[KB], lj[KB];
+            int ej[KB];  // their rows were stored times 2^-e
             u32x2 oj[KB][CB / 4];
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu) {
               const int j = min(j0 + uu, nvalid - 1);  // entries past nvalid re-read the last split, weight 0
               mj[uu] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                      mrows, (j * kSlots + slot) * 4, 0, AUX));
-              ej[uu] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(
-                                                   lrows, (j * kSlots + slot) * 4, 0, AUX));
+              const uint32_t lb = __builtin_amdgcn_raw_buffer_load_b32(lrows, (j * kSlots + slot) * 4, 0, AUX);
+              lj[uu] = __uint_as_float(lb & ~0xffu);
+              ej[uu] = (int)(lb & 0xffu);
 #pragma unroll
               for (int qd = 0; qd < CB / 4; ++qd)
                 oj[uu][qd] = __builtin_amdgcn_raw_buffer_load_b64(
@@ -650,7 +650,7 @@ __global__ void __launch_bounds__(64 * NC / CW * KH) prefill_mfma_bf16(const Pre
             for (int qd = 0; qd < CB / 4; ++qd) num[qd] *= rescale;
 #pragma unroll
             for (int uu = 0; uu < KB; ++uu) {
-              const float w = fast_exp2(mj[uu] - mb);  // 0 for padding entries and keyless splits
+              const float w = fast_exp2(mj[uu] - mb) * lj[uu];  // 0 for padding entries and keyless splits
               den += w;
               const float wo = __builtin_amdgcn_ldexpf(w, ej[uu]);
 #pragma unroll

@@ -260,8 +260,8 @@ def test_prefill_layout_and_empty_calls():
 
 def test_prefill_split_policy_and_workspace():
     """About two workgroups per CU over (KV head, 16-token query tile) units, no split under 256 keys, at most
-    32; the workspace holds two fp32 words (the split's weight m + log2 l, the row's exponent) and O / l fp16
-    for 8 heads x 16 tokens per unit and split, and nothing for one split."""
+    32; the workspace holds (m, l) fp32 (the row's exponent in l's low mantissa bits) and O / l fp16 for 8 heads
+    x 16 tokens per unit and split, and nothing for one split."""
     lib = _hip.lib()
     assert lib.sipa_prefill_splits(12, 2, 128, 32, 8192, 256) == 8    # 1.5B, 512-token chunk at 8K: 64 units
     assert lib.sipa_prefill_splits(14, 2, 64, 32, 8192, 256) == 8     # 0.5B likewise
