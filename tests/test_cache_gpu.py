@@ -4,17 +4,17 @@ decode rows and prefill chunks, as engine/model.py:145-146 drives it (reference 
 
 Checked against the oracle: each row's softmax attention over the cache contents gathered back to fp32 (for the
 INT8 caches, the dequantized contents), causal within a chunk. Tolerances: fp32 caches 1e-5; bf16 decode rows
-(the HIP decode kernel) 8e-3 max-abs; bf16 prefill rows of the model-dtype cache (the HIP prefill kernel) 8e-3
-max-abs where |out| < 2 and 2^-7 |out| above, whose bf16 rounding alone reaches 2^-8 |out|; bf16 prefill rows of
-the INT8 caches 3e-2 against the oracle's fp32 dequantization, since the prefill kernel dequantizes K/V to bf16
-as the reference's gather path does (engine/quant_cache.py:179-190).
+(the HIP decode kernel) 8e-3 max-abs; bf16 prefill rows of the model-dtype cache (the HIP prefill kernel) within
+8e-3 or a bf16 rounding of the oracle (`cases.assert_decode_close`); bf16 prefill rows of the INT8 caches 3e-2
+against the oracle's fp32 dequantization, since the prefill kernel dequantizes K/V to bf16 as the reference's
+gather path does (engine/quant_cache.py:179-190).
 """
 
 import numpy as np
 import pytest
 import torch
 
-from cases import fragmented_manager
+from cases import assert_decode_close, fragmented_manager
 from engine.config import ModelConfig
 from engine.paged_cache import PagedKVCache, build_metadata
 from engine.quant_cache import QuantPagedKVCache
@@ -78,10 +78,7 @@ def check_rows(cache, meta, q, out, layer, dtype, what):
     if isinstance(cache, QuantPagedKVCache):  # K/V dequantized to the model dtype, as gather() does
         assert err[~dec].max() <= 3e-2, f"{what}: chunk rows {err[~dec].max():.3e}"
         return
-    big = np.abs(ref[~dec]) >= 2
-    e = err[~dec]
-    assert e[~big].max(initial=0.0) <= 8e-3, f"{what}: chunk rows {e[~big].max(initial=0.0):.3e}"
-    assert (e[big] / np.abs(ref[~dec][big])).max(initial=0.0) <= 2 ** -7, f"{what}: chunk rows, |out| >= 2"
+    assert_decode_close(got[~dec], ref[~dec], f"{what}: chunk rows")
 
 
 def run_mixed(make_cache, dtype, D, seed):
