@@ -414,8 +414,8 @@ def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False, v_mag=1.0):
 @pytest.mark.parametrize("splits", [1, 3, None, "list"], ids=["single", "split3", "auto", "worklist"])
 def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     """Both INT8 kernels against the oracle's fp32 dequantize-then-attend, outlier K channels (4 per head scaled
-    by U[20, 68], as config C4), ragged lengths with partial last blocks: max-abs 8e-3 where |ref| < 2, relative
-    2^-7 above; the fp32-output VALU kernel at 8e-3 everywhere."""
+    by U[20, 68], as config C4), ragged lengths with partial last blocks: every element within 8e-3 of the oracle or
+    a bf16 rounding of it; the fp32-output VALU kernel within 8e-3 everywhere."""
     Hq, Hkv, D = HEADS[heads]
     lengths = [1, 15, 16, 17, 33, 100, 700, 2100]
     q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=5)
@@ -428,8 +428,8 @@ def test_int8_kernels_match_oracle(fmt, heads, impl, splits):
     got = out.double().cpu().numpy()
     ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
                     for s in range(len(lengths))])
-    # 8e-3 max-abs where |ref| < 2; above that (outlier channels make the softmax peaked and
-    # |out| reach a few units) relative 2^-7, since half a bf16 unit of the output alone is 2^-8 |out| there.
+    # 8e-3 max-abs, or one of the two bf16 values bracketing the oracle's (outlier channels make
+    # the softmax peaked and |out| reach a few units, where half a bf16 unit of the output approaches 8e-3).
     assert_decode_close(got, ref, f"int8 {fmt} {heads} {impl} splits={splits}")
     if impl == "valu":  # the same case with an fp32 query and output: the fp32 math itself, no rounding allowance
         out32 = paged_decode_attention(q.float(), cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t,
