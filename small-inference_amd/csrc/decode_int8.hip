@@ -369,12 +369,14 @@ __global__ void __launch_bounds__(kThreads, 2) decode_mfma_int8(const DecodeArgs
         } else {
           // Q' = q * s with the block's fp16 channel scales s, as an exact high part plus a low part: s_hi keeps
           // the top 3 significant bits of s (sign, exponent, 2 mantissa bits), so q * s_hi (8 x 3 bits) is exact
-          // in fp16; s_lo = s - s_hi is exact and q * s_lo is rounded relative to that small remainder only.
+          // in fp16; the low part q * s - q_hi, one fused multiply-add (packed fp16), is q * (s - s_hi) rounded
+          // once, relative to that small remainder only. (Written as q * (s - s_hi), the subtraction compiled to
+          // unpacked fp16 subtracts and repacks: three instructions a pair.)
           const u32x4 cw = *(const u32x4*)(kcw + 64 * mt + kchan(j) / 2);
           const f16x8 s_all = __builtin_bit_cast(f16x8, cw);
           const f16x8 s_hi = __builtin_bit_cast(f16x8, cw & 0xff00ff00u);
           const f16x8 q_hi = qh[j] * s_hi;
-          const f16x8 q_lo = qh[j] * (s_all - s_hi);
+          const f16x8 q_lo = __builtin_elementwise_fma(qh[j], s_all, -q_hi);
           sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, q_hi, sc[mt], 0, 0, 0);
           sc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, q_lo, sc[mt], 0, 0, 0);
         }
