@@ -355,7 +355,7 @@ def test_kernel_matches_dequantized_reference(dtype, fmt, heads, B, splits):
 
 # ---- INT8 decode kernels, forced: MFMA and VALU, both formats, and constant channel scales ------------------------
 
-def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False, v_mag=1.0):
+def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False, v_mag=1.0, k_mag=1.0):
     """INT8 pools built by the HIP quantizers (through the cache), outlier channels in K, and the oracle's fp32
     dequantized K/V per sequence. Returns (q, cache, meta, k32 list, v32 list). The closing step re-writes every
     sequence's last token, so format B stages one block per sequence: twice as many staging slots as sequences
@@ -370,7 +370,7 @@ def int8_case(Hq, Hkv, D, lengths, fmt, seed, const_channels=False, v_mag=1.0):
     for s in range(len(lengths)):
         m.allocate(s, 0)
     for s, n in enumerate(lengths):
-        k = (torch.randn(n, Hkv, D, generator=g) * outlier).to("cuda", torch.bfloat16)
+        k = (torch.randn(n, Hkv, D, generator=g) * outlier * k_mag).to("cuda", torch.bfloat16)
         v = (torch.randn(n, Hkv, D, generator=g) * v_mag).to("cuda", torch.bfloat16)
         write_chunks(m, cache, s, k, v, [n] if n < 50 else [37, n - 37])
     meta = build_metadata(m, [(s, n - 1, 1) for s, n in enumerate(lengths)], "cuda")
@@ -569,6 +569,29 @@ def test_int8_mfma_small_v_scales(v_mag, fmt, heads):
         got = out.double().cpu().numpy()
         assert np.isfinite(got).all()
         assert_decode_close(got / v_mag, ref / v_mag, f"int8 V x {v_mag:g} {fmt} {heads} splits={splits}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("heads", list(HEADS))
+def test_int8_mfma_small_k_scales(fmt, heads):
+    """K of magnitude 2^-12 with the query 2^12 larger (the same scores): format B's channel scales of the
+    ordinary channels are then fp16 subnormals (about 8e-6) and the per-token format's token scales small, so the
+    query's fp16 product with the scale (format B: an exact high part and a low part from one fused multiply-add)
+    runs where its high part may itself be inexact. The output meets the unit-scale bound against the oracle's
+    fp32 dequantize-then-attend of the same cache and query."""
+    Hq, Hkv, D = HEADS[heads]
+    lengths = [1, 17, 300, 1000, 3000]
+    q, cache, meta, quant, k32, v32 = int8_case(Hq, Hkv, D, lengths, fmt, seed=23, k_mag=2.0 ** -12)
+    q = (q.float() * 2.0 ** 12).bfloat16()  # exact: a power of two
+    ref = np.stack([paged_ref.attend_one(as_np32(q[s]), k32[s], v32[s], D ** -0.5, np.float32)
+                    for s in range(len(lengths))])
+    for splits in (1, None):
+        print(f"case int8 small K {fmt} {heads} splits={splits}", flush=True)
+        out = paged_decode_attention(q, cache.k[0], cache.v[0], meta.block_tables, meta.context_lens_t, D ** -0.5,
+                                     max(lengths), num_splits=splits, quant=quant, impl="mfma")
+        got = out.double().cpu().numpy()
+        assert np.isfinite(got).all()
+        assert_decode_close(got, ref, f"int8 K x 2^-12 {fmt} {heads} splits={splits}")
 
 
 @pytest.mark.parametrize("fmt", FMTS)
